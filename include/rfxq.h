@@ -1,0 +1,177 @@
+/*
+ * rfxq -- MI355X (gfx950) GGUF quantized-matmul library: the C ABI.
+ *
+ * Drop-in for the quantized-matmul path of the reference engine's Rust `Model`
+ * (src/model/kernels.rs, src/model/dense.rs, src/moe.rs). Every entry point
+ * takes plain device pointers, sizes and a hipStream_t, writes every element of
+ * its outputs, launches on that stream only and adds no host synchronisation
+ * (except rfxq_moe_ffn_grouped, whose routing needs the host logits, as the
+ * reference's does). Weights are raw GGUF blocks, row-major [out][in/QK],
+ * never repacked.
+ *
+ * Errors: every int-returning call returns 0 (RFXQ_OK) or an error code; the
+ * message is then available from rfxq_last_error() on the calling thread
+ * (pattern of src/ffi.rs:112-127 reflex_last_error / reflex_last_error_code).
+ * Codes reuse the reference's ReflexErrorCode values (include/reflex_engine.h:55-72).
+ */
+#ifndef RFXQ_H
+#define RFXQ_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RFXQ_OK 0
+#define RFXQ_ERR_GGUF 1           /* type without a kernel here (ReflexError::Gguf) */
+#define RFXQ_ERR_GPU 3            /* a HIP call failed (ReflexError::Cuda) */
+#define RFXQ_ERR_OUT_OF_MEMORY 5  /* device allocation failed */
+#define RFXQ_ERR_INVALID_INPUT 11 /* bad argument (null pointer, k out of range, ...) */
+#define RFXQ_ERR_OTHER 12         /* shape / alignment precondition (ReflexError::Other) */
+
+/* ggml type ids, as in GGUF files (src/gguf.rs:124-152). */
+#define RFXQ_TYPE_F32 0
+#define RFXQ_TYPE_F16 1
+#define RFXQ_TYPE_Q8_0 8
+#define RFXQ_TYPE_Q8_1 9
+#define RFXQ_TYPE_Q4_K 12
+#define RFXQ_TYPE_Q6_K 14
+
+/*
+ * A quantized-resident weight: `Weight { data: WeightData::Quant { ty, arena,
+ * offset, len }, shape }` (src/model/loading.rs:139-165). `data` is the device
+ * address arena + offset; shape is [in_features, out_features] or, for a
+ * stacked per-expert tensor, [in_features, out_features, expert_count].
+ * Alignment preconditions (src/kernels_cuda/gemv_q4k.cu:60-63): Q4_K data is
+ * 16-byte aligned; Q6_K and Q8_0 data are 2-byte aligned.
+ */
+typedef struct rfxq_weight {
+    uint32_t ggml_type;
+    uint32_t in_features;   /* K */
+    uint32_t out_features;  /* N */
+    uint32_t expert_count;  /* 0 for a 2-D weight */
+    const void* data;       /* device pointer to the raw blocks */
+    uint64_t len;           /* bytes */
+} rfxq_weight;
+
+/* One GEMV of a fused launch: y[N] = W . x[K]. */
+typedef struct rfxq_gemv_item {
+    const float* x;
+    const rfxq_weight* w;
+    float* y;
+} rfxq_gemv_item;
+
+typedef struct rfxq_gemv_plan rfxq_gemv_plan;
+
+/* ---- errors / setup ---------------------------------------------------- */
+
+/* Message of this thread's last failing call, or NULL (src/ffi.rs:112-127). */
+const char* rfxq_last_error(void);
+/* Code of this thread's last failing call, or RFXQ_OK. */
+int rfxq_last_error_code(void);
+/* Load the embedded gfx950 code object on `device` now (otherwise on first use),
+ * like the reference's lazy module load (src/aot.rs:136-160, kernels.rs:948-959). */
+int rfxq_init(int device);
+/* (elements per block, bytes per block) of a ggml type (src/gguf.rs:366-400). */
+int rfxq_block_dims(uint32_t ggml_type, uint32_t* block_elems, uint32_t* block_bytes);
+
+/* ---- dequantization ------------------------------------------------------ */
+
+/* Raw Q4_K / Q6_K / Q8_0 blocks -> f32 (f16_out = 0) or f16 (f16_out = 1).
+ * f32 output is bit-identical to src/dequant.rs:53 `dequantize`; f16 is its RNE
+ * rounding. Replaces dequantize_{q4k,q6k,q8_0}_coalesced{,_f16}_kernel
+ * (src/kernels_cuda/gemv_q4k.cu:359-448, gemv_q8_0.cu:253-282). */
+int rfxq_dequantize(uint32_t ggml_type, const void* blocks, uint64_t num_blocks, void* y, int f16_out,
+                    hipStream_t stream);
+
+/* ---- decode GEMV --------------------------------------------------------- */
+
+/* Model::gemv_to (src/model/kernels.rs:1463): y[N] = W . x, x_len == K.
+ * Q4_K -> gemv_q4k_r1 path (kernels.rs:2069-2103), Q6_K -> gemv_q6k_r1 path
+ * (:2022-2065), Q8_0 -> gemv_q8_0_direct (:1909-1933). */
+int rfxq_gemv_to(const float* x, uint64_t x_len, const rfxq_weight* w, float* y, hipStream_t stream);
+
+/* Model::gemv_q4k / gemv_q6k / gemv_q8_0 with `rows` input rows
+ * (kernels.rs:2110, :1972, :1874): y[rows][N] = x[rows][K] . W^T with f32
+ * activations (the fused few-row GEMV path). */
+int rfxq_gemv_rows(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y,
+                   hipStream_t stream);
+
+/* Fused GEMVs of independent weights in one launch (Model::gemv_qkv_to /
+ * gemv_gate_up_to, kernels.rs:1761-1823, generalised to any count and mix of
+ * Q4_K / Q6_K / Q8_0). */
+int rfxq_gemv_batch(const rfxq_gemv_item* items, uint32_t count, hipStream_t stream);
+
+/* A fused GEMV launch whose descriptor table is built and uploaded once and
+ * replayed by rfxq_gemv_plan_run (the decode workspace pattern of
+ * decode_step_dense_ws, src/model/decode_step.rs:139). */
+int rfxq_gemv_plan_create(const rfxq_gemv_item* items, uint32_t count, int device, rfxq_gemv_plan** out);
+int rfxq_gemv_plan_run(const rfxq_gemv_plan* plan, hipStream_t stream);
+void rfxq_gemv_plan_destroy(rfxq_gemv_plan* plan);
+
+/* ---- prefill GEMM (int8 MMQ) -------------------------------------------- */
+
+/* Q8_1-style activation quantization: xq[rows][k] int8 and xds[rows][k/32]
+ * = d_bits | s_bits << 16 (d = amax/127, q = roundf(x/d), s = d*sum(q)). */
+int rfxq_quantize_q8_1(const float* x, uint32_t rows, uint32_t k, int8_t* xq, uint32_t* xds, hipStream_t stream);
+
+/* Bytes of workspace rfxq_gemm needs for this weight and row count. */
+uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows);
+
+/* Model::gemm (src/model/kernels.rs:2197) on a quantized-resident weight:
+ * y[rows][N] = x[rows][K] . W^T. rows == 1 takes the decode GEMV; rows >= 2
+ * quantize x per 32 to int8 and run the int8-MFMA MMQ kernel (replacing
+ * gemm_quant_mma, kernels.rs:2262-2340). `workspace` may be NULL (the library
+ * then uses its own per-device buffer; concurrent calls on different streams
+ * must then not overlap) or hold rfxq_gemm_workspace_size() bytes. */
+int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
+              uint64_t workspace_bytes, hipStream_t stream);
+
+/* Test hook (the role of q{4,6}k_mma_dequant_check_kernel,
+ * src/kernels_cuda/gemm_q_mma.cu:791-838): the MMQ kernel's int32 dot product
+ * of every (row, output, 32-block): dots[rows][N][K/32]. For Q6_K the two
+ * 16-run int8 scales are folded in: sum_j qa_j * (q6_j - 32) * sc_run(j). */
+int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, const rfxq_weight* w, int32_t* dots,
+                        hipStream_t stream);
+
+/* ---- MoE ----------------------------------------------------------------- */
+
+/* src/moe.rs:47-98 route_top_k_with_norm on the host: softmax, top-k by
+ * probability (ties to the lower index), optional renormalisation. */
+int rfxq_route_top_k(const float* logits, uint32_t n, uint32_t k, int normalize, uint32_t* expert, float* weight);
+
+/* Model::quant_expert_weight (kernels.rs:2656-2694): expert e's 2-D slice of a
+ * stacked [in, out, E] quantized tensor. */
+int rfxq_quant_expert_weight(const rfxq_weight* w, uint32_t expert, rfxq_weight* out);
+
+/* Model::expert_gemv / expert_gemm (src/model/dense.rs:1086-1115). */
+int rfxq_expert_gemv(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t expert, float* y,
+                     hipStream_t stream);
+int rfxq_expert_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t expert, uint32_t rows, float* y,
+                     void* workspace, uint64_t workspace_bytes, hipStream_t stream);
+
+/* moe_gather_kernel / moe_scatter_add_kernel (src/kernels_cuda/elementwise.cu:175-222)
+ * and silu_and_mul_kernel (src/kernels_cuda/silu_and_mul.cu:7-23). */
+int rfxq_moe_gather(const float* src, const uint32_t* perm_row, float* dst, uint32_t num, uint32_t hidden,
+                    hipStream_t stream);
+int rfxq_moe_scatter_add(const float* src, const uint32_t* dest_row, const float* weight, float* dst, uint32_t num,
+                         uint32_t hidden, hipStream_t stream);
+int rfxq_silu_and_mul(const float* gate, const float* up, float* out, uint64_t n, hipStream_t stream);
+
+/* Model::moe_ffn_grouped (src/model/dense.rs:1509-1559): route every row on the
+ * host (route_top_k_with_norm, weights scaled by weight_scale), then run all
+ * experts' gate/up MMQ as one grouped launch, SiLU*up, the down MMQ as one
+ * grouped launch and a fixed-order weighted combine into out[rows][hidden]
+ * (overwritten). gate/up: [hidden, ffn, E]; down: [ffn, hidden, E]. One
+ * host-to-device copy of the routing table; no per-expert launches. */
+int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits_host,
+                         uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
+                         const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
+                         hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RFXQ_H */

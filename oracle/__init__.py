@@ -1,0 +1,233 @@
+"""TEST INFRASTRUCTURE ONLY: the CPU oracle for the GGUF quantized-matmul path.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker (or the timed CPU
+baseline). The product package ``reflex_amd`` never imports it.
+
+The numerics live in ``oracle.c`` (a C restatement of the reference's
+``src/dequant.rs`` and friends, built with ``-ffp-contract=off``); this module
+is a thin numpy/ctypes wrapper. Each function names the reference code it
+follows in ``oracle.c``'s header.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+
+F32, F16, Q8_0, Q8_1, Q4K, Q6K = 0, 1, 8, 9, 12, 14
+BLOCK_DIMS = {Q8_0: (32, 34), Q8_1: (32, 36), Q4K: (256, 144), Q6K: (256, 210)}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so from oracle.c (make)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i64, u64, i32 = ctypes.c_long, ctypes.c_uint64, ctypes.c_int
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f16_to_f32.restype = ctypes.c_float
+        L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_get_scale_min_k4.argtypes = [i32, P, P, P]
+        L.oracle_dequantize.argtypes = [i32, P, ctypes.c_size_t, u64, P]
+        L.oracle_dequantize.restype = i64
+        L.oracle_quantize_q8_1.argtypes = [P, i64, i64, P, P]
+        L.oracle_block_dots.argtypes = [i32, P, i64, i64, P, i64, P]
+        L.oracle_block_dots.restype = i32
+        L.oracle_host_matmul.argtypes = [P, P, i64, i64, i64, P]
+        for name in ("oracle_synthetic_q4k", "oracle_synthetic_q6k", "oracle_synthetic_q8_0"):
+            getattr(L, name).argtypes = [i64, i64, u64, P]
+        L.oracle_activations.argtypes = [i64, u64, P]
+        L.oracle_route_top_k.argtypes = [P, i64, i64, i32, P, P]
+        L.oracle_route_top_k.restype = i32
+        L.oracle_silu_and_mul.argtypes = [P, P, P, i64]
+        L.oracle_cpu_dequant_matmul.argtypes = [i32, P, i64, i64, P, i64, P, i32]
+        L.oracle_cpu_dequant_matmul.restype = i32
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def f16_to_f32(bits: int) -> float:
+    return lib().oracle_f16_to_f32(bits)
+
+
+def f32_to_f16(v: float) -> int:
+    return lib().oracle_f32_to_f16(v)
+
+
+def get_scale_min_k4(j: int, scales: bytes) -> tuple[int, int]:
+    q = np.frombuffer(bytes(scales), dtype=np.uint8).copy()
+    d = ctypes.c_uint8()
+    m = ctypes.c_uint8()
+    lib().oracle_get_scale_min_k4(j, _p(q), ctypes.byref(d), ctypes.byref(m))
+    return d.value, m.value
+
+
+def dequantize(ty: int, data, element_count: int) -> np.ndarray:
+    """dequant.rs:53 ``dequantize``: raw bytes -> f32, truncated to element_count.
+
+    Raises ValueError for a type without a dequantizer (the reference's Err)."""
+    buf = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, dtype=np.uint8)
+    if ty in BLOCK_DIMS:
+        qk, bb = BLOCK_DIMS[ty]
+        cap = (buf.size // bb) * qk
+    elif ty == F32:
+        cap = buf.size // 4
+    elif ty == F16:
+        cap = buf.size // 2
+    else:
+        raise ValueError(f"unknown ggml_type={ty}: no dequantizer known for it")
+    out = np.zeros(max(cap, 1), dtype=np.float32)
+    n = lib().oracle_dequantize(ty, _p(buf), buf.size, element_count, _p(out))
+    if n < 0:
+        raise ValueError(f"unknown ggml_type={ty}: no dequantizer known for it")
+    return out[:n].copy()
+
+
+def quantize_q8_1(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-32 Q8_1 activation quantization. Returns (qs int8 [rows,k], ds uint16 [rows,k/32,2])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    qs = np.zeros((rows, k), dtype=np.int8)
+    ds = np.zeros((rows, k // 32, 2), dtype=np.uint16)
+    lib().oracle_quantize_q8_1(_p(x), rows, k, _p(qs), _p(ds))
+    return qs, ds
+
+
+def block_dots(ty: int, w: np.ndarray, n: int, k: int, qa: np.ndarray) -> np.ndarray:
+    """int32 [m, n, k/32] per-32 dots of quantized activations with weight codes."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    qa = np.ascontiguousarray(qa, dtype=np.int8)
+    m = qa.shape[0]
+    out = np.zeros((m, n, k // 32), dtype=np.int32)
+    rc = lib().oracle_block_dots(ty, _p(w), n, k, _p(qa), m, _p(out))
+    if rc != 0:
+        raise ValueError(f"block_dots: unsupported type {ty}")
+    return out
+
+
+def host_matmul(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """quant_resident_tests.rs:709-729: x[rows,in] @ w[out,in]^T in f64, result f32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, in_f = x.shape
+    out_f = w.shape[0]
+    y = np.zeros((rows, out_f), dtype=np.float32)
+    lib().oracle_host_matmul(_p(x), _p(w), rows, in_f, out_f, _p(y))
+    return y
+
+
+def dequant_matrix(ty: int, w: np.ndarray, n: int, k: int) -> np.ndarray:
+    return dequantize(ty, w, n * k).reshape(n, k)
+
+
+def reference_gemm(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) -> np.ndarray:
+    """The north star's reference: dequant.rs dequantization + f64 host matmul."""
+    x2 = x.reshape(-1, k)
+    return host_matmul(x2, dequant_matrix(ty, w, n, k))
+
+
+def synthetic(ty: int, in_f: int, out_f: int, seed: int) -> np.ndarray:
+    """The reference tests' xorshift64 weight generators."""
+    qk, bb = BLOCK_DIMS[ty]
+    out = np.zeros(in_f // qk * out_f * bb, dtype=np.uint8)
+    fn = {Q4K: "oracle_synthetic_q4k", Q6K: "oracle_synthetic_q6k", Q8_0: "oracle_synthetic_q8_0"}[ty]
+    getattr(lib(), fn)(in_f, out_f, seed, _p(out))
+    return out
+
+
+def activations(n: int, seed: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float32)
+    lib().oracle_activations(n, seed, _p(out))
+    return out
+
+
+def route_top_k(logits, k: int, normalize: bool = True) -> list[tuple[int, float]]:
+    """moe.rs:47-98 route_top_k_with_norm. Raises ValueError on the reference's errors."""
+    lg = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+    idx = np.zeros(max(k, 1), dtype=np.int32)
+    w = np.zeros(max(k, 1), dtype=np.float32)
+    rc = lib().oracle_route_top_k(_p(lg) if lg.size else None, lg.size, k, int(normalize), _p(idx), _p(w))
+    if rc != 0:
+        raise ValueError("route_top_k: invalid logits or k")
+    return [(int(i), float(v)) for i, v in zip(idx[:k], w[:k])]
+
+
+def silu_and_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.zeros_like(g)
+    lib().oracle_silu_and_mul(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def moe_ffn_grouped_reference(x, routes, gate_w, up_w, down_w, ty, hidden, ffn, n_experts):
+    """dense.rs:1509-1559 semantics on the host: for each expert, gather its rows,
+    gate/up GEMM, silu*up, down GEMM, weighted scatter-add. f64 matmuls on the
+    dequantized expert slices (quant_expert_weight: kernels.rs:2656-2694)."""
+    rows = x.shape[0]
+    out = np.zeros((rows, hidden), dtype=np.float32)
+    groups = [[] for _ in range(n_experts)]
+    for r, picks in enumerate(routes):
+        for e, wgt in picks:
+            groups[e].append((r, wgt))
+    g_len = gate_w.size // n_experts
+    d_len = down_w.size // n_experts
+    for e, grp in enumerate(groups):
+        if not grp:
+            continue
+        rr = np.array([r for r, _ in grp])
+        ww = np.array([w for _, w in grp], dtype=np.float32)
+        xe = x[rr]
+        g = reference_gemm(ty, gate_w[e * g_len:(e + 1) * g_len], ffn, hidden, xe)
+        u = reference_gemm(ty, up_w[e * g_len:(e + 1) * g_len], ffn, hidden, xe)
+        a = silu_and_mul(g, u)
+        dn = reference_gemm(ty, down_w[e * d_len:(e + 1) * d_len], hidden, ffn, a)
+        out[rr] += ww[:, None] * dn
+    return out
+
+
+def cpu_dequant_matmul(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray, threads: int) -> np.ndarray:
+    """The CPU baseline: dequant restatement + f32 matmul over `threads` OpenMP threads."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x2 = np.ascontiguousarray(x.reshape(-1, k), dtype=np.float32)
+    y = np.zeros((x2.shape[0], n), dtype=np.float32)
+    rc = lib().oracle_cpu_dequant_matmul(ty, _p(w), n, k, _p(x2), x2.shape[0], _p(y), threads)
+    if rc != 0:
+        raise ValueError(f"unsupported type {ty}")
+    return y
+
+
+def rel_max_diff(a: np.ndarray, b: np.ndarray) -> float:
+    """quant_resident_tests.rs:6-10: max|a-b| / max|b|."""
+    scale = max(float(np.max(np.abs(b))), 1e-30)
+    return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64)))) / scale
+
+
+def rel_err_row_l2(y: np.ndarray, ref: np.ndarray) -> float:
+    """The north star's metric: max over output rows of max|y - ref| / ||ref_row||_2."""
+    y2 = y.reshape(-1, y.shape[-1]).astype(np.float64)
+    r2 = ref.reshape(-1, ref.shape[-1]).astype(np.float64)
+    num = np.max(np.abs(y2 - r2), axis=1)
+    den = np.maximum(np.linalg.norm(r2, axis=1), 1e-30)
+    return float(np.max(num / den))

@@ -1,0 +1,83 @@
+"""reflex_amd: MI355X-native GGUF quantized-matmul path (Q4_K / Q6_K / Q8_0).
+
+The compute lives in ``librfxq.so`` (HIP C++ host code + an embedded gfx950
+code object, see ``build.py``); its C ABI is ``include/rfxq.h``. This package
+loads it with ctypes and mirrors the reference's Rust call surface for the
+path (``reflex_amd.quant``). There is no CPU fallback: if the library is not
+built, or the device is not a gfx950, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librfxq.so")
+
+_lib = None
+
+
+class RfxqWeight(ctypes.Structure):
+    """``rfxq_weight`` (include/rfxq.h)."""
+
+    _fields_ = [
+        ("ggml_type", ctypes.c_uint32),
+        ("in_features", ctypes.c_uint32),
+        ("out_features", ctypes.c_uint32),
+        ("expert_count", ctypes.c_uint32),
+        ("data", ctypes.c_void_p),
+        ("len", ctypes.c_uint64),
+    ]
+
+
+class RfxqGemvItem(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.POINTER(RfxqWeight)), ("y", ctypes.c_void_p)]
+
+
+# name -> (restype, argtypes); every symbol declared in include/rfxq.h
+_P, _U32, _U64, _I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+_WP = ctypes.POINTER(RfxqWeight)
+SIGNATURES = {
+    "rfxq_last_error": (ctypes.c_char_p, []),
+    "rfxq_last_error_code": (_I, []),
+    "rfxq_init": (_I, [_I]),
+    "rfxq_block_dims": (_I, [_U32, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
+    "rfxq_dequantize": (_I, [_U32, _P, _U64, _P, _I, _P]),
+    "rfxq_gemv_to": (_I, [_P, _U64, _WP, _P, _P]),
+    "rfxq_gemv_rows": (_I, [_P, _U64, _WP, _U32, _P, _P]),
+    "rfxq_gemv_batch": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _P]),
+    "rfxq_gemv_plan_create": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _I, ctypes.POINTER(_P)]),
+    "rfxq_gemv_plan_run": (_I, [_P, _P]),
+    "rfxq_gemv_plan_destroy": (None, [_P]),
+    "rfxq_quantize_q8_1": (_I, [_P, _U32, _U32, _P, _P, _P]),
+    "rfxq_gemm_workspace_size": (_U64, [_WP, _U32]),
+    "rfxq_gemm": (_I, [_P, _U64, _WP, _U32, _P, _P, _U64, _P]),
+    "rfxq_mmq_block_dots": (_I, [_P, _P, _U32, _WP, _P, _P]),
+    "rfxq_route_top_k": (_I, [_P, _U32, _U32, _I, _P, _P]),
+    "rfxq_quant_expert_weight": (_I, [_WP, _U32, _WP]),
+    "rfxq_expert_gemv": (_I, [_P, _U64, _WP, _U32, _P, _P]),
+    "rfxq_expert_gemm": (_I, [_P, _U64, _WP, _U32, _U32, _P, _P, _U64, _P]),
+    "rfxq_moe_gather": (_I, [_P, _P, _P, _U32, _U32, _P]),
+    "rfxq_moe_scatter_add": (_I, [_P, _P, _P, _P, _U32, _U32, _P]),
+    "rfxq_silu_and_mul": (_I, [_P, _P, _P, _U64, _P]),
+    "rfxq_moe_ffn_grouped": (_I, [_P, _U32, _U32, _P, _U32, _U32, _I, ctypes.c_float, _WP, _WP, _WP, _P, _P]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load librfxq.so (built by ``python -m reflex_amd.build``); raises if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m reflex_amd.build` "
+                               "(there is no CPU fallback for this path)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+from .quant import *  # noqa: E402,F401,F403

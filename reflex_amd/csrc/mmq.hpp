@@ -1,0 +1,383 @@
+// MMQ prefill GEMM: Y[M,N] = X[M,K] . W[N,K]^T with X quantized per 32 to int8
+// (Q8_1: quant.hpp) and W raw Q4_K / Q6_K / Q8_0 blocks, contracted on the
+// gfx950 int8 matrix cores (v_mfma_i32_32x32x32_i8: one MFMA = one 32-element
+// activation block) with the per-block scale and min corrections applied in
+// f32. Replaces the reference's f16 tensor-core prefill
+// `gemm_q{4,6}k_mma_*_kernel` (src/kernels_cuda/gemm_q_mma.cu:299-764) and its
+// split-K reduce (:769-783), and serves `Model::gemm` (src/model/kernels.rs:2197)
+// and the per-expert `expert_gemm` (src/model/dense.rs:1103) as one grouped
+// launch over a descriptor table.
+//
+// Per 32-block s of super-block sb, for output (m, n):
+//   D = sum_{k in s} qa[m,k] * code[n,k]                    (exact int32, MFMA)
+//   Q4_K: y += da[m,s] * (d*sc_s)[n] * D  -  s_a[m,s] * (dmin*m_s)[n]
+//   Q6_K: D folds the two 16-run scales: D = sc_lo*D_lo + sc_hi*D_hi;
+//         y += da[m,s] * d[n] * D
+//   Q8_0: y += da[m,s] * d[n,s] * D
+// The min term of a Q4_K super-block is one f16 MFMA (32x32x8, K = the 8
+// sub-blocks) accumulated into the same f32 accumulators.
+//
+// Tile: 128 (M) x 128 (N) per 256-thread workgroup; each wave owns 64 x 64 =
+// 2 x 2 MFMA tiles. Activation scales for the tile's 128 rows are staged in
+// LDS once per super-block; A (int8 activations) and B (unpacked weights) go
+// straight from global memory into MFMA operand registers (lane l holds row /
+// column l%32 and the 16 K-values [16*(l/32), +16) of the 32-block).
+// Split-K writes partial tiles to a workspace reduced in fixed order.
+#pragma once
+#include "common.hpp"
+
+struct MmqDesc {
+    const uint8_t* w;       // raw blocks [n][k/QK]
+    const int8_t* xq;       // quantized activations [rows_src][ldq]
+    const uint32_t* xds;    // [rows_src][k/32] d | s << 16
+    const int32_t* rows;    // optional [m] source rows (gather); null = identity
+    float* y;               // [splits][m][ldy] (splits > 1: workspace)
+    uint32_t m, n, k, type;
+    uint32_t ldq, ldy, tiles_m, tiles_n;
+    uint32_t splits, sb_per_split, wg_begin, pad;
+    int32_t* dots_out;      // [m][n][k/32] for the rfxq_mmq_dots_* test hook
+};
+
+#define MMQ_INLINE 2
+struct MmqArgs {
+    const MmqDesc* table;
+    uint32_t ndesc, pad;
+    MmqDesc inl[MMQ_INLINE];
+};
+
+#define MMQ_BM 128
+#define MMQ_BN 128
+
+RFXQ_DEV v16i_t mfma_i8(v4i_t a, v4i_t b) {
+    const v16i_t z = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+}
+
+RFXQ_DEV v4i_t as_v4i(u4_t v) { return __builtin_bit_cast(v4i_t, v); }
+
+// ---------------------------------------------------------------- weights
+
+// Q4_K: (scale, min) pairs of sub-blocks 2g and 2g+1 from the 16-byte header
+// (get_scale_min_k4, src/dequant.rs:39-47), as d*sc and dmin*m.
+RFXQ_DEV void q4k_pair_scales(const u4_t hdr, uint32_t g, float& dsc0, float& dsc1) {
+    const uint32_t sh = (g & 1u) * 16u;
+    const uint32_t a = hdr.y >> sh, c = hdr.w >> sh;
+    uint32_t sc1, sc2;
+    if (g < 2u) {
+        sc1 = a & 63u;
+        sc2 = (a >> 8) & 63u;
+    } else {
+        sc1 = (c & 0xFu) | ((a >> 2) & 0x30u);
+        sc2 = ((c >> 8) & 0xFu) | ((a >> 10) & 0x30u);
+    }
+    const float d = f16_bits_to_f32(hdr.x);
+    dsc0 = d * (float)sc1;
+    dsc1 = d * (float)sc2;
+}
+
+// -(dmin * m_s) for s = 4h .. 4h+3 as f16 (the min MFMA's B operand).
+RFXQ_DEV h4_t q4k_neg_mins(const u4_t hdr, uint32_t h) {
+    const float dmin = f16_bits_to_f32(hdr.x >> 16);
+    uint32_t m[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t lo = (hdr.z >> (8 * e)) & 63u;                                         // j = e < 4
+        const uint32_t hi = ((hdr.w >> (8 * e + 4)) & 0xFu) | (((hdr.z >> (8 * e + 6)) & 3u) << 4);  // j = 4 + e
+        m[e] = h ? hi : lo;
+    }
+    return h4_t{(half_t)(-(dmin * (float)m[0])), (half_t)(-(dmin * (float)m[1])), (half_t)(-(dmin * (float)m[2])),
+                (half_t)(-(dmin * (float)m[3]))};
+}
+
+RFXQ_DEV u4_t nib_lo(u4_t v) { return v & 0x0F0F0F0Fu; }
+RFXQ_DEV u4_t nib_hi(u4_t v) { return (v >> 4) & 0x0F0F0F0Fu; }
+
+// Q8_0: one 34-byte block (2-byte aligned, never read past its end); returns
+// the lane's 16 quants (K half h) and d.
+RFXQ_DEV u4_t load_q8_0_half(const uint8_t* blk, uint32_t h, float& d) {
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
+    const uint8_t* pa = reinterpret_cast<const uint8_t*>(addr & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(addr & 3u);
+    const u4_t w0 = ld16_a4(pa), w1 = ld16_a4(pa + 16);
+    uint32_t w8;
+    if (sh) w8 = *reinterpret_cast<const uint32_t*>(pa + 32);
+    else w8 = *reinterpret_cast<const uint16_t*>(blk + 32);
+    d = f16_bits_to_f32(sh ? (w0.x >> 16) : w0.x);
+    // qs dword j = bytes [2+4j, 6+4j) of the block; the lane needs j = 4h..4h+3,
+    // i.e. dwords W0..W4 = w[4h .. 4h+4] of the dword-aligned read.
+    const uint32_t W0 = h ? w1.x : w0.x, W1 = h ? w1.y : w0.y, W2 = h ? w1.z : w0.z, W3 = h ? w1.w : w0.w;
+    const uint32_t W4 = h ? w8 : w1.x;
+    u4_t q;
+    if (sh) {
+        q.x = W1;
+        q.y = W2;
+        q.z = W3;
+        q.w = W4;
+    } else {
+        q.x = alignbyte(W1, W0, 2u);
+        q.y = alignbyte(W2, W1, 2u);
+        q.z = alignbyte(W3, W2, 2u);
+        q.w = alignbyte(W4, W3, 2u);
+    }
+    return q;
+}
+
+RFXQ_DEV u4_t seg16_mmq(const uint8_t* pa, uint32_t o, uint32_t sh) {
+    const u4_t v = ld16_a4(pa + o);
+    const uint32_t e = *reinterpret_cast<const uint32_t*>(pa + o + 16);
+    u4_t r;
+    r.x = alignbyte(v.y, v.x, sh);
+    r.y = alignbyte(v.z, v.y, sh);
+    r.z = alignbyte(v.w, v.z, sh);
+    r.w = alignbyte(e, v.w, sh);
+    return r;
+}
+
+// Signed Q6_K codes (q6 - 32) of run t for the lane's 16 positions, from the
+// ql segment (low or high nibbles) and the qh segment.
+RFXQ_DEV u4_t q6_codes(u4_t ql, u4_t qh, uint32_t t) {
+    const u4_t lo = (t & 2u) ? nib_hi(ql) : nib_lo(ql);
+    const u4_t hb = ((qh >> (2u * t)) & 0x03030303u) << 4;
+    return (((lo | hb) | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+RFXQ_DEV int sbyte(uint32_t w, uint32_t byte) { return (int)(int8_t)(w >> (8u * byte)); }
+
+template <uint32_t TY, bool DOTS>
+RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, half_t* lds_sa) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+    const uint32_t h = lane >> 5, l32 = lane & 31u;
+
+    const uint32_t ks = t_local % ds.splits;
+    const uint32_t rest = t_local / ds.splits;
+    const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
+    const uint32_t m0 = tm * MMQ_BM, n0 = tn * MMQ_BN;
+    const uint32_t nsb = ds.k / 256u;
+    const uint32_t sb0 = ks * ds.sb_per_split;
+    const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
+    const uint32_t nkb = ds.k / 32u;
+    const uint64_t row_bytes = TY == TY_Q4K ? (uint64_t)nsb * 144u : TY == TY_Q6K ? (uint64_t)nsb * 210u
+                                                                                 : (uint64_t)nkb * 34u;
+
+    const uint8_t* arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        uint32_t m = m0 + 64u * wm + 32u * i + l32;
+        m = m < ds.m ? m : ds.m - 1u;
+        const uint32_t src = ds.rows ? (uint32_t)ds.rows[m] : m;
+        arow[i] = reinterpret_cast<const uint8_t*>(ds.xq) + (uint64_t)src * ds.ldq + 16u * h;
+    }
+    const uint8_t* brow[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        uint32_t n = n0 + 64u * wn + 32u * j + l32;
+        n = n < ds.n ? n : ds.n - 1u;
+        brow[j] = ds.w + (uint64_t)n * row_bytes;
+    }
+    const uint32_t st_r = tid >> 1, st_part = tid & 1u;
+    const uint32_t* st_src;
+    {
+        uint32_t m = m0 + st_r;
+        m = m < ds.m ? m : ds.m - 1u;
+        const uint32_t src = ds.rows ? (uint32_t)ds.rows[m] : m;
+        st_src = ds.xds + (uint64_t)src * nkb + 4u * st_part;
+    }
+
+    v16f_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
+
+    for (uint32_t sb = sb0; sb < sb1; sb++) {
+        // ---- activation scales of the tile's 128 rows: da as f32 [s][row], s_a as f16 [row][s]
+        {
+            const u4_t v = *reinterpret_cast<const u4_t*>(st_src + 8u * sb);
+            lds_da[(4u * st_part + 0u) * MMQ_BM + st_r] = f16_bits_to_f32(v.x);
+            lds_da[(4u * st_part + 1u) * MMQ_BM + st_r] = f16_bits_to_f32(v.y);
+            lds_da[(4u * st_part + 2u) * MMQ_BM + st_r] = f16_bits_to_f32(v.z);
+            lds_da[(4u * st_part + 3u) * MMQ_BM + st_r] = f16_bits_to_f32(v.w);
+            const uint2 sa = {(v.x >> 16) | (v.y & 0xFFFF0000u), (v.z >> 16) | (v.w & 0xFFFF0000u)};
+            *reinterpret_cast<uint2*>(lds_sa + st_r * 8u + 4u * st_part) = sa;
+        }
+        __syncthreads();
+
+        u4_t hdr[2];
+        uint32_t q6sh[2];
+        const uint8_t* q6pa[2];
+        uint32_t q6sc[2][4];
+        float q6d[2];
+        if (TY == TY_Q4K) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) hdr[j] = ld16(brow[j] + (uint64_t)sb * 144u);
+        } else if (TY == TY_Q6K) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint8_t* blk = brow[j] + (uint64_t)sb * 210u;
+                const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
+                q6pa[j] = reinterpret_cast<const uint8_t*>(addr & ~(uintptr_t)3);
+                q6sh[j] = (uint32_t)(addr & 3u);
+                const u4_t sw = ld16_a4(q6pa[j] + 192);
+                uint32_t tail;
+                if (q6sh[j]) tail = *reinterpret_cast<const uint32_t*>(q6pa[j] + 208);
+                else tail = *reinterpret_cast<const uint16_t*>(blk + 208);
+                q6sc[j][0] = alignbyte(sw.y, sw.x, q6sh[j]);
+                q6sc[j][1] = alignbyte(sw.z, sw.y, q6sh[j]);
+                q6sc[j][2] = alignbyte(sw.w, sw.z, q6sh[j]);
+                q6sc[j][3] = alignbyte(tail, sw.w, q6sh[j]);
+                q6d[j] = f16_bits_to_f32(q6sh[j] ? (tail >> 16) : tail);
+            }
+        }
+
+#pragma unroll 1
+        for (uint32_t g = 0; g < 4; g++) {
+            // per 32-block pair (2g, 2g+1): B operands and weight scales
+            u4_t bw[2][2];
+            float wsc[2][2];
+            int scl[2][2], sch[2][2];  // Q6_K: scales of the two 16-runs
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if (TY == TY_Q4K) {
+                    const u4_t qv = ld16(brow[j] + (uint64_t)sb * 144u + 16u + 32u * g + 16u * h);
+                    bw[j][0] = nib_lo(qv);
+                    bw[j][1] = nib_hi(qv);
+                    q4k_pair_scales(hdr[j], g, wsc[j][0], wsc[j][1]);
+                } else if (TY == TY_Q6K) {
+                    const uint32_t n = g >> 1, t0 = 2u * (g & 1u);
+                    const u4_t qla = seg16_mmq(q6pa[j], 64u * n + 16u * h, q6sh[j]);
+                    const u4_t qlc = seg16_mmq(q6pa[j], 64u * n + 32u + 16u * h, q6sh[j]);
+                    const u4_t qh = seg16_mmq(q6pa[j], 128u + 32u * n + 16u * h, q6sh[j]);
+                    bw[j][0] = q6_codes(qla, qh, t0);
+                    bw[j][1] = q6_codes(qlc, qh, t0 + 1u);
+                    // scales sc[8n + hh + 2t]: dword (2n + (t>>1)), byte (hh + 2(t&1))
+                    const uint32_t wv = n ? (g & 1u ? q6sc[j][3] : q6sc[j][2]) : (g & 1u ? q6sc[j][1] : q6sc[j][0]);
+                    scl[j][0] = sbyte(wv, 0);
+                    sch[j][0] = sbyte(wv, 1);
+                    scl[j][1] = sbyte(wv, 2);
+                    sch[j][1] = sbyte(wv, 3);
+                    wsc[j][0] = q6d[j];
+                    wsc[j][1] = q6d[j];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2; e++)
+                        bw[j][e] = load_q8_0_half(brow[j] + (uint64_t)(8u * sb + 2u * g + e) * 34u, h, wsc[j][e]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t s = 2u * g + e;
+                v4i_t a[2];
+#pragma unroll
+                for (int i = 0; i < 2; i++) a[i] = as_v4i(ld16(arow[i] + 256u * sb + 32u * s));
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const float* dap = lds_da + s * MMQ_BM + 64u * wm + 32u * i + 4u * h;
+                    float da[16];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v = *reinterpret_cast<const float4*>(dap + 8u * q);
+                        da[4 * q + 0] = v.x;
+                        da[4 * q + 1] = v.y;
+                        da[4 * q + 2] = v.z;
+                        da[4 * q + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        v16i_t D;
+                        if (TY == TY_Q6K) {
+                            const u4_t z = {0u, 0u, 0u, 0u};
+                            const v16i_t D0 = mfma_i8(a[i], as_v4i(h ? z : bw[j][e]));
+                            const v16i_t D1 = mfma_i8(a[i], as_v4i(h ? bw[j][e] : z));
+#pragma unroll
+                            for (int r = 0; r < 16; r++) D[r] = D0[r] * scl[j][e] + D1[r] * sch[j][e];
+                        } else {
+                            D = mfma_i8(a[i], as_v4i(bw[j][e]));
+                        }
+                        if (DOTS) {
+                            const uint32_t col = n0 + 64u * wn + 32u * j + l32;
+#pragma unroll
+                            for (int r = 0; r < 16; r++) {
+                                const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+                                if (row < ds.m && col < ds.n)
+                                    ds.dots_out[((uint64_t)row * ds.n + col) * nkb + 8u * sb + s] = D[r];
+                            }
+                        } else {
+                            const float ws = wsc[j][e];
+#pragma unroll
+                            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)D[r], da[r] * ws, acc[i][j][r]);
+                        }
+                    }
+                }
+            }
+        }
+        if (TY == TY_Q4K && !DOTS) {
+            // min correction: acc -= sum_s s_a[m,s] * (dmin*m_s)[n] over this super-block
+            h4_t nm[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) nm[j] = q4k_neg_mins(hdr[j], h);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const h4_t sa = *reinterpret_cast<const h4_t*>(lds_sa + (64u * wm + 32u * i + l32) * 8u + 4u * h);
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, nm[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    if (DOTS) return;
+    float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t col = n0 + 64u * wn + 32u * j + l32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+                if (row < ds.m && col < ds.n) y[(uint64_t)row * ds.ldy + col] = acc[i][j][r];
+            }
+        }
+}
+
+RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
+    if (a.ndesc <= MMQ_INLINE) {
+        MmqDesc d = a.inl[0];
+        if (a.ndesc > 1 && wg >= a.inl[1].wg_begin) d = a.inl[1];
+        return d;
+    }
+    uint32_t lo = 0, hi = a.ndesc - 1u;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) >> 1;
+        if (a.table[mid].wg_begin <= wg) lo = mid;
+        else hi = mid - 1u;
+    }
+    return a.table[lo];
+}
+
+#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS)                                            \
+    extern "C" __global__ __launch_bounds__(256) void NAME(MmqArgs args) {    \
+        __shared__ float lds_da[8 * MMQ_BM];                                  \
+        __shared__ half_t lds_sa[MMQ_BM * 8];                                 \
+        const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
+        mmq_tile<TY, DOTS>(d, blockIdx.x - d.wg_begin, lds_da, lds_sa);       \
+    }
+RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true)
+
+// y[i] = sum_z ws[z][i], added in split order (deterministic).
+extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float* __restrict__ ws,
+                                                                    float* __restrict__ y, uint64_t n,
+                                                                    uint32_t splits) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) {
+        float s = ws[i];
+        for (uint32_t z = 1; z < splits; z++) s += ws[(uint64_t)z * n + i];
+        y[i] = s;
+    }
+}

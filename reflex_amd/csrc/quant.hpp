@@ -1,0 +1,55 @@
+// Activation quantization to int8 per 32 elements with an f16 scale and sum
+// (the Q8_1 block of src/dequant.rs:228-240: d, s = d * sum(q), qs[32]),
+// using ggml's published quantize_row_q8_1_ref rounding: d = amax / 127,
+// id = d ? 1/d : 0, q = roundf(x * id). The reference has no activation
+// quantizer (its prefill casts to f16, src/kernels_cuda/convert.cu:91); this
+// is the input stage of the int8 MMQ GEMM.
+//
+// Layout for the GEMM: xq [rows][k] int8 (row stride ldq bytes) and xds
+// [rows][k/32] u32 = d_bits | s_bits << 16. Optional `src_rows` gathers
+// x rows (x row src_rows[r] -> output row r).
+#pragma once
+#include "common.hpp"
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,
+                                                                    const int32_t* __restrict__ src_rows,
+                                                                    uint32_t rows, uint32_t k,
+                                                                    int8_t* __restrict__ xq, uint32_t ldq,
+                                                                    uint32_t* __restrict__ xds) {
+    const uint32_t nblk = k / 32u;
+    const uint64_t total = (uint64_t)rows * nblk;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t wave_global = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint64_t nwaves = ((uint64_t)gridDim.x * blockDim.x) >> 6;
+    for (uint64_t b0 = wave_global * 8u; b0 < total; b0 += nwaves * 8u) {
+        const uint64_t bi = b0 + (lane >> 3);
+        const bool valid = bi < total;
+        const uint64_t bb = valid ? bi : total - 1u;
+        const uint32_t row = (uint32_t)(bb / nblk), blk = (uint32_t)(bb % nblk);
+        const uint32_t part = lane & 7u;
+        const uint32_t srow = src_rows ? (uint32_t)src_rows[row] : row;
+        const float4 v = *reinterpret_cast<const float4*>(x + (uint64_t)srow * ldx + 32u * blk + 4u * part);
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id);
+        const int q2 = (int)roundf(v.z * id), q3 = (int)roundf(v.w * id);
+        int sum = q0 + q1 + q2 + q3;
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 1, 64);
+        if (valid) {
+            const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
+                                    ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
+            *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
+            if (part == 0u) {
+                const uint32_t dbits = __builtin_bit_cast(uint16_t, (half_t)d);
+                const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)((float)sum * d));
+                xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
+            }
+        }
+    }
+}

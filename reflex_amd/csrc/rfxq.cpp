@@ -1,0 +1,959 @@
+// Host side of librfxq: the C ABI declared in include/rfxq.h.
+//
+// Mirrors the reference's matmul dispatch for quantized-resident weights
+// (src/model/kernels.rs: gemv_to :1463, gemv :1826, gemv_q4k :2110,
+// gemv_q6k :1972, gemv_q8_0 :1874, gemm :2197, gemm_quant_mma :2262,
+// quant_expert_weight :2656, moe_gather/moe_scatter_add :2722-2790;
+// src/model/dense.rs: expert_gemv/expert_gemm :1086-1115, moe_ffn_grouped
+// :1509-1559; src/moe.rs:47-98 route_top_k_with_norm): the same preconditions
+// and error kinds, checked on the host before any launch, and the kernels of
+// the embedded gfx950 code object resolved by name (src/aot.rs:113-160).
+#include "../../include/rfxq.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+extern "C" const unsigned char rfxq_code_object[];
+extern "C" const unsigned char rfxq_code_object_end[];
+
+namespace {
+
+// ------------------------------------------------------------------ errors
+
+thread_local std::string g_err;
+thread_local int g_code = RFXQ_OK;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    g_code = code;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    g_code = RFXQ_OK;
+    return RFXQ_OK;
+}
+
+#define HIPCHK(expr, what)                                                                        \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess) return fail(RFXQ_ERR_GPU, "%s: %s", (what), hipGetErrorString(e_)); \
+    } while (0)
+
+// ------------------------------------------------------------------ descriptors (device layout)
+
+struct GemvDesc {
+    const void* w;
+    const float* x;
+    float* y;
+    uint32_t k, n, type, lpr_log2;
+    uint32_t rows_per_wg, wg_begin, pad0, pad1;
+};
+constexpr uint32_t kGemvInline = 4;
+struct GemvArgs {
+    const GemvDesc* table;
+    uint32_t ndesc, pad;
+    GemvDesc inl[kGemvInline];
+};
+static_assert(sizeof(GemvDesc) == 56, "GemvDesc layout");
+
+struct MmqDesc {
+    const void* w;
+    const int8_t* xq;
+    const uint32_t* xds;
+    const int32_t* rows;
+    float* y;
+    uint32_t m, n, k, type;
+    uint32_t ldq, ldy, tiles_m, tiles_n;
+    uint32_t splits, sb_per_split, wg_begin, pad;
+    int32_t* dots_out;
+};
+constexpr uint32_t kMmqInline = 2;
+struct MmqArgs {
+    const MmqDesc* table;
+    uint32_t ndesc, pad;
+    MmqDesc inl[kMmqInline];
+};
+static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
+
+constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
+constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
+
+// ------------------------------------------------------------------ per-device module
+
+struct Ctx {
+    int device = -1;
+    int cus = 256;
+    hipModule_t mod = nullptr;
+    hipFunction_t gemv = nullptr, quant = nullptr, reduce = nullptr;
+    hipFunction_t mmq[3] = {}, dots[3] = {};
+    hipFunction_t deq[3][2] = {};
+    hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
+    void* ws = nullptr;
+    uint64_t ws_bytes = 0;
+};
+
+std::mutex g_mu;
+std::map<int, std::unique_ptr<Ctx>> g_ctx;
+
+int type_index(uint32_t ty) { return ty == RFXQ_TYPE_Q4_K ? 0 : ty == RFXQ_TYPE_Q6_K ? 1 : 2; }
+
+int load_ctx(int device, Ctx** out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ctx.find(device);
+    if (it != g_ctx.end()) {
+        *out = it->second.get();
+        return RFXQ_OK;
+    }
+    auto c = std::make_unique<Ctx>();
+    c->device = device;
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(RFXQ_ERR_GPU, "device %d is %s; this build's kernels are gfx950 only", device, prop.gcnArchName);
+    c->cus = prop.multiProcessorCount;
+    HIPCHK(hipModuleLoadData(&c->mod, rfxq_code_object), "hipModuleLoadData(embedded gfx950 code object)");
+    struct {
+        hipFunction_t* f;
+        const char* name;
+    } fns[] = {
+        {&c->gemv, "rfxq_gemv"},
+        {&c->quant, "rfxq_quantize_q8_1"},
+        {&c->reduce, "rfxq_splitk_reduce"},
+        {&c->mmq[0], "rfxq_mmq_q4k"},
+        {&c->mmq[1], "rfxq_mmq_q6k"},
+        {&c->mmq[2], "rfxq_mmq_q8_0"},
+        {&c->dots[0], "rfxq_mmq_dots_q4k"},
+        {&c->dots[1], "rfxq_mmq_dots_q6k"},
+        {&c->dots[2], "rfxq_mmq_dots_q8_0"},
+        {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
+        {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
+        {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
+        {&c->deq[1][1], "rfxq_dequant_q6k_f16"},
+        {&c->deq[2][0], "rfxq_dequant_q8_0_f32"},
+        {&c->deq[2][1], "rfxq_dequant_q8_0_f16"},
+        {&c->gather, "rfxq_moe_gather"},
+        {&c->scatter, "rfxq_moe_scatter_add"},
+        {&c->silu, "rfxq_silu_and_mul"},
+        {&c->combine, "rfxq_moe_combine"},
+    };
+    for (auto& f : fns) {
+        hipError_t e = hipModuleGetFunction(f.f, c->mod, f.name);
+        if (e != hipSuccess)
+            return fail(RFXQ_ERR_GPU, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
+    }
+    *out = c.get();
+    g_ctx[device] = std::move(c);
+    return RFXQ_OK;
+}
+
+int current_ctx(Ctx** out) {
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev), "hipGetDevice");
+    return load_ctx(dev, out);
+}
+
+// Grow-only per-device scratch (the reference allocates per call, alloc_out
+// kernels.rs:1001); freed at process exit.
+int ctx_workspace(Ctx* c, uint64_t bytes, void** out) {
+    if (bytes > c->ws_bytes) {
+        if (c->ws) {
+            HIPCHK(hipDeviceSynchronize(), "hipDeviceSynchronize before workspace growth");
+            HIPCHK(hipFree(c->ws), "hipFree(workspace)");
+            c->ws = nullptr;
+            c->ws_bytes = 0;
+        }
+        const uint64_t sz = std::max<uint64_t>(bytes, 1u << 20);
+        hipError_t e = hipMalloc(&c->ws, sz);
+        if (e != hipSuccess) return fail(RFXQ_ERR_OUT_OF_MEMORY, "workspace alloc of %llu bytes: %s",
+                                         (unsigned long long)sz, hipGetErrorString(e));
+        c->ws_bytes = sz;
+    }
+    *out = c->ws;
+    return RFXQ_OK;
+}
+
+int launch(hipFunction_t f, uint32_t grid, uint32_t lds, hipStream_t stream, void* args, size_t args_size,
+           const char* what) {
+    void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
+                   HIP_LAUNCH_PARAM_END};
+    HIPCHK(hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, lds, stream, nullptr, cfg), what);
+    return RFXQ_OK;
+}
+
+// ------------------------------------------------------------------ shapes
+
+bool block_dims(uint32_t ty, uint32_t* qk, uint32_t* bb) {
+    switch (ty) {
+        case RFXQ_TYPE_F32: *qk = 1; *bb = 4; return true;
+        case RFXQ_TYPE_F16: *qk = 1; *bb = 2; return true;
+        case RFXQ_TYPE_Q8_0: *qk = 32; *bb = 34; return true;
+        case RFXQ_TYPE_Q8_1: *qk = 32; *bb = 36; return true;
+        case RFXQ_TYPE_Q4_K: *qk = 256; *bb = 144; return true;
+        case RFXQ_TYPE_Q6_K: *qk = 256; *bb = 210; return true;
+        default: return false;
+    }
+}
+
+bool is_kernel_type(uint32_t ty) {
+    return ty == RFXQ_TYPE_Q4_K || ty == RFXQ_TYPE_Q6_K || ty == RFXQ_TYPE_Q8_0;
+}
+
+const char* type_name(uint32_t ty) {
+    return ty == RFXQ_TYPE_Q4_K ? "Q4K" : ty == RFXQ_TYPE_Q6_K ? "Q6K" : ty == RFXQ_TYPE_Q8_0 ? "Q8_0" : "?";
+}
+
+uint64_t row_bytes(uint32_t ty, uint32_t k) {
+    uint32_t qk = 1, bb = 1;
+    block_dims(ty, &qk, &bb);
+    return (uint64_t)(k / qk) * bb;
+}
+
+// The 2-D weight preconditions every kernel shares (kernels.rs:2118-2130).
+int check_weight(const rfxq_weight* w, const char* what) {
+    if (!w) return fail(RFXQ_ERR_INVALID_INPUT, "%s: weight is NULL", what);
+    if (!is_kernel_type(w->ggml_type))
+        return fail(RFXQ_ERR_GGUF, "%s: no quantized kernel for ggml_type=%u", what, w->ggml_type);
+    if (w->expert_count != 0)
+        return fail(RFXQ_ERR_OTHER, "%s: 3-D per-expert weight; slice it with rfxq_quant_expert_weight", what);
+    const uint32_t qk = w->ggml_type == RFXQ_TYPE_Q8_0 ? 32u : 256u;
+    if (w->in_features == 0 || w->in_features % qk != 0)
+        return fail(RFXQ_ERR_OTHER, "%s: in_features=%u (must be a multiple of %u)", what, w->in_features, qk);
+    if (w->out_features == 0) return fail(RFXQ_ERR_OTHER, "%s: out_features=0", what);
+    const uint64_t need = row_bytes(w->ggml_type, w->in_features) * w->out_features;
+    if (w->len < need)
+        return fail(RFXQ_ERR_OTHER, "%s: %s weight of %llu bytes, shape [%u, %u] needs %llu", what,
+                    type_name(w->ggml_type), (unsigned long long)w->len, w->in_features, w->out_features,
+                    (unsigned long long)need);
+    if (!w->data) return fail(RFXQ_ERR_INVALID_INPUT, "%s: weight data is NULL", what);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w->data);
+    if (w->ggml_type == RFXQ_TYPE_Q4_K ? (a % 16u) != 0 : (a % 2u) != 0)
+        return fail(RFXQ_ERR_OTHER, "%s: %s weight data at %p is not %u-byte aligned", what,
+                    type_name(w->ggml_type), w->data, w->ggml_type == RFXQ_TYPE_Q4_K ? 16u : 2u);
+    return RFXQ_OK;
+}
+
+uint32_t env_u32(const char* name, uint32_t dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    char* end = nullptr;
+    unsigned long x = std::strtoul(v, &end, 10);
+    if (end == v || *end) return dflt;
+    return (uint32_t)x;
+}
+
+// ------------------------------------------------------------------ GEMV planning
+
+int make_gemv_desc(const Ctx* c, const float* x, const rfxq_weight* w, float* y, GemvDesc* d, uint32_t* wgs,
+                   uint32_t* lds) {
+    if (int rc = check_weight(w, "gemv")) return rc;
+    const uint32_t k = w->in_features, n = w->out_features;
+    if (k > kMaxGemvK) return fail(RFXQ_ERR_OTHER, "gemv: in_features=%u exceeds %u", k, kMaxGemvK);
+    if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemv: x or y is NULL");
+    if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemv: x is not 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(y) % 4u) return fail(RFXQ_ERR_OTHER, "gemv: y is not 4-byte aligned");
+    const uint32_t units = w->ggml_type == RFXQ_TYPE_Q8_0 ? k / 32u : k / 64u;
+    uint32_t lpr_log2 = 0;
+    while (lpr_log2 < 6 && (units % (2u << lpr_log2)) == 0) lpr_log2++;
+    if (lpr_log2 < 2) lpr_log2 = 2;  // >= 4 lanes per row (units is always a multiple of 4 here)
+    if (units % (1u << lpr_log2)) {
+        // Q8_0 with k/32 not a multiple of 4: not supported by the lane mapping
+        return fail(RFXQ_ERR_OTHER, "gemv: %s in_features=%u needs k/32 %% 4 == 0", type_name(w->ggml_type), k);
+    }
+    const uint32_t rpi = 64u >> lpr_log2;
+    const uint32_t rows_iter = 4u * rpi;
+    const uint32_t iters_total = (n + rows_iter - 1u) / rows_iter;
+    const uint32_t target = env_u32("RFXQ_GEMV_WGS", 4u * (uint32_t)c->cus);
+    const uint32_t iters = std::max(1u, (iters_total + target - 1u) / target);
+    const uint32_t rows_per_wg = rows_iter * iters;
+    std::memset(d, 0, sizeof *d);
+    d->w = w->data;
+    d->x = x;
+    d->y = y;
+    d->k = k;
+    d->n = n;
+    d->type = w->ggml_type;
+    d->lpr_log2 = lpr_log2;
+    d->rows_per_wg = rows_per_wg;
+    *wgs = (n + rows_per_wg - 1u) / rows_per_wg;
+    *lds = k * 2u + k / 4u;
+    return RFXQ_OK;
+}
+
+int gemv_launch_descs(Ctx* c, GemvDesc* descs, uint32_t count, uint32_t total_wgs, uint32_t lds,
+                      const GemvDesc* table, hipStream_t stream) {
+    GemvArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.ndesc = count;
+    a.table = table;
+    if (count <= kGemvInline) std::copy(descs, descs + count, a.inl);
+    return launch(c->gemv, total_wgs, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+}
+
+// Up to kGemvInline GEMVs per launch, descriptors passed inline.
+int gemv_items(Ctx* c, const rfxq_gemv_item* items, uint32_t count, hipStream_t stream) {
+    for (uint32_t base = 0; base < count; base += kGemvInline) {
+        const uint32_t cnt = std::min(kGemvInline, count - base);
+        GemvDesc d[kGemvInline];
+        uint32_t total = 0, lds = 0;
+        for (uint32_t i = 0; i < cnt; i++) {
+            uint32_t wgs, l;
+            if (int rc = make_gemv_desc(c, items[base + i].x, items[base + i].w, items[base + i].y, &d[i], &wgs, &l))
+                return rc;
+            d[i].wg_begin = total;
+            total += wgs;
+            lds = std::max(lds, l);
+        }
+        if (int rc = gemv_launch_descs(c, d, cnt, total, lds, nullptr, stream)) return rc;
+    }
+    return RFXQ_OK;
+}
+
+// ------------------------------------------------------------------ MMQ planning
+
+uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
+
+struct GemmPlan {
+    uint32_t splits, sb_per_split, tiles_m, tiles_n;
+    uint64_t off_xds, off_part, total;
+};
+
+GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
+    GemmPlan p;
+    p.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
+    p.tiles_n = (n + kMmqBN - 1u) / kMmqBN;
+    const uint32_t nsb = k / 256u;
+    const uint32_t tiles = p.tiles_m * p.tiles_n;
+    uint32_t splits = 1;
+    const uint32_t cus = c ? (uint32_t)c->cus : 256u;
+    if (tiles < cus) splits = std::min(nsb, (2u * cus + tiles - 1u) / tiles);
+    splits = std::max(1u, env_u32("REFLEX_QUANT_MMA_SPLITS", splits));
+    splits = std::min(splits, nsb);
+    p.sb_per_split = (nsb + splits - 1u) / splits;
+    p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
+    p.off_xds = align256((uint64_t)rows * k);
+    p.off_part = p.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+    p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
+    return p;
+}
+
+uint32_t quant_grid(uint64_t blocks) {
+    const uint64_t waves = (blocks + 7u) / 8u;
+    return (uint32_t)std::min<uint64_t>(std::max<uint64_t>((waves + 3u) / 4u, 1u), 8192u);
+}
+
+int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
+                 int8_t* xq, uint32_t* xds, hipStream_t stream) {
+    struct {
+        const float* x;
+        uint32_t ldx, pad0;
+        const int32_t* src_rows;
+        uint32_t rows, k;
+        int8_t* xq;
+        uint32_t ldq, pad1;
+        uint32_t* xds;
+    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds};
+    return launch(c->quant, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
+                  "rfxq_quantize_q8_1 launch");
+}
+
+int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
+               bool dots, hipStream_t stream) {
+    MmqArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.ndesc = count;
+    a.table = table;
+    if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
+    hipFunction_t f = dots ? c->dots[type_index(ty)] : c->mmq[type_index(ty)];
+    return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
+}
+
+int check_mmq_weight(const rfxq_weight* w, const char* what) {
+    if (int rc = check_weight(w, what)) return rc;
+    if (w->in_features % 256u)
+        return fail(RFXQ_ERR_OTHER, "%s: in_features=%u (the MMQ path needs a multiple of 256)", what,
+                    w->in_features);
+    return RFXQ_OK;
+}
+
+int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+              hipStream_t stream) {
+    const uint32_t k = w->in_features, n = w->out_features;
+    const GemmPlan p = plan_gemm(c, rows, k, n);
+    if (!ws) {
+        if (int rc = ctx_workspace(c, p.total, &ws)) return rc;
+    } else if (ws_bytes < p.total) {
+        return fail(RFXQ_ERR_INVALID_INPUT, "gemm: workspace of %llu bytes, needs %llu",
+                    (unsigned long long)ws_bytes, (unsigned long long)p.total);
+    }
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    int8_t* xq = reinterpret_cast<int8_t*>(base);
+    uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
+    float* part = reinterpret_cast<float*>(base + p.off_part);
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, xq, xds, stream)) return rc;
+    MmqDesc d;
+    std::memset(&d, 0, sizeof d);
+    d.w = w->data;
+    d.xq = xq;
+    d.xds = xds;
+    d.y = p.splits > 1 ? part : y;
+    d.m = rows;
+    d.n = n;
+    d.k = k;
+    d.type = w->ggml_type;
+    d.ldq = k;
+    d.ldy = n;
+    d.tiles_m = p.tiles_m;
+    d.tiles_n = p.tiles_n;
+    d.splits = p.splits;
+    d.sb_per_split = p.sb_per_split;
+    const uint32_t wgs = p.tiles_m * p.tiles_n * p.splits;
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream)) return rc;
+    if (p.splits > 1) {
+        struct {
+            const float* ws;
+            float* y;
+            uint64_t n;
+            uint32_t splits, pad;
+        } a = {part, y, (uint64_t)rows * n, p.splits, 0};
+        const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * n + 255u) / 256u, 8192u);
+        if (int rc = launch(c->reduce, (uint32_t)blocks, 0, stream, &a, sizeof a, "rfxq_splitk_reduce launch"))
+            return rc;
+    }
+    return RFXQ_OK;
+}
+
+// ------------------------------------------------------------------ router (src/moe.rs:47-98)
+
+int route_top_k(const float* logits, uint32_t n, uint32_t k, bool normalize, uint32_t* idx, float* w) {
+    if (!logits || n == 0) return fail(RFXQ_ERR_OTHER, "route_top_k: logits must not be empty");
+    if (k == 0 || k > n) return fail(RFXQ_ERR_OTHER, "route_top_k: k (%u) must be in 1..=%u (logits.len())", k, n);
+    float maxl = -INFINITY;
+    for (uint32_t i = 0; i < n; i++) maxl = std::max(maxl, logits[i]);
+    std::vector<float> probs(n);
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < n; i++) {
+        probs[i] = std::exp(logits[i] - maxl);
+    }
+    for (uint32_t i = 0; i < n; i++) sum += probs[i];
+    if (!std::isfinite(sum) || sum <= 0.0f)
+        return fail(RFXQ_ERR_OTHER, "route_top_k: softmax sum is non-finite or non-positive (%g)", (double)sum);
+    for (uint32_t i = 0; i < n; i++) probs[i] = probs[i] / sum;
+    std::vector<uint32_t> order(n);
+    for (uint32_t i = 0; i < n; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
+        if (probs[a] > probs[b]) return true;
+        if (probs[a] < probs[b]) return false;
+        return a < b;
+    });
+    float top_sum = 0.0f;
+    for (uint32_t t = 0; t < k; t++) top_sum += probs[order[t]];
+    if (normalize && (!std::isfinite(top_sum) || top_sum <= 0.0f))
+        return fail(RFXQ_ERR_OTHER, "route_top_k: top-%u probability mass is non-finite or non-positive (%g)", k,
+                    (double)top_sum);
+    for (uint32_t t = 0; t < k; t++) {
+        idx[t] = order[t];
+        w[t] = normalize ? probs[order[t]] / top_sum : probs[order[t]];
+    }
+    return RFXQ_OK;
+}
+
+int expert_slice(const rfxq_weight* w, uint32_t e, rfxq_weight* out, const char* what) {
+    if (!w || !out) return fail(RFXQ_ERR_INVALID_INPUT, "%s: NULL weight", what);
+    if (w->expert_count == 0)
+        return fail(RFXQ_ERR_OTHER, "%s: expected 3-D per-expert tensor shape, got [%u, %u]", what, w->in_features,
+                    w->out_features);
+    if (e >= w->expert_count || w->len % w->expert_count != 0)
+        return fail(RFXQ_ERR_OTHER, "%s: expert %u of %u in a %llu-byte %s tensor", what, e, w->expert_count,
+                    (unsigned long long)w->len, type_name(w->ggml_type));
+    const uint64_t el = w->len / w->expert_count;
+    *out = *w;
+    out->expert_count = 0;
+    out->data = static_cast<const uint8_t*>(w->data) + (uint64_t)e * el;
+    out->len = el;
+    return RFXQ_OK;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+struct rfxq_gemv_plan {
+    int device;
+    GemvDesc* table;
+    std::vector<GemvDesc> host;
+    uint32_t total_wgs, lds;
+};
+
+extern "C" {
+
+const char* rfxq_last_error(void) { return g_code == RFXQ_OK ? nullptr : g_err.c_str(); }
+
+int rfxq_last_error_code(void) { return g_code; }
+
+int rfxq_init(int device) {
+    int n = 0;
+    HIPCHK(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_init: device %d of %d", device, n);
+    int prev = 0;
+    HIPCHK(hipGetDevice(&prev), "hipGetDevice");
+    HIPCHK(hipSetDevice(device), "hipSetDevice");
+    Ctx* c = nullptr;
+    const int rc = load_ctx(device, &c);
+    (void)hipSetDevice(prev);
+    return rc ? rc : ok();
+}
+
+int rfxq_block_dims(uint32_t ty, uint32_t* qk, uint32_t* bb) {
+    if (!qk || !bb) return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_block_dims: NULL output");
+    if (!block_dims(ty, qk, bb))
+        return fail(RFXQ_ERR_GGUF, "unknown ggml_type=%u: on-disk block size not known to this library", ty);
+    return ok();
+}
+
+int rfxq_dequantize(uint32_t ty, const void* blocks, uint64_t num_blocks, void* y, int f16_out, hipStream_t stream) {
+    if (!is_kernel_type(ty)) return fail(RFXQ_ERR_GGUF, "dequantize: no device dequantizer for ggml_type=%u", ty);
+    if (num_blocks == 0) return ok();
+    if (!blocks || !y) return fail(RFXQ_ERR_INVALID_INPUT, "dequantize: NULL pointer");
+    if (num_blocks > 0xFFFFFFFFull) return fail(RFXQ_ERR_OTHER, "dequantize: too many blocks");
+    if (reinterpret_cast<uintptr_t>(blocks) % 2u) return fail(RFXQ_ERR_OTHER, "dequantize: blocks not 2-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    const uint64_t groups = ty == RFXQ_TYPE_Q8_0 ? (num_blocks + 7u) / 8u : num_blocks;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(groups, 16384u);
+    struct {
+        const void* b;
+        void* y;
+        uint32_t n, pad;
+    } a = {blocks, y, (uint32_t)num_blocks, 0};
+    if (int rc = launch(c->deq[type_index(ty)][f16_out ? 1 : 0], grid, 0, stream, &a, sizeof a, "dequantize launch"))
+        return rc;
+    return ok();
+}
+
+int rfxq_gemv_to(const float* x, uint64_t x_len, const rfxq_weight* w, float* y, hipStream_t stream) {
+    if (int rc = check_weight(w, "gemv_to")) return rc;
+    if (x_len != w->in_features)
+        return fail(RFXQ_ERR_OTHER, "gemv_to: x.len()=%llu != in_features=%u", (unsigned long long)x_len,
+                    w->in_features);
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    rfxq_gemv_item it = {x, w, y};
+    if (int rc = gemv_items(c, &it, 1, stream)) return rc;
+    return ok();
+}
+
+int rfxq_gemv_rows(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y,
+                   hipStream_t stream) {
+    if (int rc = check_weight(w, "gemv_rows")) return rc;
+    if (rows == 0 || x_len != (uint64_t)rows * w->in_features)
+        return fail(RFXQ_ERR_OTHER, "gemv_rows: x.len()=%llu rows=%u in_features=%u (must be rows*in_features)",
+                    (unsigned long long)x_len, rows, w->in_features);
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    std::vector<rfxq_gemv_item> items(rows);
+    for (uint32_t r = 0; r < rows; r++)
+        items[r] = {x + (uint64_t)r * w->in_features, w, y + (uint64_t)r * w->out_features};
+    if (int rc = gemv_items(c, items.data(), rows, stream)) return rc;
+    return ok();
+}
+
+int rfxq_gemv_batch(const rfxq_gemv_item* items, uint32_t count, hipStream_t stream) {
+    if (count == 0) return ok();
+    if (!items) return fail(RFXQ_ERR_INVALID_INPUT, "gemv_batch: items is NULL");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    // validate everything before launching anything
+    for (uint32_t i = 0; i < count; i++) {
+        GemvDesc d;
+        uint32_t wgs, lds;
+        if (int rc = make_gemv_desc(c, items[i].x, items[i].w, items[i].y, &d, &wgs, &lds)) return rc;
+    }
+    if (int rc = gemv_items(c, items, count, stream)) return rc;
+    return ok();
+}
+
+int rfxq_gemv_plan_create(const rfxq_gemv_item* items, uint32_t count, int device, rfxq_gemv_plan** out) {
+    if (!out || !items || count == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemv_plan_create: empty plan");
+    *out = nullptr;
+    int prev = 0;
+    HIPCHK(hipGetDevice(&prev), "hipGetDevice");
+    HIPCHK(hipSetDevice(device), "hipSetDevice");
+    Ctx* c = nullptr;
+    int rc = load_ctx(device, &c);
+    auto plan = std::make_unique<rfxq_gemv_plan>();
+    plan->device = device;
+    plan->table = nullptr;
+    plan->total_wgs = 0;
+    plan->lds = 0;
+    plan->host.resize(count);
+    for (uint32_t i = 0; rc == RFXQ_OK && i < count; i++) {
+        uint32_t wgs, lds;
+        rc = make_gemv_desc(c, items[i].x, items[i].w, items[i].y, &plan->host[i], &wgs, &lds);
+        if (rc == RFXQ_OK) {
+            plan->host[i].wg_begin = plan->total_wgs;
+            plan->total_wgs += wgs;
+            plan->lds = std::max(plan->lds, lds);
+        }
+    }
+    if (rc == RFXQ_OK && count > kGemvInline) {
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&plan->table), sizeof(GemvDesc) * count);
+        if (e != hipSuccess) rc = fail(RFXQ_ERR_OUT_OF_MEMORY, "gemv_plan_create: %s", hipGetErrorString(e));
+        else {
+            e = hipMemcpy(plan->table, plan->host.data(), sizeof(GemvDesc) * count, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemv_plan_create upload: %s", hipGetErrorString(e));
+        }
+    }
+    (void)hipSetDevice(prev);
+    if (rc != RFXQ_OK) {
+        if (plan->table) (void)hipFree(plan->table);
+        return rc;
+    }
+    *out = plan.release();
+    return ok();
+}
+
+int rfxq_gemv_plan_run(const rfxq_gemv_plan* plan, hipStream_t stream) {
+    if (!plan) return fail(RFXQ_ERR_INVALID_INPUT, "gemv_plan_run: NULL plan");
+    Ctx* c;
+    if (int rc = load_ctx(plan->device, &c)) return rc;
+    GemvDesc tmp[kGemvInline];
+    const uint32_t n = (uint32_t)plan->host.size();
+    if (n <= kGemvInline) std::copy(plan->host.begin(), plan->host.end(), tmp);
+    if (int rc = gemv_launch_descs(c, tmp, n, plan->total_wgs, plan->lds, plan->table, stream)) return rc;
+    return ok();
+}
+
+void rfxq_gemv_plan_destroy(rfxq_gemv_plan* plan) {
+    if (!plan) return;
+    if (plan->table) (void)hipFree(plan->table);
+    delete plan;
+}
+
+int rfxq_quantize_q8_1(const float* x, uint32_t rows, uint32_t k, int8_t* xq, uint32_t* xds, hipStream_t stream) {
+    if (rows == 0) return ok();
+    if (!x || !xq || !xds) return fail(RFXQ_ERR_INVALID_INPUT, "quantize_q8_1: NULL pointer");
+    if (k == 0 || k % 32u) return fail(RFXQ_ERR_OTHER, "quantize_q8_1: k=%u (must be a multiple of 32)", k);
+    if (reinterpret_cast<uintptr_t>(x) % 16u || reinterpret_cast<uintptr_t>(xq) % 4u ||
+        reinterpret_cast<uintptr_t>(xds) % 4u)
+        return fail(RFXQ_ERR_OTHER, "quantize_q8_1: x must be 16-byte and xq/xds 4-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, xq, xds, stream)) return rc;
+    return ok();
+}
+
+uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows) {
+    if (!w || rows == 0) return 0;
+    Ctx* c = nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_ctx.find(dev);
+        if (it != g_ctx.end()) c = it->second.get();
+    }
+    return plan_gemm(c, rows, w->in_features, w->out_features).total;
+}
+
+int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
+              uint64_t workspace_bytes, hipStream_t stream) {
+    if (int rc = check_weight(w, "gemm")) return rc;
+    if (rows == 0 || x_len != (uint64_t)rows * w->in_features)
+        return fail(RFXQ_ERR_OTHER, "gemm: x.len()=%llu != rows*in_features=%llu", (unsigned long long)x_len,
+                    (unsigned long long)rows * w->in_features);
+    if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm: x or y is NULL");
+    if (rows == 1) return rfxq_gemv_to(x, x_len, w, y, stream);
+    if (env_u32("REFLEX_QUANT_MMA", 1) == 0) return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
+    if (int rc = check_mmq_weight(w, "gemm")) return rc;
+    if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemm: x is not 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    if (int rc = gemm_impl(c, x, w, rows, y, workspace, workspace_bytes, stream)) return rc;
+    return ok();
+}
+
+int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, const rfxq_weight* w, int32_t* dots,
+                        hipStream_t stream) {
+    if (int rc = check_mmq_weight(w, "mmq_block_dots")) return rc;
+    if (!xq || !xds || !dots || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "mmq_block_dots: bad arguments");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    MmqDesc d;
+    std::memset(&d, 0, sizeof d);
+    d.w = w->data;
+    d.xq = xq;
+    d.xds = xds;
+    d.m = rows;
+    d.n = w->out_features;
+    d.k = w->in_features;
+    d.type = w->ggml_type;
+    d.ldq = w->in_features;
+    d.ldy = w->out_features;
+    d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
+    d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
+    d.splits = 1;
+    d.sb_per_split = d.k / 256u;
+    d.dots_out = dots;
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, d.tiles_m * d.tiles_n, true, stream)) return rc;
+    return ok();
+}
+
+int rfxq_route_top_k(const float* logits, uint32_t n, uint32_t k, int normalize, uint32_t* expert, float* weight) {
+    if (!expert || !weight) return fail(RFXQ_ERR_INVALID_INPUT, "route_top_k: NULL output");
+    if (int rc = route_top_k(logits, n, k, normalize != 0, expert, weight)) return rc;
+    return ok();
+}
+
+int rfxq_quant_expert_weight(const rfxq_weight* w, uint32_t expert, rfxq_weight* out) {
+    if (int rc = expert_slice(w, expert, out, "quant_expert_weight")) return rc;
+    return ok();
+}
+
+int rfxq_expert_gemv(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t expert, float* y,
+                     hipStream_t stream) {
+    rfxq_weight ew;
+    if (int rc = expert_slice(w, expert, &ew, "expert_gemv")) return rc;
+    return rfxq_gemv_to(x, x_len, &ew, y, stream);
+}
+
+int rfxq_expert_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t expert, uint32_t rows, float* y,
+                     void* workspace, uint64_t workspace_bytes, hipStream_t stream) {
+    rfxq_weight ew;
+    if (int rc = expert_slice(w, expert, &ew, "expert_gemm")) return rc;
+    return rfxq_gemm(x, x_len, &ew, rows, y, workspace, workspace_bytes, stream);
+}
+
+int rfxq_moe_gather(const float* src, const uint32_t* perm_row, float* dst, uint32_t num, uint32_t hidden,
+                    hipStream_t stream) {
+    if (num == 0 || hidden == 0) return ok();
+    if (!src || !perm_row || !dst) return fail(RFXQ_ERR_INVALID_INPUT, "moe_gather: NULL pointer");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    struct {
+        const float* s;
+        const uint32_t* p;
+        float* d;
+        uint32_t num, hidden;
+    } a = {src, perm_row, dst, num, hidden};
+    const uint64_t blocks = std::min<uint64_t>(((uint64_t)num * hidden + 255u) / 256u, 16384u);
+    if (int rc = launch(c->gather, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_gather launch")) return rc;
+    return ok();
+}
+
+int rfxq_moe_scatter_add(const float* src, const uint32_t* dest_row, const float* weight, float* dst, uint32_t num,
+                         uint32_t hidden, hipStream_t stream) {
+    if (num == 0 || hidden == 0) return ok();
+    if (!src || !dest_row || !weight || !dst) return fail(RFXQ_ERR_INVALID_INPUT, "moe_scatter_add: NULL pointer");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    struct {
+        const float* s;
+        const uint32_t* r;
+        const float* w;
+        float* d;
+        uint32_t num, hidden;
+    } a = {src, dest_row, weight, dst, num, hidden};
+    const uint64_t blocks = std::min<uint64_t>(((uint64_t)num * hidden + 255u) / 256u, 16384u);
+    if (int rc = launch(c->scatter, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_scatter_add launch")) return rc;
+    return ok();
+}
+
+int rfxq_silu_and_mul(const float* gate, const float* up, float* out, uint64_t n, hipStream_t stream) {
+    if (n == 0) return ok();
+    if (!gate || !up || !out) return fail(RFXQ_ERR_INVALID_INPUT, "silu_and_mul: NULL pointer");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    struct {
+        const float* g;
+        const float* u;
+        float* o;
+        uint64_t n;
+    } a = {gate, up, out, n};
+    const uint64_t blocks = std::min<uint64_t>((n + 255u) / 256u, 16384u);
+    if (int rc = launch(c->silu, (uint32_t)blocks, 0, stream, &a, sizeof a, "silu_and_mul launch")) return rc;
+    return ok();
+}
+
+int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits_host,
+                         uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
+                         const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
+                         hipStream_t stream) {
+    if (!x || !out || !router_logits_host || !gate || !up || !down)
+        return fail(RFXQ_ERR_INVALID_INPUT, "moe_ffn_grouped: NULL argument");
+    if (rows == 0) return ok();
+    if (gate->expert_count != expert_count || up->expert_count != expert_count || down->expert_count != expert_count)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: expert tensors must have expert_count=%u", expert_count);
+    if (gate->in_features != hidden || up->in_features != hidden || down->out_features != hidden ||
+        gate->out_features != up->out_features || down->in_features != gate->out_features)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: shapes gate [%u,%u] up [%u,%u] down [%u,%u] hidden %u",
+                    gate->in_features, gate->out_features, up->in_features, up->out_features, down->in_features,
+                    down->out_features, hidden);
+    const uint32_t ffn = gate->out_features;
+    rfxq_weight g0, u0, d0;
+    if (int rc = expert_slice(gate, 0, &g0, "moe_ffn_grouped gate")) return rc;
+    if (int rc = expert_slice(up, 0, &u0, "moe_ffn_grouped up")) return rc;
+    if (int rc = expert_slice(down, 0, &d0, "moe_ffn_grouped down")) return rc;
+    if (int rc = check_mmq_weight(&g0, "moe_ffn_grouped gate")) return rc;
+    if (int rc = check_mmq_weight(&u0, "moe_ffn_grouped up")) return rc;
+    if (int rc = check_mmq_weight(&d0, "moe_ffn_grouped down")) return rc;
+    if (gate->ggml_type != up->ggml_type)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: gate and up must share a type");
+    if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: x not 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+
+    // host routing and grouping (dense.rs:1523-1530)
+    std::vector<std::vector<std::pair<uint32_t, float>>> groups(expert_count);
+    std::vector<uint32_t> idx(top_k);
+    std::vector<float> wts(top_k);
+    for (uint32_t r = 0; r < rows; r++) {
+        if (int rc = route_top_k(router_logits_host + (uint64_t)r * expert_count, expert_count, top_k,
+                                 normalize != 0, idx.data(), wts.data()))
+            return rc;
+        for (uint32_t t = 0; t < top_k; t++) groups[idx[t]].push_back({r, wts[t] * weight_scale});
+    }
+    const uint32_t P = rows * top_k;
+    std::vector<int32_t> pair_row(P), comb_idx((uint64_t)rows * top_k, -1);
+    std::vector<float> comb_w((uint64_t)rows * top_k, 0.0f);
+    std::vector<uint32_t> fill(rows, 0), off(expert_count + 1, 0);
+    uint32_t p = 0;
+    for (uint32_t e = 0; e < expert_count; e++) {
+        off[e] = p;
+        for (auto& rw : groups[e]) {
+            pair_row[p] = (int32_t)rw.first;
+            const uint32_t slot = fill[rw.first]++;
+            comb_idx[(uint64_t)rw.first * top_k + slot] = (int32_t)p;
+            comb_w[(uint64_t)rw.first * top_k + slot] = rw.second;
+            p++;
+        }
+    }
+    off[expert_count] = p;
+
+    // workspace layout
+    const uint64_t o_xq = 0;
+    const uint64_t o_xds = o_xq + align256((uint64_t)rows * hidden);
+    const uint64_t o_gate = o_xds + align256((uint64_t)rows * (hidden / 32u) * 4u);
+    const uint64_t o_up = o_gate + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_xq2 = o_up + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_xds2 = o_xq2 + align256((uint64_t)P * ffn);
+    const uint64_t o_down = o_xds2 + align256((uint64_t)P * (ffn / 32u) * 4u);
+    const uint64_t o_tab = o_down + align256((uint64_t)P * hidden * 4u);
+    // tables: pair_row[P], comb_idx[rows*k], comb_w[rows*k], descs (up to 3E)
+    const uint64_t o_pr = o_tab;
+    const uint64_t o_ci = o_pr + align256((uint64_t)P * 4u);
+    const uint64_t o_cw = o_ci + align256((uint64_t)rows * top_k * 4u);
+    const uint64_t o_desc = o_cw + align256((uint64_t)rows * top_k * 4u);
+    const uint64_t total = o_desc + align256((uint64_t)3u * expert_count * sizeof(MmqDesc));
+    void* ws;
+    if (int rc = ctx_workspace(c, total, &ws)) return rc;
+    uint8_t* B = static_cast<uint8_t*>(ws);
+    int8_t* xq = reinterpret_cast<int8_t*>(B + o_xq);
+    uint32_t* xds = reinterpret_cast<uint32_t*>(B + o_xds);
+    float* gout = reinterpret_cast<float*>(B + o_gate);
+    float* uout = reinterpret_cast<float*>(B + o_up);
+    int8_t* xq2 = reinterpret_cast<int8_t*>(B + o_xq2);
+    uint32_t* xds2 = reinterpret_cast<uint32_t*>(B + o_xds2);
+    float* dout = reinterpret_cast<float*>(B + o_down);
+    int32_t* d_pr = reinterpret_cast<int32_t*>(B + o_pr);
+    int32_t* d_ci = reinterpret_cast<int32_t*>(B + o_ci);
+    float* d_cw = reinterpret_cast<float*>(B + o_cw);
+    MmqDesc* d_desc = reinterpret_cast<MmqDesc*>(B + o_desc);
+
+    // descriptor tables: [gate+up descs][down descs]
+    std::vector<MmqDesc> descs;
+    uint32_t wg_gu = 0;
+    auto add = [&](const rfxq_weight* w, uint32_t e, const int8_t* q, const uint32_t* s, const int32_t* rws,
+                   uint32_t m, uint32_t ldq, float* y, uint32_t n, uint32_t& wg) {
+        rfxq_weight ew;
+        expert_slice(w, e, &ew, "moe_ffn_grouped");
+        MmqDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.w = ew.data;
+        d.xq = q;
+        d.xds = s;
+        d.rows = rws;
+        d.y = y;
+        d.m = m;
+        d.n = n;
+        d.k = ew.in_features;
+        d.type = ew.ggml_type;
+        d.ldq = ldq;
+        d.ldy = n;
+        d.tiles_m = (m + kMmqBM - 1u) / kMmqBM;
+        d.tiles_n = (n + kMmqBN - 1u) / kMmqBN;
+        d.splits = 1;
+        d.sb_per_split = d.k / 256u;
+        d.wg_begin = wg;
+        wg += d.tiles_m * d.tiles_n;
+        descs.push_back(d);
+    };
+    for (uint32_t e = 0; e < expert_count; e++) {
+        const uint32_t m = off[e + 1] - off[e];
+        if (!m) continue;
+        add(gate, e, xq, xds, d_pr + off[e], m, hidden, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+        add(up, e, xq, xds, d_pr + off[e], m, hidden, uout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+    }
+    const uint32_t n_gu = (uint32_t)descs.size();
+    uint32_t wg_dn = 0;
+    for (uint32_t e = 0; e < expert_count; e++) {
+        const uint32_t m = off[e + 1] - off[e];
+        if (!m) continue;
+        add(down, e, xq2 + (uint64_t)off[e] * ffn, xds2 + (uint64_t)off[e] * (ffn / 32u), nullptr, m, ffn,
+            dout + (uint64_t)off[e] * hidden, hidden, wg_dn);
+    }
+    const uint32_t n_dn = (uint32_t)descs.size() - n_gu;
+
+    // one upload of all tables (stream-ordered; the reference copies per expert)
+    std::vector<uint8_t> host(total - o_tab, 0);
+    std::memcpy(host.data() + (o_pr - o_tab), pair_row.data(), (size_t)P * 4u);
+    std::memcpy(host.data() + (o_ci - o_tab), comb_idx.data(), comb_idx.size() * 4u);
+    std::memcpy(host.data() + (o_cw - o_tab), comb_w.data(), comb_w.size() * 4u);
+    std::memcpy(host.data() + (o_desc - o_tab), descs.data(), descs.size() * sizeof(MmqDesc));
+    HIPCHK(hipMemcpyAsync(B + o_tab, host.data(), host.size(), hipMemcpyHostToDevice, stream),
+           "moe_ffn_grouped table upload");
+
+    if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
+    if (n_gu) {
+        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream)) return rc;
+    }
+    if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
+    if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
+    if (n_dn) {
+        if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream))
+            return rc;
+    }
+    {
+        struct {
+            const float* po;
+            const int32_t* idx;
+            const float* w;
+            float* out;
+            uint32_t tokens, k, hidden, pad;
+        } a = {dout, d_ci, d_cw, out, rows, top_k, hidden, 0};
+        const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
+        if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
+    }
+    // The host staging vector dies with this frame: make sure the copy is done.
+    HIPCHK(hipStreamSynchronize(stream), "moe_ffn_grouped sync");
+    return ok();
+}
+
+}  // extern "C"

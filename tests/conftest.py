@@ -1,0 +1,33 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    """The CPU oracle (test infrastructure): built on first use."""
+    import oracle
+
+    oracle.lib()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def rq():
+    """The product package on the GPU: fails loudly if the library or device is missing."""
+    import torch
+
+    import reflex_amd
+
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    reflex_amd.init(0)
+    return reflex_amd

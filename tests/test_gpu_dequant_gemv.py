@@ -1,0 +1,179 @@
+"""GPU parity: device dequantization (bit-exact with src/dequant.rs) and the
+decode GEMV (within tolerance of dequant + f64 host matmul), through the C ABI.
+
+Tolerances: the north star's bound is 1e-3 max error normalised by the output
+row's L2 norm; the GEMV (f16-rounded activations, f32 accumulation) is held to
+1e-4 on that metric and to the reference's own rel_max_diff < 1e-3
+(quant_resident_tests.rs:6-10)."""
+import numpy as np
+import pytest
+import torch
+
+from reflex_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4K, Q6K = 8, 12, 14
+DEV = "cuda:0"
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _weight(rq, ty, blocks, n, k, offset=0):
+    """A Weight whose blocks sit at `offset` bytes into a fresh device arena."""
+    buf = torch.zeros(blocks.size + offset + 64, dtype=torch.uint8, device=DEV)
+    buf[offset:offset + blocks.size].copy_(_dev(blocks))
+    return rq.Weight(rq.GgmlType(ty), buf, [k, n], offset=offset, len=blocks.size)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("gen", ["reference", "baseline"])
+def test_dequant_bit_exact(rq, orc, ty, gen):
+    k, n = 1024, 96
+    w = orc.synthetic(ty, k, n, 21) if gen == "reference" else synth.weights(ty, n, k, 77)
+    want = orc.dequantize(ty, w, n * k)
+    blocks = _dev(w)
+    got32 = rq.dequantize(ty, blocks, n * k, torch.float32).cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), want.view(np.uint32))
+    got16 = rq.dequantize(ty, blocks, n * k, torch.float16).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("ty", [Q6K, Q8_0])
+def test_dequant_unaligned_blocks(rq, orc, ty):
+    """Q6_K / Q8_0 blocks are only 2-byte aligned (gemv_q4k.cu:60-63)."""
+    k, n = 512, 7
+    w = orc.synthetic(ty, k, n, 5)
+    buf = torch.zeros(w.size + 8, dtype=torch.uint8, device=DEV)
+    buf[2:2 + w.size].copy_(_dev(w))
+    got = rq.dequantize(ty, buf[2:2 + w.size], n * k).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), orc.dequantize(ty, w, n * k).view(np.uint32))
+
+
+def test_dequant_committed_fixtures(rq):
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "fixtures.npz"))
+    for ty, name in [(Q4K, "q4k"), (Q6K, "q6k"), (Q8_0, "q8_0")]:
+        n, k = f[f"{name}_shape"]
+        got = rq.dequantize(ty, _dev(f[f"{name}_w"]), n * k).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), f[f"{name}_deq"].view(np.uint32))
+
+
+# ------------------------------------------------------------------ GEMV
+
+def _check_gemv(rq, orc, ty, n, k, w_np, x_np, offset=0, tol=1e-4):
+    w = _weight(rq, ty, w_np, n, k, offset)
+    x = _dev(x_np)
+    y = rq.gemv(x, w).cpu().numpy()
+    ref = orc.reference_gemm(ty, w_np, n, k, x_np)[0]
+    e = orc.rel_err_row_l2(y[None], ref[None])
+    assert e < tol, f"type {ty} [{n}x{k}] row-L2 error {e}"
+    assert orc.rel_max_diff(y, ref) < 1e-3
+    return y
+
+
+CONFIG2 = [(name, ty, n, k) for name, ty, n, k in synth.QWEN3_06B_LAYER]
+CONFIG4 = [(name, ty, n, k) for name, ty, n, k in synth.QWEN3_8B_LAYER] + [synth.LM_HEAD]
+
+
+@pytest.mark.parametrize("name,ty,n,k", CONFIG2, ids=[c[0] for c in CONFIG2])
+def test_gemv_qwen3_06b_shapes(rq, orc, name, ty, n, k):
+    seed = synth.seed_for(2, 0, [c[0] for c in CONFIG2].index(name))
+    _check_gemv(rq, orc, ty, n, k, synth.weights(ty, n, k, seed), synth.activations(k, seed + 1000))
+
+
+@pytest.mark.parametrize("name,ty,n,k", CONFIG4, ids=[c[0] for c in CONFIG4])
+def test_gemv_8b_shapes(rq, orc, name, ty, n, k):
+    seed = synth.seed_for(4, 0, [c[0] for c in CONFIG4].index(name))
+    _check_gemv(rq, orc, ty, n, k, synth.weights(ty, n, k, seed), synth.activations(k, seed + 1000))
+
+
+def test_gemv_config1_q8_0(rq, orc):
+    seed = synth.seed_for(1)
+    _check_gemv(rq, orc, Q8_0, 1024, 1024, synth.weights(Q8_0, 1024, 1024, seed), synth.activations(1024, seed + 1))
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("n,k", [(1, 256), (3, 256), (5, 768), (37, 512), (130, 1536), (17, 3072), (9, 14336)])
+def test_gemv_edge_shapes_reference_generators(rq, orc, ty, n, k):
+    """Reference generators: Q6_K d zero / negative, Q8_0 d zero / subnormal / signed."""
+    w = orc.synthetic(ty, k, n, 1000 + n)
+    x = orc.activations(k, 7 + n)
+    _check_gemv(rq, orc, ty, n, k, w, x)
+
+
+@pytest.mark.parametrize("ty", [Q6K, Q8_0])
+def test_gemv_two_byte_aligned_weights(rq, orc, ty):
+    n, k = 33, 1024
+    w = orc.synthetic(ty, k, n, 99)
+    _check_gemv(rq, orc, ty, n, k, w, orc.activations(k, 3), offset=2)
+
+
+def test_gemv_zero_activations_and_one_hot(rq, orc):
+    """Closed forms: x = 0 gives y = 0; x = e_j gives column j of the dequantized weight."""
+    n, k = 64, 1024
+    for ty in (Q4K, Q6K, Q8_0):
+        w_np = orc.synthetic(ty, k, n, 4)
+        w = _weight(rq, ty, w_np, n, k)
+        y0 = rq.gemv(torch.zeros(k, device=DEV), w).cpu().numpy()
+        assert np.all(y0 == 0)
+        deq = orc.dequant_matrix(ty, w_np, n, k)
+        for j in (0, 31, 32, 100, 1023):
+            x = torch.zeros(k, device=DEV)
+            x[j] = 1.0
+            y = rq.gemv(x, w).cpu().numpy()
+            # exact weights, but the kernel removes the f16 magic offset (1024 * scale) in f32
+            assert np.allclose(y, deq[:, j], rtol=1e-4, atol=1e-4 * np.abs(deq).max()), (ty, j)
+
+
+def test_gemv_rows_matches_single_row_bitwise(rq, orc):
+    n, k = 200, 2048
+    for ty in (Q4K, Q6K, Q8_0):
+        w_np = orc.synthetic(ty, k, n, 8)
+        w = _weight(rq, ty, w_np, n, k)
+        xs = orc.activations(13 * k, 3)
+        x = _dev(xs)
+        y = rq.gemv_q4k(x, w, 13).cpu().numpy().reshape(13, n)
+        for r in range(13):
+            yr = rq.gemv(_dev(xs[r * k:(r + 1) * k]), w).cpu().numpy()
+            assert np.array_equal(y[r], yr)
+
+
+def test_gemv_batch_and_plan_match_single_calls(rq, orc):
+    """A fused launch of mixed types (q/k/v with Q6_K v) equals separate calls bit for bit."""
+    items, singles = [], []
+    for i, (name, ty, n, k) in enumerate(CONFIG2 * 2):
+        w_np = synth.weights(ty, n, k, 500 + i)
+        w = _weight(rq, ty, w_np, n, k)
+        x = _dev(synth.activations(k, 900 + i))
+        items.append((x, w, torch.empty(n, device=DEV)))
+        singles.append(rq.gemv(x, w).cpu().numpy())
+    rq.gemv_batch(items[:3])
+    for (x, w, y), s in zip(items[:3], singles[:3]):
+        assert np.array_equal(y.cpu().numpy(), s)
+    plan = rq.GemvPlan(items)
+    for y in (it[2] for it in items):
+        y.fill_(float("nan"))
+    plan.run()
+    plan.run()
+    for (x, w, y), s in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), s)
+
+
+def test_gemv_deterministic(rq):
+    n, k = 3072, 1024
+    w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 3), n, k)
+    x = _dev(synth.activations(k, 4))
+    a = rq.gemv(x, w).cpu().numpy()
+    b = rq.gemv(x, w).cpu().numpy()
+    assert np.array_equal(a, b)
+
+
+def test_gemv_errors_raise(rq):
+    w = _weight(rq, Q4K, synth.weights(Q4K, 8, 512, 3), 8, 512)
+    with pytest.raises(rq.ReflexError):
+        rq.gemv(torch.zeros(511, device=DEV), w)

@@ -1,0 +1,174 @@
+"""GPU parity of the prefill path: Q8_1 activation quantization (bit-exact),
+the MMQ kernel's per-32 int32 dots (bit-exact with the CPU emulation), and the
+GEMM output within the north star's 1e-3 bound (max error normalised by the
+output row's L2 norm) of dequant.rs + f64 host matmul.
+
+Tolerance note: per-32 int8 quantization of N(0,1) activations has a relative
+RMS error of about 4.8e-3 per element, so the expected worst row is about
+6-8e-4 on this metric at N = 1024 (the margin the bound was set with)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from reflex_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4K, Q6K = 8, 12, 14
+DEV = "cuda:0"
+TOL = 1e-3
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _weight(rq, ty, blocks, n, k):
+    return rq.Weight(rq.GgmlType(ty), _dev(blocks), [k, n])
+
+
+# ------------------------------------------------------------------ quantizer
+
+def test_quantize_q8_1_bit_exact(rq, orc):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((97, 1024)).astype(np.float32)
+    x[0, :32] = 0
+    x[1, :64] = np.repeat(np.float32([0.5, -0.5, 1.5, -2.5]), 16)    # exact halves of d*q
+    x[2, :32] = np.float32(1e-30)
+    x[3, 32:64] = rng.standard_normal(32).astype(np.float32) * 1e4
+    xq, xds = rq.quantize_q8_1(_dev(x), 97, 1024)
+    qs, ds = orc.quantize_q8_1(x)
+    assert np.array_equal(xq.cpu().numpy(), qs)
+    d = xds.cpu().numpy().view(np.uint32)
+    assert np.array_equal((d & 0xFFFF).astype(np.uint16), ds[..., 0])
+    assert np.array_equal((d >> 16).astype(np.uint16), ds[..., 1])
+
+
+def test_quantize_committed_fixtures(rq):
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "fixtures.npz"))
+    m, k = f["x"].shape
+    xq, xds = rq.quantize_q8_1(_dev(f["x"]), m, k)
+    assert np.array_equal(xq.cpu().numpy(), f["xq"])
+    d = xds.cpu().numpy().view(np.uint32)
+    assert np.array_equal((d & 0xFFFF).astype(np.uint16), f["xds"][..., 0])
+
+
+# ------------------------------------------------------------------ int32 block dots
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("m,n,k", [(3, 8, 512), (37, 70, 512), (130, 129, 768), (1, 300, 256)])
+def test_mmq_block_dots_bit_exact(rq, orc, ty, m, n, k):
+    w_np = orc.synthetic(ty, k, n, 31 + m)
+    x = orc.activations(m * k, 5 + n).reshape(m, k) * 3
+    xq, xds = rq.quantize_q8_1(_dev(x), m, k)
+    w = _weight(rq, ty, w_np, n, k)
+    got = rq.mmq_block_dots(xq, xds, m, w).cpu().numpy()
+    want = orc.block_dots(ty, w_np, n, k, xq.cpu().numpy())
+    assert np.array_equal(got, want)
+
+
+def test_mmq_block_dots_committed_fixtures(rq):
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "fixtures.npz"))
+    m, k = f["x"].shape
+    xq, xds = rq.quantize_q8_1(_dev(f["x"]), m, k)
+    for ty, name in [(Q4K, "q4k"), (Q6K, "q6k"), (Q8_0, "q8_0")]:
+        n, kk = f[f"{name}_shape"]
+        w = _weight(rq, ty, f[f"{name}_w"], n, kk)
+        got = rq.mmq_block_dots(xq, xds, m, w).cpu().numpy()
+        assert np.array_equal(got, f[f"{name}_dots"]), name
+
+
+# ------------------------------------------------------------------ GEMM
+
+def _check_gemm(rq, orc, ty, m, n, k, w_np, x_np, rows_checked=None):
+    w = _weight(rq, ty, w_np, n, k)
+    y = rq.gemm(_dev(x_np), w, m).cpu().numpy().reshape(m, n)
+    rows = np.arange(m) if rows_checked is None else rows_checked
+    ref = orc.reference_gemm(ty, w_np, n, k, x_np.reshape(m, k)[rows])
+    e = orc.rel_err_row_l2(y[rows], ref)
+    assert e < TOL, f"type {ty} M={m} [{n}x{k}] row-L2 error {e}"
+    return y, e
+
+
+@pytest.mark.parametrize("name,ty,n,k", synth.QWEN3_06B_LAYER, ids=[c[0] for c in synth.QWEN3_06B_LAYER])
+def test_gemm_prefill_qwen3_06b(rq, orc, name, ty, n, k):
+    seed = synth.seed_for(3, 0, [c[0] for c in synth.QWEN3_06B_LAYER].index(name))
+    x = synth.activations(512 * k, seed + 1000).reshape(512, k)
+    _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x)
+
+
+@pytest.mark.parametrize("name,ty,n,k", synth.QWEN3_8B_LAYER, ids=[c[0] for c in synth.QWEN3_8B_LAYER])
+def test_gemm_prefill_8b_sampled_rows(rq, orc, name, ty, n, k):
+    """Full M=512 on the GPU; 24 sampled rows checked (rows are independent)."""
+    seed = synth.seed_for(4, 1, [c[0] for c in synth.QWEN3_8B_LAYER].index(name))
+    x = synth.activations(512 * k, seed + 1000).reshape(512, k)
+    rows = np.random.default_rng(seed).choice(512, 24, replace=False)
+    _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x, rows)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("m", [2, 7, 33, 129, 513])
+def test_gemm_row_counts(rq, orc, ty, m):
+    n, k = 200, 1024
+    w_np = orc.synthetic(ty, k, n, 60 + m)
+    x = synth.activations(m * k, 61 + m).reshape(m, k)
+    _check_gemm(rq, orc, ty, m, n, k, w_np, x)
+
+
+def test_gemm_rows_independent_and_deterministic(rq, orc):
+    """Row r of the output depends only on row r of x, and repeats give identical bits."""
+    n, k = 1024, 2048
+    w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 9), n, k)
+    x = synth.activations(300 * k, 10).reshape(300, k)
+    ya = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
+    yb = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
+    assert np.array_equal(ya, yb)
+    yc = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
+    # same tile decomposition along K -> same bits for the shared rows
+    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
+    try:
+        y1 = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
+        y2 = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
+    finally:
+        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
+    assert np.array_equal(y1[:130], y2)
+    ref = orc.reference_gemm(Q4K, synth.weights(Q4K, n, k, 9), n, k, x[:130])
+    assert orc.rel_err_row_l2(yc, ref) < TOL
+
+
+def test_gemm_split_k_matches_unsplit(rq, orc):
+    n, k = 1024, 4096
+    w_np = synth.weights(Q4K, n, k, 12)
+    w = _weight(rq, Q4K, w_np, n, k)
+    x = synth.activations(64 * k, 13).reshape(64, k)
+    outs = []
+    for s in ("1", "4", "16"):
+        os.environ["REFLEX_QUANT_MMA_SPLITS"] = s
+        try:
+            outs.append(rq.gemm(_dev(x), w, 64).cpu().numpy().reshape(64, n))
+        finally:
+            del os.environ["REFLEX_QUANT_MMA_SPLITS"]
+    scale = np.abs(outs[0]).max()
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) <= 1e-5 * scale
+
+
+def test_gemm_one_row_is_decode_gemv(rq):
+    n, k = 512, 1024
+    w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 14), n, k)
+    x = _dev(synth.activations(k, 15))
+    assert np.array_equal(rq.gemm(x, w, 1).cpu().numpy(), rq.gemv(x, w).cpu().numpy())
+
+
+def test_gemm_caller_workspace(rq, orc):
+    n, k, m = 256, 1024, 40
+    w_np = synth.weights(Q6K, n, k, 16)
+    w = _weight(rq, Q6K, w_np, n, k)
+    x = synth.activations(m * k, 17).reshape(m, k)
+    ws = torch.empty(rq.gemm_workspace_size(w, m), dtype=torch.uint8, device=DEV)
+    y = rq.gemm(_dev(x), w, m, workspace=ws).cpu().numpy().reshape(m, n)
+    assert orc.rel_err_row_l2(y, orc.reference_gemm(Q6K, w_np, n, k, x)) < TOL
+    with pytest.raises(rq.ReflexError):
+        rq.gemm(_dev(x), w, m, workspace=ws[:100])
