@@ -218,6 +218,54 @@ def cpu_dequant_matmul(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray, th
     return y
 
 
+def q4k_scale_min_np(w: np.ndarray, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """Vectorised get_scale_min_k4 (dequant.rs:39-47) over every block: (sc, m) as
+    int arrays [n, k/32] (checked against the C function in tests)."""
+    b = np.ascontiguousarray(w, dtype=np.uint8).reshape(n, k // 256, 144)
+    q = b[:, :, 4:16].astype(np.int64)
+    sc = np.zeros((n, k // 256, 8), dtype=np.int64)
+    m = np.zeros((n, k // 256, 8), dtype=np.int64)
+    for j in range(4):
+        sc[..., j] = q[..., j] & 63
+        m[..., j] = q[..., j + 4] & 63
+    for j in range(4, 8):
+        sc[..., j] = (q[..., j + 4] & 0xF) | ((q[..., j - 4] >> 6) << 4)
+        m[..., j] = (q[..., j + 4] >> 4) | ((q[..., j] >> 6) << 4)
+    return sc.reshape(n, k // 32), m.reshape(n, k // 32)
+
+
+def mmq_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) -> np.ndarray:
+    """The MMQ algorithm in exact (f64) arithmetic on the quantized activations:
+    x_hat = f16(d) * q per 32-block (quantize_q8_1); for Q4_K the weights split as
+    w = d*sc*(q - 8) + c with c = 8*d*sc - dmin*m, and the constant part c takes
+    the block's activation sum d * s (s = f16(sum(x)/d)); Q6_K / Q8_0 use
+    x_hat @ W^T. Any difference
+    between the kernel and this is the kernel's own rounding."""
+    x2 = np.ascontiguousarray(x.reshape(-1, k), dtype=np.float32)
+    qs, ds = quantize_q8_1(x2)
+    d = ds[..., 0].view(np.float16).astype(np.float64)
+    xh = (qs.reshape(x2.shape[0], -1, 32).astype(np.float64) * d[..., None]).reshape(x2.shape[0], k)
+    W = dequant_matrix(ty, w, n, k).astype(np.float64)
+    if ty != Q4K:
+        return (xh @ W.T).astype(np.float32)
+    sc, m = q4k_scale_min_np(w, n, k)
+    b = np.ascontiguousarray(w, dtype=np.uint8).reshape(n, k // 256, 144)
+    dd = b[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    dm = b[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float32)
+    dsc = (np.repeat(dd, 8, axis=1) * sc.astype(np.float32)).astype(np.float64)   # f32 product, as dequant.rs
+    dmw = (np.repeat(dm, 8, axis=1) * m.astype(np.float32)).astype(np.float64)
+    c = 8.0 * dsc - dmw
+    # centered part dsc * (q - 8), with the nibbles q read from the block bytes
+    qb = b[:, :, 16:144]
+    nib = np.empty((n, k // 256, 256), dtype=np.int64)
+    for g in range(4):
+        nib[:, :, 64 * g:64 * g + 32] = qb[:, :, 32 * g:32 * g + 32] & 15
+        nib[:, :, 64 * g + 32:64 * g + 64] = qb[:, :, 32 * g:32 * g + 32] >> 4
+    wc = np.repeat(dsc, 32, axis=1) * (nib.reshape(n, k) - 8)
+    sx = ds[..., 1].view(np.float16).astype(np.float64) * d  # [rows, k/32]: d * f16(sum(x)/d)
+    return (xh @ wc.T + sx @ c.T).astype(np.float32)
+
+
 def rel_max_diff(a: np.ndarray, b: np.ndarray) -> float:
     """quant_resident_tests.rs:6-10: max|a-b| / max|b|."""
     scale = max(float(np.max(np.abs(b))), 1e-30)

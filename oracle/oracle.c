@@ -21,8 +21,9 @@
  *     (ggml-quants.c: d = amax/127, id = 1/d, q = roundf(x*id), s = d*sum(q)).
  *     The reference has no activation quantizer; this is the north star's spec.
  *   - block_dots: the per-32 int32 dot products sum(qa*qw) that the MMQ kernel's
- *     int8 MFMA produces, qw being the weight's integer code (Q4_K nibble,
- *     Q6_K q6-32, Q8_0 int8) exactly as the dequant formulas above read it.
+ *     int8 MFMA produces, qw being the weight's centered integer code (Q4_K
+ *     nibble - 8, Q6_K (q6-32) times its 16-run scale, Q8_0 int8) as read
+ *     from the same bytes the dequant formulas above read.
  *
  * Build with -ffp-contract=off so `d1 * q - m1` rounds twice, as Rust does.
  */
@@ -206,7 +207,9 @@ long oracle_dequantize(int ty, const uint8_t* bytes, size_t nbytes, uint64_t ele
 /*
  * x: [rows][k] f32, k % 32 == 0. qs: [rows][k] int8. ds: [rows][k/32][2] f16 bits
  * (d, s). d = amax/127 in f32, id = d ? 1/d : 0, q = roundf(x*id) (half away
- * from zero), stored d = f16(d), s = f16(d * (float)sum(q)).
+ * from zero), stored d = f16(d), s = f16(sum(x) * id) with the sum taken in
+ * f32 in the device kernel's order: p_j = ((x[4j]+x[4j+1])+x[4j+2])+x[4j+3],
+ * then ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)).
  */
 void oracle_quantize_q8_1(const float* x, long rows, long k, int8_t* qs, uint16_t* ds) {
     long nblk = k / 32;
@@ -220,25 +223,27 @@ void oracle_quantize_q8_1(const float* x, long rows, long k, int8_t* qs, uint16_
             }
             float d = amax / 127.0f;
             float id = d != 0.0f ? 1.0f / d : 0.0f;
-            int sum = 0;
             for (int j = 0; j < 32; j++) {
                 float v = xb[j] * id;
                 int q = (int)roundf(v);
                 qs[r * k + b * 32 + j] = (int8_t)q;
-                sum += q;
             }
+            float p[8];
+            for (int j = 0; j < 8; j++) p[j] = ((xb[4 * j] + xb[4 * j + 1]) + xb[4 * j + 2]) + xb[4 * j + 3];
+            float sum = ((p[0] + p[4]) + (p[2] + p[6])) + ((p[1] + p[5]) + (p[3] + p[7]));
             ds[(r * nblk + b) * 2 + 0] = oracle_f32_to_f16(d);
-            ds[(r * nblk + b) * 2 + 1] = oracle_f32_to_f16((float)sum * d);
+            ds[(r * nblk + b) * 2 + 1] = oracle_f32_to_f16(sum * id);
         }
     }
 }
 
-/* Integer weight code of element e (0..255) of a Q4_K / Q6_K block, or of a Q8_0 block (e < 32). */
+/* Integer weight code of element e (0..255) of a Q4_K / Q6_K block, or of a
+ * Q8_0 block (e < 32): Q4_K nibble - 8, Q6_K q6 - 32, Q8_0 q. */
 static int wcode(int ty, const uint8_t* blk, int e) {
     if (ty == T_Q4K) {
         int g = e / 64, r = e % 64;
         uint8_t b = blk[16 + 32 * g + (r % 32)];
-        return r < 32 ? (b & 0xF) : (b >> 4);
+        return (r < 32 ? (b & 0xF) : (b >> 4)) - 8; /* centered: the MMQ kernel's B operand */
     }
     if (ty == T_Q6K) {
         int n = e / 128, r = e % 128, t = r / 32, l = r % 32;

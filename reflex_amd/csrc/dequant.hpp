@@ -13,7 +13,13 @@
 template <typename T>
 RFXQ_DEV T store_cvt(float v);
 template <> __device__ __forceinline__ float store_cvt<float>(float v) { return v; }
-template <> __device__ __forceinline__ half_t store_cvt<half_t>(float v) { return (half_t)v; }
+// The empty asm keeps the f32 value opaque so the narrowing is a plain RNE
+// conversion: fusing the producing multiply into a mixed-precision mad with a
+// +0 addend would turn -0.0 (a Q6_K block with d = 0) into +0.0.
+template <> __device__ __forceinline__ half_t store_cvt<half_t>(float v) {
+    asm volatile("" : "+v"(v));
+    return (half_t)v;
+}
 
 RFXQ_DEV void q4k_scale_min(uint32_t j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
     if (j < 4) {

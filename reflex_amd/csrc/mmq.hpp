@@ -10,12 +10,16 @@
 //
 // Per 32-block s of super-block sb, for output (m, n):
 //   D = sum_{k in s} qa[m,k] * code[n,k]                    (exact int32, MFMA)
-//   Q4_K: y += da[m,s] * (d*sc_s)[n] * D  -  s_a[m,s] * (dmin*m_s)[n]
+//   Q4_K: code = q - 8 (centered), and with c_s = 8*d*sc_s - dmin*m_s
+//         y += da[m,s] * (d*sc_s)[n] * D  +  Sx[m,s] * c_s[n]
+//         where Sx = d * s is the block's exact activation sum (the sum
+//         field, stored in units of d), so the weights' constant part sees
+//         unquantized activations.
 //   Q6_K: D folds the two 16-run scales: D = sc_lo*D_lo + sc_hi*D_hi;
 //         y += da[m,s] * d[n] * D
 //   Q8_0: y += da[m,s] * d[n,s] * D
-// The min term of a Q4_K super-block is one f16 MFMA (32x32x8, K = the 8
-// sub-blocks) accumulated into the same f32 accumulators.
+// The constant term of a Q4_K super-block is four f32 MFMAs (32x32x2, K = 2
+// of the 8 sub-blocks each) into the same f32 accumulators.
 //
 // Tile: 128 (M) x 128 (N) per 256-thread workgroup; each wave owns 64 x 64 =
 // 2 x 2 MFMA tiles. Activation scales for the tile's 128 rows are staged in
@@ -75,22 +79,32 @@ RFXQ_DEV void q4k_pair_scales(const u4_t hdr, uint32_t g, float& dsc0, float& ds
     dsc1 = d * (float)sc2;
 }
 
-// -(dmin * m_s) for s = 4h .. 4h+3 as f16 (the min MFMA's B operand).
-RFXQ_DEV h4_t q4k_neg_mins(const u4_t hdr, uint32_t h) {
-    const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    uint32_t m[4];
+// Constant part of the centered Q4_K weights, c_s = 8*(d*sc_s) - dmin*m_s
+// (w = d*sc*q - dmin*m = d*sc*(q - 8) + c), for the sub-blocks s = 2t + h,
+// t = 0..3, that this lane feeds to the K=2 f32 MFMAs.
+RFXQ_DEV void q4k_offsets(const u4_t hdr, uint32_t h, float c[4]) {
+    const float d = f16_bits_to_f32(hdr.x), dmin = f16_bits_to_f32(hdr.x >> 16);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const uint32_t lo = (hdr.z >> (8 * e)) & 63u;                                         // j = e < 4
-        const uint32_t hi = ((hdr.w >> (8 * e + 4)) & 0xFu) | (((hdr.z >> (8 * e + 6)) & 3u) << 4);  // j = 4 + e
-        m[e] = h ? hi : lo;
+    for (int t = 0; t < 4; t++) {
+        // j = 2t + h; bytes: q[j] of scales 0-3 (hdr.y) or 4-7 (hdr.z), q[j+4], q[j-4]
+        const uint32_t j = 2u * t + h;
+        uint32_t sc, m;
+        if (t < 2) {  // j < 4
+            sc = (hdr.y >> (8u * j)) & 63u;
+            m = (hdr.z >> (8u * j)) & 63u;
+        } else {      // j >= 4, e = j - 4
+            const uint32_t e = j - 4u;
+            sc = ((hdr.w >> (8u * e)) & 0xFu) | (((hdr.y >> (8u * e + 6u)) & 3u) << 4);
+            m = ((hdr.w >> (8u * e + 4u)) & 0xFu) | (((hdr.z >> (8u * e + 6u)) & 3u) << 4);
+        }
+        c[t] = 8.0f * (d * (float)sc) - dmin * (float)m;
     }
-    return h4_t{(half_t)(-(dmin * (float)m[0])), (half_t)(-(dmin * (float)m[1])), (half_t)(-(dmin * (float)m[2])),
-                (half_t)(-(dmin * (float)m[3]))};
 }
 
 RFXQ_DEV u4_t nib_lo(u4_t v) { return v & 0x0F0F0F0Fu; }
 RFXQ_DEV u4_t nib_hi(u4_t v) { return (v >> 4) & 0x0F0F0F0Fu; }
+// bytes q in [0, 15] -> q - 8 as int8 (no borrow between bytes)
+RFXQ_DEV u4_t center8(u4_t q) { return ((q | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
 // Q8_0: one 34-byte block (2-byte aligned, never read past its end); returns
 // the lane's 16 quants (K half h) and d.
@@ -144,7 +158,7 @@ RFXQ_DEV u4_t q6_codes(u4_t ql, u4_t qh, uint32_t t) {
 RFXQ_DEV int sbyte(uint32_t w, uint32_t byte) { return (int)(int8_t)(w >> (8u * byte)); }
 
 template <uint32_t TY, bool DOTS>
-RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, half_t* lds_sa) {
+RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float* lds_sx) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave & 1u, wn = wave >> 1;
     const uint32_t h = lane >> 5, l32 = lane & 31u;
@@ -198,8 +212,13 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, half_
             lds_da[(4u * st_part + 1u) * MMQ_BM + st_r] = f16_bits_to_f32(v.y);
             lds_da[(4u * st_part + 2u) * MMQ_BM + st_r] = f16_bits_to_f32(v.z);
             lds_da[(4u * st_part + 3u) * MMQ_BM + st_r] = f16_bits_to_f32(v.w);
-            const uint2 sa = {(v.x >> 16) | (v.y & 0xFFFF0000u), (v.z >> 16) | (v.w & 0xFFFF0000u)};
-            *reinterpret_cast<uint2*>(lds_sa + st_r * 8u + 4u * st_part) = sa;
+            // block activation sums d * s (s = sum(x)/d in f16), f32 [row][s]
+            float4 sx;
+            sx.x = f16_bits_to_f32(v.x) * f16_bits_to_f32(v.x >> 16);
+            sx.y = f16_bits_to_f32(v.y) * f16_bits_to_f32(v.y >> 16);
+            sx.z = f16_bits_to_f32(v.z) * f16_bits_to_f32(v.z >> 16);
+            sx.w = f16_bits_to_f32(v.w) * f16_bits_to_f32(v.w >> 16);
+            *reinterpret_cast<float4*>(lds_sx + st_r * 8u + 4u * st_part) = sx;
         }
         __syncthreads();
 
@@ -240,8 +259,8 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, half_
             for (int j = 0; j < 2; j++) {
                 if (TY == TY_Q4K) {
                     const u4_t qv = ld16(brow[j] + (uint64_t)sb * 144u + 16u + 32u * g + 16u * h);
-                    bw[j][0] = nib_lo(qv);
-                    bw[j][1] = nib_hi(qv);
+                    bw[j][0] = center8(nib_lo(qv));
+                    bw[j][1] = center8(nib_hi(qv));
                     q4k_pair_scales(hdr[j], g, wsc[j][0], wsc[j][1]);
                 } else if (TY == TY_Q6K) {
                     const uint32_t n = g >> 1, t0 = 2u * (g & 1u);
@@ -312,16 +331,21 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, half_
             }
         }
         if (TY == TY_Q4K && !DOTS) {
-            // min correction: acc -= sum_s s_a[m,s] * (dmin*m_s)[n] over this super-block
-            h4_t nm[2];
+            // constant part: acc += sum_s Sx[m,s] * c_s[n] over this super-block,
+            // as four K=2 f32 MFMAs (lane half h carries sub-blocks 2t + h)
+            float cw[2][4];
 #pragma unroll
-            for (int j = 0; j < 2; j++) nm[j] = q4k_neg_mins(hdr[j], h);
+            for (int j = 0; j < 2; j++) q4k_offsets(hdr[j], h, cw[j]);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                const h4_t sa = *reinterpret_cast<const h4_t*>(lds_sa + (64u * wm + 32u * i + l32) * 8u + 4u * h);
+                const float* sxp = lds_sx + (64u * wm + 32u * i + l32) * 8u + h;
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, nm[j], acc[i][j], 0, 0, 0);
+                for (int t = 0; t < 4; t++) {
+                    const float sx = sxp[2 * t];
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(sx, cw[j][t], acc[i][j], 0, 0, 0);
+                }
             }
         }
         __syncthreads();
@@ -360,9 +384,9 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
 #define RFXQ_MMQ_ENTRY(NAME, TY, DOTS)                                            \
     extern "C" __global__ __launch_bounds__(256) void NAME(MmqArgs args) {    \
         __shared__ float lds_da[8 * MMQ_BM];                                  \
-        __shared__ half_t lds_sa[MMQ_BM * 8];                                 \
+        __shared__ float lds_sx[MMQ_BM * 8];                                  \
         const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
-        mmq_tile<TY, DOTS>(d, blockIdx.x - d.wg_begin, lds_da, lds_sa);       \
+        mmq_tile<TY, DOTS>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx);       \
     }
 RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false)
 RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false)

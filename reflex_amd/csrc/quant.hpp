@@ -1,7 +1,13 @@
 // Activation quantization to int8 per 32 elements with an f16 scale and sum
-// (the Q8_1 block of src/dequant.rs:228-240: d, s = d * sum(q), qs[32]),
-// using ggml's published quantize_row_q8_1_ref rounding: d = amax / 127,
-// id = d ? 1/d : 0, q = roundf(x * id). The reference has no activation
+// (the Q8_1 block of src/dequant.rs:228-240: d, s, qs[32]), using ggml's
+// published quantize_row_q8_1_ref rounding: d = amax / 127, id = d ? 1/d : 0,
+// q = roundf(x * id). The sum field holds the block's exact activation sum in
+// units of d, s = f16(sum(x) * id) (|s| <= 32*127, so it cannot overflow f16),
+// rather than ggml's d*sum(q): the MMQ epilogue multiplies d*s by each weight
+// block's constant part, which removes that part's quantization error (about
+// half of the total for Q4_K). sum(x) is taken in f32 in a fixed order: lane
+// partials ((x0+x1)+x2)+x3 over 8 lanes, then a butterfly over lane distance
+// 4, 2, 1. The reference has no activation
 // quantizer (its prefill casts to f16, src/kernels_cuda/convert.cu:91); this
 // is the input stage of the int8 MMQ GEMM.
 //
@@ -37,7 +43,7 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id);
         const int q2 = (int)roundf(v.z * id), q3 = (int)roundf(v.w * id);
-        int sum = q0 + q1 + q2 + q3;
+        float sum = ((v.x + v.y) + v.z) + v.w;
         sum += __shfl_xor(sum, 4, 64);
         sum += __shfl_xor(sum, 2, 64);
         sum += __shfl_xor(sum, 1, 64);
@@ -47,7 +53,10 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
             *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
             if (part == 0u) {
                 const uint32_t dbits = __builtin_bit_cast(uint16_t, (half_t)d);
-                const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)((float)sum * d));
+                // round the product to f32 first (no fused single-rounding mixed mad)
+                float sid = sum * id;
+                asm volatile("" : "+v"(sid));
+                const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)sid);
                 xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
             }
         }

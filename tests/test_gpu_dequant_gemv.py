@@ -100,17 +100,19 @@ def test_gemv_config1_q8_0(rq, orc):
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("n,k", [(1, 256), (3, 256), (5, 768), (37, 512), (130, 1536), (17, 3072), (9, 14336)])
 def test_gemv_edge_shapes_reference_generators(rq, orc, ty, n, k):
-    """Reference generators: Q6_K d zero / negative, Q8_0 d zero / subnormal / signed."""
+    """Reference generators: Q6_K d zero / negative, Q8_0 d zero / subnormal / signed.
+    With a handful of outputs the row-L2 normalisation is over few values, so the
+    f16 activation rounding shows as up to ~2e-4 here (bound: 5e-4; spec: 1e-3)."""
     w = orc.synthetic(ty, k, n, 1000 + n)
     x = orc.activations(k, 7 + n)
-    _check_gemv(rq, orc, ty, n, k, w, x)
+    _check_gemv(rq, orc, ty, n, k, w, x, tol=5e-4)
 
 
 @pytest.mark.parametrize("ty", [Q6K, Q8_0])
 def test_gemv_two_byte_aligned_weights(rq, orc, ty):
     n, k = 33, 1024
     w = orc.synthetic(ty, k, n, 99)
-    _check_gemv(rq, orc, ty, n, k, w, orc.activations(k, 3), offset=2)
+    _check_gemv(rq, orc, ty, n, k, w, orc.activations(k, 3), offset=2, tol=5e-4)
 
 
 def test_gemv_zero_activations_and_one_hot(rq, orc):

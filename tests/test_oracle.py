@@ -169,7 +169,10 @@ def _np_quantize(x):
     idv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
     v = (xb * idv[..., None]).astype(np.float32).astype(np.float64)
     q = (np.trunc(v + np.copysign(0.5, v))).astype(np.int32)
-    s = (q.sum(axis=2).astype(np.float32) * d).astype(np.float32)
+    # exact block sum in f32, in the device kernel's order (8 lane partials, butterfly 4, 2, 1)
+    p = ((xb[..., 0::4] + xb[..., 1::4]) + xb[..., 2::4]) + xb[..., 3::4]
+    s = ((p[..., 0] + p[..., 4]) + (p[..., 2] + p[..., 6])) + ((p[..., 1] + p[..., 5]) + (p[..., 3] + p[..., 7]))
+    s = (s * idv).astype(np.float32)  # in units of d
     return q.astype(np.int8).reshape(x.shape), d.astype(np.float16).view(np.uint16), s.astype(np.float16).view(np.uint16)
 
 
@@ -205,7 +208,7 @@ def _codes_via_dequant(orc, ty, w, n, k):
         b[:, 0:2] = np.array(f16b(1.0), dtype=np.uint8)
         b[:, 2:4] = 0
         b[:, 4:16] = np.frombuffer(_pack_scale_min([1] * 8, [0] * 8), dtype=np.uint8)
-        return orc.dequantize(Q4K, b.reshape(-1), n * k).astype(np.int64).reshape(n, k)
+        return orc.dequantize(Q4K, b.reshape(-1), n * k).astype(np.int64).reshape(n, k) - 8  # centered
     if ty == Q6K:
         b = w.reshape(-1, 210)
         sc = b[:, 192:208].view(np.int8).astype(np.int64).copy()
@@ -231,6 +234,33 @@ def test_block_dots_brute_force(orc, ty):
     codes = _codes_via_dequant(orc, ty, w, n, k)
     want = np.einsum("mbj,nbj->mnb", qa.astype(np.int64).reshape(m, k // 32, 32), codes.reshape(n, k // 32, 32))
     assert np.array_equal(got, want)
+
+
+def test_q4k_scale_min_np_matches_c(orc):
+    w = orc.synthetic(Q4K, 512, 6, 17)
+    sc, m = orc.q4k_scale_min_np(w, 6, 512)
+    b = w.reshape(6, 2, 144)
+    for n in range(6):
+        for sb in range(2):
+            for j in range(8):
+                assert orc.get_scale_min_k4(j, bytes(b[n, sb, 4:16])) == (sc[n, 8 * sb + j], m[n, 8 * sb + j])
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+def test_mmq_model_reference_without_quantization(orc, ty):
+    """With activations already on the int8 grid of their own block scale
+    (x = d*q exactly, d a power of two) the model reference equals the plain
+    dequant + f64 matmul: the centered split w = d*sc*(q-8) + c is an identity."""
+    n, k = 6, 512
+    w = orc.synthetic(ty, k, n, 23)
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, (4, k)).astype(np.float32)
+    q[:, ::32] = 127  # block amax = 127 * d exactly
+    x = (q * np.float32(2.0 ** -7)).astype(np.float32)
+    got = orc.mmq_model_reference(ty, w, n, k, x)
+    want = orc.reference_gemm(ty, w, n, k, x)
+    # the Q4_K constant part uses the f16-rounded block sum / d, exact here (an integer below 2048)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
 
 
 # ------------------------------------------------------------ host matmul
