@@ -28,30 +28,59 @@ RFXQ_DEV float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-// Four dwords from a 16-byte-aligned global address.
-RFXQ_DEV u4_t ld16(const uint8_t* p) { return *reinterpret_cast<const u4_t*>(p); }
+// Global-address-space loads/stores: generic (flat) accesses would also count
+// against the LDS counter, making every LDS wait wait on HBM loads too.
+#define RFXQ_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t u4a4_t __attribute__((ext_vector_type(4), aligned(4)));
 
+// Four dwords from a 16-byte-aligned global address.
+RFXQ_DEV u4_t ld16(const void* p) { return *(const RFXQ_GLOBAL u4_t*)p; }
 // Four dwords from a dword-aligned global address.
-RFXQ_DEV u4_t ld16_a4(const uint8_t* p) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    u4_t r;
-    r.x = q[0];
-    r.y = q[1];
-    r.z = q[2];
-    r.w = q[3];
-    return r;
+RFXQ_DEV u4_t ld16_a4(const void* p) { return *(const RFXQ_GLOBAL u4a4_t*)p; }
+RFXQ_DEV uint32_t ld4(const void* p) { return *(const RFXQ_GLOBAL uint32_t*)p; }
+RFXQ_DEV uint32_t ld2(const void* p) { return *(const RFXQ_GLOBAL uint16_t*)p; }
+typedef float f4v_t __attribute__((ext_vector_type(4)));
+RFXQ_DEV float4 ldf4(const float* p) {
+    const f4v_t v = *(const RFXQ_GLOBAL f4v_t*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+RFXQ_DEV void stf(float* p, float v) { *(RFXQ_GLOBAL float*)p = v; }
+
+// Raw buffer access (gfx9 V#: base, stride 0, num_records = bytes): 32-bit
+// offsets, and reads at or past num_records return 0 instead of faulting.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+RFXQ_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+RFXQ_DEV u4_t bld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+RFXQ_DEV uint32_t bld4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+RFXQ_DEV void bst4f(rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
 }
 
 RFXQ_DEV uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t shift_bytes) {
     return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
-// Sum over groups of `width` consecutive lanes (width a power of two <= 64);
-// every lane of the group ends with the group sum.
+// DPP lane moves (row = 16 lanes): quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror.
+#define RFXQ_DPP(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+
+// Sum over groups of WIDTH consecutive lanes (a power of two <= 64). Within a
+// 16-lane row the sum uses DPP (every lane of the group ends with it); across
+// rows a swizzle (32) and readlanes (64, result valid in every lane).
 template <int WIDTH>
 RFXQ_DEV float group_sum(float v) {
-#pragma unroll
-    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (WIDTH >= 2) v += RFXQ_DPP(v, 0xB1);
+    if (WIDTH >= 4) v += RFXQ_DPP(v, 0x4E);
+    if (WIDTH >= 8) v += RFXQ_DPP(v, 0x141);
+    if (WIDTH >= 16) v += RFXQ_DPP(v, 0x140);
+    if (WIDTH >= 32)  // xor 16 within each 32-lane half: and_mask 0x1f, xor_mask 0x10
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if (WIDTH >= 64)
+        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     return v;
 }
 

@@ -7,10 +7,13 @@
 // table of independent GEMVs (descriptors), each with its own weight, x and y.
 //
 // Design (wave64, gfx950):
-//  * Each 256-thread workgroup owns a contiguous tile of output rows of one
-//    descriptor. Its prologue converts x once into LDS as f16, pair-permuted
-//    (see pair_perm) and, for Q4_K, with the high-nibble runs pre-scaled by
-//    1/16, plus per-16 sums of those f16 values.
+//  * Each 256-thread workgroup owns a small contiguous tile of output rows
+//    (tens of KB of weights) of one descriptor; its four waves work
+//    independently (no barriers), so tiles can be small enough to spread any
+//    GEMV over the whole chip and keep many loads in flight per CU.
+//  * Each lane converts the x values of its unit to f16 registers,
+//    pair-permuted and, for Q4_K high-nibble runs, pre-scaled by 1/16, plus
+//    per-16 sums of those f16 values.
 //  * Weights stream with 16-byte loads. A packed byte word is turned into two
 //    f16 values by masking a nibble (or byte) into the mantissa of 1024.0
 //    (0x6400 | q == 1024 + q), and contracted with v_dot2_f32_f16 against the
@@ -34,13 +37,14 @@ struct GemvDesc {
     const float* x;    // [k] f32
     float* y;          // [n] f32
     uint32_t k, n, type, lpr_log2;
-    uint32_t rows_per_wg, wg_begin, pad0, pad1;
+    uint32_t pad0, pad1, pad2, pad3;
 };
 
 #define GEMV_INLINE 4
 struct GemvArgs {
-    const GemvDesc* table;  // device table when ndesc > GEMV_INLINE
-    uint32_t ndesc, pad;
+    const GemvDesc* table;  // ndesc > GEMV_INLINE: the descriptors
+    const uint4* ranges;    // optional: per workgroup {d0, it0, d1, it1}
+    uint32_t ndesc, part_floats;
     GemvDesc inl[GEMV_INLINE];
 };
 
@@ -48,19 +52,39 @@ struct GemvArgs {
 
 // x -> LDS f16 (pair-permuted; Q4_K high-nibble runs scaled by 1/16) and the
 // per-16 sums of the stored f16 values (computed with the same dot2 op).
-RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, uint32_t* lds_x,
-                           float* lds_s) {
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t e = 4u * tid; e < k; e += 1024u) {
-        const float4 v = *reinterpret_cast<const float4*>(x + e);
-        const float sc = (prescale_hi && (e & 32u)) ? 0.0625f : 1.0f;
-        const h2_t a = {(half_t)(v.x * sc), (half_t)(v.z * sc)};
-        const h2_t b = {(half_t)(v.y * sc), (half_t)(v.w * sc)};
-        uint2 st;
-        st.x = h2_bits(a);
-        st.y = h2_bits(b);
-        *reinterpret_cast<uint2*>(lds_x + e / 2u) = st;
+// The first 4096 elements are loaded into registers by gemv_x_load before the
+// weight loads are issued, so their latency overlaps; the barriers wait on LDS
+// only, weight loads issued before stay in flight.
+struct XRegs {
+    float4 v[4];
+};
+
+RFXQ_DEV void gemv_x_load(const float* __restrict__ x, uint32_t k, XRegs& xr, uint32_t tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t e = 4u * tid + 1024u * i;
+        if (e < k) xr.v[i] = ldf4(x + e);
     }
+}
+
+RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, bool prescale_hi) {
+    const float sc = (prescale_hi && (e & 32u)) ? 0.0625f : 1.0f;
+    const h2_t a = {(half_t)(v.x * sc), (half_t)(v.z * sc)};
+    const h2_t b = {(half_t)(v.y * sc), (half_t)(v.w * sc)};
+    uint2 st;
+    st.x = h2_bits(a);
+    st.y = h2_bits(b);
+    *reinterpret_cast<uint2*>(lds_x + e / 2u) = st;
+}
+
+RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
+                           uint32_t* lds_x, float* lds_s, uint32_t tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t e = 4u * tid + 1024u * i;
+        if (e < k) gemv_x_put(lds_x, e, xr.v[i], prescale_hi);
+    }
+    for (uint32_t e = 4u * tid + 4096u; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), prescale_hi);
     __syncthreads();
     const uint32_t ng = k / 16u;
     for (uint32_t g = tid; g < ng; g += 256u) {
@@ -81,309 +105,421 @@ RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescal
     __syncthreads();
 }
 
-// ---------------------------------------------------------------- Q4_K unit
-
-// 64 weights: qs bytes [32g, 32g+32) of one super-block = sub-blocks 2g (low
-// nibbles) and 2g+1 (high nibbles). xl/xh: 16 dwords each of pair-permuted x.
-struct XQ4 {
-    uint4 l[4], h[4];
-};
-
-RFXQ_DEV void load_x_q4k(const uint32_t* lds_x, uint32_t xoff, XQ4& x) {
-    const uint4* p = reinterpret_cast<const uint4*>(lds_x + xoff / 2u);
-#pragma unroll
-    for (int i = 0; i < 4; i++) x.l[i] = p[i];
-#pragma unroll
-    for (int i = 0; i < 4; i++) x.h[i] = p[4 + i];
-}
-
 RFXQ_DEV uint32_t u4_at(const uint4* a, int j) {
     const uint4 v = a[j >> 2];
     return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
 }
 
-RFXQ_DEV float q4k_unit(const u4_t hdr, const u4_t qa, const u4_t qb, uint32_t g, const XQ4& x, const float* s) {
-    const uint32_t sh = (g & 1u) * 16u;
-    const uint32_t a = hdr.y >> sh, b = hdr.z >> sh, c = hdr.w >> sh;
-    uint32_t sc1, sc2, m1, m2;
-    if (g < 2u) {
-        sc1 = a & 63u;
-        sc2 = (a >> 8) & 63u;
-        m1 = b & 63u;
-        m2 = (b >> 8) & 63u;
-    } else {
-        sc1 = (c & 0xFu) | ((a >> 2) & 0x30u);
-        sc2 = ((c >> 8) & 0xFu) | ((a >> 10) & 0x30u);
-        m1 = ((c >> 4) & 0xFu) | ((b >> 2) & 0x30u);
-        m2 = ((c >> 12) & 0xFu) | ((b >> 10) & 0x30u);
-    }
-    const float d = f16_bits_to_f32(hdr.x);
-    const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    const float d1 = d * (float)sc1, d2 = d * (float)sc2;
-    const float mm1 = dmin * (float)m1, mm2 = dmin * (float)m2;
+// ---------------------------------------------------------------- per-type units
+//
+// A "unit" is one lane's share of one row: 64 weights for Q4_K / Q6_K (a
+// quarter super-block), 32 for Q8_0 (one block). Each type provides
+//   Raw      the unit's raw bytes as loaded (kept in registers while in flight)
+//   XV       the unit's x values (from LDS) and x sums
+//   load()   issue the global loads of a unit
+//   loadx()  read the unit's x from LDS
+//   dot()    the unit's contribution to the row's dot product
 
-    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    float rl0 = 0.f, rl1 = 0.f, rh0 = 0.f, rh1 = 0.f;
+struct Q4K {
+    static constexpr uint32_t QK = 256, BB = 144, UPB = 4;  // units per block
+    static constexpr int PF = 2;                            // items in flight per wave
+    struct Raw {
+        u4_t hdr, qa, qb;
+    };
+    struct XV {
+        uint4 l[4], h[4];
+        float s[4];
+    };
+    static RFXQ_DEV uint32_t xoff(uint32_t unit) { return 256u * (unit >> 2) + 64u * (unit & 3u); }
+    // byte offset of the unit's block within a row
+    static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return (unit >> 2) * BB; }
+    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t unit) {
+        const uint32_t q = off + 16u + 32u * (unit & 3u);
+        return Raw{bld16(w, off), bld16(w, q), bld16(w, q + 16u)};
+    }
+    static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
+        const uint32_t o = xoff(unit);
+        const uint4* p = reinterpret_cast<const uint4*>(lds_x + o / 2u);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t v = q[j], v8 = v >> 8;
-        rl0 = dot2((v & 0x000F000Fu) | 0x64006400u, u4_at(x.l, 2 * j), rl0);
-        rl1 = dot2((v8 & 0x000F000Fu) | 0x64006400u, u4_at(x.l, 2 * j + 1), rl1);
-        rh0 = dot2((v & 0x00F000F0u) | 0x64006400u, u4_at(x.h, 2 * j), rh0);
-        rh1 = dot2((v8 & 0x00F000F0u) | 0x64006400u, u4_at(x.h, 2 * j + 1), rh1);
+        for (int i = 0; i < 4; i++) x.l[i] = p[i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x.h[i] = p[4 + i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x.s[i] = lds_s[o / 16u + i];
     }
-    const float slo = s[0] + s[1], shi = s[2] + s[3];
-    const float lo = d1 * (rl0 + rl1) - (1024.0f * d1 + mm1) * slo;
-    const float hi = d2 * (rh0 + rh1) - (1024.0f * d2 + 16.0f * mm2) * shi;
-    return lo + hi;
-}
+    // qs bytes [32g, 32g+32) = sub-blocks 2g (low nibbles) and 2g+1 (high).
+    // The 6-bit scales/mins of sub-blocks j = 2g, 2g+1 (g = unit & 3, fixed
+    // per lane) are decoded without branches: bytes (q[j], q[j+4], q[j-4]) of
+    // the 12-byte table sit in a = hdr.y, b = hdr.z, c = hdr.w, 16*(g&1) bits
+    // up; j < 4 takes the low 6 bits of a (scales) and b (mins), j >= 4 takes
+    // a nibble of c plus the top 2 bits of a (scales) or b (mins).
+    static RFXQ_DEV float dot(const Raw& r, uint32_t unit, const XV& x, uint32_t MG) {
+#pragma clang fp contract(off)
+        const uint32_t g = unit & 3u;
+        const uint32_t sh = (g & 1u) * 16u;
+        const bool low = g < 2u;
+        const uint32_t a = r.hdr.y >> sh, b = r.hdr.z >> sh, c = r.hdr.w >> sh;
+        const uint32_t mlo = low ? 0x3F3Fu : 0x0F0Fu, mhi = low ? 0u : 0x3030u;
+        const uint32_t SC = ((low ? a : c) & mlo) | ((a >> 2) & mhi);
+        const uint32_t M = (((low ? b : c) >> (low ? 0u : 4u)) & mlo) | ((b >> 2) & mhi);
+        const float d = f16_bits_to_f32(r.hdr.x);
+        const float dmin = f16_bits_to_f32(r.hdr.x >> 16);
+        const float d1 = d * (float)(SC & 0xFFu), d2 = d * (float)((SC >> 8) & 0xFFu);
+        const float mm1 = dmin * (float)(M & 0xFFu), mm2 = dmin * (float)((M >> 8) & 0xFFu);
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        float rl0 = 0.f, rl1 = 0.f, rh0 = 0.f, rh1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t v = q[j], v8 = v >> 8;
+            rl0 = dot2((v & 0x000F000Fu) | MG, u4_at(x.l, 2 * j), rl0);
+            rl1 = dot2((v8 & 0x000F000Fu) | MG, u4_at(x.l, 2 * j + 1), rl1);
+            rh0 = dot2((v & 0x00F000F0u) | MG, u4_at(x.h, 2 * j), rh0);
+            rh1 = dot2((v8 & 0x00F000F0u) | MG, u4_at(x.h, 2 * j + 1), rh1);
+        }
+        const float slo = x.s[0] + x.s[1], shi = x.s[2] + x.s[3];
+        const float lo = fmaf(d1, rl0 + rl1, -(fmaf(1024.0f, d1, mm1) * slo));
+        const float hi = fmaf(d2, rh0 + rh1, -(fmaf(1024.0f, d2, 16.0f * mm2) * shi));
+        return lo + hi;
+    }
+};
 
-// ---------------------------------------------------------------- Q6_K unit
-
-// 16 bytes at byte offset o of a 2-byte-aligned block base p (pa = p & ~3,
-// sh = p & 3), read as dwords from the dword-aligned base and realigned.
-// Never reads past o + 20 from p's dword-aligned base, i.e. stays inside the
-// block for o <= 176.
-RFXQ_DEV u4_t seg16(const uint8_t* pa, uint32_t o, uint32_t sh) {
-    const u4_t v = ld16_a4(pa + o);
-    const uint32_t e = *reinterpret_cast<const uint32_t*>(pa + o + 16);
+// 16 bytes at byte offset o of a 2-byte-aligned block: four dwords from the
+// dword-aligned offset below plus one more, realigned by sh = 0 or 2 bytes.
+// Buffer loads return 0 past the end of the weights, so the extra dword is
+// always safe.
+struct Seg {
+    u4_t v;
+    uint32_t e;
+};
+RFXQ_DEV Seg seg_load(rsrc_t w, uint32_t off4) { return Seg{bld16(w, off4), bld4(w, off4 + 16u)}; }
+RFXQ_DEV u4_t seg_align(const Seg& s, uint32_t sh) {
     u4_t r;
-    r.x = alignbyte(v.y, v.x, sh);
-    r.y = alignbyte(v.z, v.y, sh);
-    r.z = alignbyte(v.w, v.z, sh);
-    r.w = alignbyte(e, v.w, sh);
+    r.x = alignbyte(s.v.y, s.v.x, sh);
+    r.y = alignbyte(s.v.z, s.v.y, sh);
+    r.z = alignbyte(s.v.w, s.v.z, sh);
+    r.w = alignbyte(s.e, s.v.w, sh);
     return r;
 }
 
-struct XQ6 {
-    uint4 r[4][2];  // 4 runs of 16 elements: 8 dwords each
+struct Q6K {
+    static constexpr uint32_t QK = 256, BB = 210, UPB = 4;
+    static constexpr int PF = 2;
+    struct Raw {
+        Seg a, c, h;
+        u4_t sw;
+        uint32_t tail, sh;
+    };
+    struct XV {
+        uint4 r[4][2];
+        float s[4];
+    };
+    // half n = g >> 1, positions [16*(g&1), +16) of the four 32-runs
+    static RFXQ_DEV uint32_t xoff(uint32_t unit) {
+        const uint32_t g = unit & 3u;
+        return 256u * (unit >> 2) + 128u * (g >> 1) + 16u * (g & 1u);
+    }
+    static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return (unit >> 2) * BB; }
+    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t unit) {
+        const uint32_t g = unit & 3u, n = g >> 1, hs = g & 1u;
+        const uint32_t a4 = off & ~3u;  // blocks are 2-byte aligned
+        Raw r;
+        r.sh = off & 3u;
+        r.a = seg_load(w, a4 + 64u * n + 16u * hs);
+        r.c = seg_load(w, a4 + 64u * n + 32u + 16u * hs);
+        r.h = seg_load(w, a4 + 128u + 32u * n + 16u * hs);
+        r.sw = bld16(w, a4 + 192u);  // scales (192..207)
+        r.tail = bld4(w, a4 + 208u); // d (208..209)
+        return r;
+    }
+    static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
+        const uint32_t o = xoff(unit);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint4* p = reinterpret_cast<const uint4*>(lds_x + (o + 32u * t) / 2u);
+            x.r[t][0] = p[0];
+            x.r[t][1] = p[1];
+            x.s[t] = lds_s[o / 16u + 2u * t];
+        }
+    }
+    static RFXQ_DEV float dot(const Raw& r, uint32_t unit, const XV& x, uint32_t MG) {
+#pragma clang fp contract(off)
+        const uint32_t g = unit & 3u, n = g >> 1, hs = g & 1u, sh = r.sh;
+        const u4_t a = seg_align(r.a, sh), c = seg_align(r.c, sh), h = seg_align(r.h, sh);
+        const uint32_t s0 = alignbyte(r.sw.y, r.sw.x, sh), s1 = alignbyte(r.sw.z, r.sw.y, sh);
+        const uint32_t s2 = alignbyte(r.sw.w, r.sw.z, sh), s3 = alignbyte(r.tail, r.sw.w, sh);
+        const float d = f16_bits_to_f32(alignbyte(r.tail, r.tail, sh));
+        const uint32_t W0 = n ? s2 : s0, W1 = n ? s3 : s1;
+        const int sc0 = (int)(int8_t)(W0 >> (8u * hs));
+        const int sc1 = (int)(int8_t)(W0 >> (8u * hs + 16u));
+        const int sc2 = (int)(int8_t)(W1 >> (8u * hs));
+        const int sc3 = (int)(int8_t)(W1 >> (8u * hs + 16u));
+        const uint32_t A[4] = {a.x, a.y, a.z, a.w}, C[4] = {c.x, c.y, c.z, c.w}, H[4] = {h.x, h.y, h.z, h.w};
+        float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+        const uint32_t M4 = 0x000F000Fu, M2 = 0x00300030u;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t av = A[j], cv = C[j], hv = H[j];
+            r0 = dot2((av & M4) | ((hv << 4) & M2) | MG, u4_at(x.r[0], 2 * j), r0);
+            r0 = dot2(((av >> 8) & M4) | ((hv >> 4) & M2) | MG, u4_at(x.r[0], 2 * j + 1), r0);
+            r1 = dot2((cv & M4) | ((hv << 2) & M2) | MG, u4_at(x.r[1], 2 * j), r1);
+            r1 = dot2(((cv >> 8) & M4) | ((hv >> 6) & M2) | MG, u4_at(x.r[1], 2 * j + 1), r1);
+            r2 = dot2(((av >> 4) & M4) | (hv & M2) | MG, u4_at(x.r[2], 2 * j), r2);
+            r2 = dot2(((av >> 12) & M4) | ((hv >> 8) & M2) | MG, u4_at(x.r[2], 2 * j + 1), r2);
+            r3 = dot2(((cv >> 4) & M4) | ((hv >> 2) & M2) | MG, u4_at(x.r[3], 2 * j), r3);
+            r3 = dot2(((cv >> 12) & M4) | ((hv >> 10) & M2) | MG, u4_at(x.r[3], 2 * j + 1), r3);
+        }
+        const float ds0 = d * (float)sc0, ds1 = d * (float)sc1, ds2 = d * (float)sc2, ds3 = d * (float)sc3;
+        float acc = fmaf(ds0, r0, -((1056.0f * ds0) * x.s[0]));
+        acc += fmaf(ds1, r1, -((1056.0f * ds1) * x.s[1]));
+        acc += fmaf(ds2, r2, -((1056.0f * ds2) * x.s[2]));
+        acc += fmaf(ds3, r3, -((1056.0f * ds3) * x.s[3]));
+        return acc;
+    }
 };
 
-RFXQ_DEV void load_x_q6k(const uint32_t* lds_x, uint32_t xoff, XQ6& x) {
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const uint4* p = reinterpret_cast<const uint4*>(lds_x + (xoff + 32u * t) / 2u);
-        x.r[t][0] = p[0];
-        x.r[t][1] = p[1];
+struct Q80 {
+    static constexpr uint32_t QK = 32, BB = 34, UPB = 1;
+    static constexpr int PF = 4;
+    struct Raw {
+        u4_t w0, w1;
+        uint32_t w8, sh;
+    };
+    struct XV {
+        uint4 v[4];
+        float s[2];
+    };
+    static RFXQ_DEV uint32_t xoff(uint32_t unit) { return unit * 32u; }
+    static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return unit * BB; }
+    // one 34-byte block (2-byte aligned): 9 dwords from the dword-aligned offset
+    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t) {
+        const uint32_t a4 = off & ~3u;
+        Raw r;
+        r.sh = off & 3u;
+        r.w0 = bld16(w, a4);
+        r.w1 = bld16(w, a4 + 16u);
+        r.w8 = bld4(w, a4 + 32u);
+        return r;
     }
-}
-
-// 64 weights of one super-block: half n = g >> 1, positions l in [16*(g&1), +16)
-// of its four 32-runs (src/dequant.rs:414-444 layout).
-RFXQ_DEV float q6k_unit(const uint8_t* blk, uint32_t g, const XQ6& x, const float* s) {
-    const uint32_t n = g >> 1, hs = g & 1u;
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
-    const uint8_t* pa = reinterpret_cast<const uint8_t*>(addr & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(addr & 3u);
-    const u4_t a = seg16(pa, 64u * n + 16u * hs, sh);
-    const u4_t c = seg16(pa, 64u * n + 32u + 16u * hs, sh);
-    const u4_t h = seg16(pa, 128u + 32u * n + 16u * hs, sh);
-    // scales (bytes 192..207) and d (208..209) without reading past byte 209
-    const u4_t sw = ld16_a4(pa + 192);
-    uint32_t tail;
-    if (sh) tail = *reinterpret_cast<const uint32_t*>(pa + 208);
-    else tail = *reinterpret_cast<const uint16_t*>(blk + 208);
-    const uint32_t s0 = alignbyte(sw.y, sw.x, sh), s1 = alignbyte(sw.z, sw.y, sh);
-    const uint32_t s2 = alignbyte(sw.w, sw.z, sh), s3 = alignbyte(tail, sw.w, sh);
-    const float d = f16_bits_to_f32(sh ? (tail >> 16) : tail);
-    const uint32_t W0 = n ? s2 : s0, W1 = n ? s3 : s1;
-    const int sc0 = (int)(int8_t)(W0 >> (8u * hs));
-    const int sc1 = (int)(int8_t)(W0 >> (8u * hs + 16u));
-    const int sc2 = (int)(int8_t)(W1 >> (8u * hs));
-    const int sc3 = (int)(int8_t)(W1 >> (8u * hs + 16u));
-
-    const uint32_t A[4] = {a.x, a.y, a.z, a.w}, C[4] = {c.x, c.y, c.z, c.w}, H[4] = {h.x, h.y, h.z, h.w};
-    float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
-    const uint32_t M4 = 0x000F000Fu, M2 = 0x00300030u, MG = 0x64006400u;
+    static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
+        const uint32_t o = xoff(unit);
+        const uint4* p = reinterpret_cast<const uint4*>(lds_x + o / 2u);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t av = A[j], cv = C[j], hv = H[j];
-        const uint32_t xe0 = u4_at(x.r[0], 2 * j), xo0 = u4_at(x.r[0], 2 * j + 1);
-        const uint32_t xe1 = u4_at(x.r[1], 2 * j), xo1 = u4_at(x.r[1], 2 * j + 1);
-        const uint32_t xe2 = u4_at(x.r[2], 2 * j), xo2 = u4_at(x.r[2], 2 * j + 1);
-        const uint32_t xe3 = u4_at(x.r[3], 2 * j), xo3 = u4_at(x.r[3], 2 * j + 1);
-        r0 = dot2((av & M4) | ((hv << 4) & M2) | MG, xe0, r0);
-        r0 = dot2(((av >> 8) & M4) | ((hv >> 4) & M2) | MG, xo0, r0);
-        r1 = dot2((cv & M4) | ((hv << 2) & M2) | MG, xe1, r1);
-        r1 = dot2(((cv >> 8) & M4) | ((hv >> 6) & M2) | MG, xo1, r1);
-        r2 = dot2(((av >> 4) & M4) | (hv & M2) | MG, xe2, r2);
-        r2 = dot2(((av >> 12) & M4) | ((hv >> 8) & M2) | MG, xo2, r2);
-        r3 = dot2(((cv >> 4) & M4) | ((hv >> 2) & M2) | MG, xe3, r3);
-        r3 = dot2(((cv >> 12) & M4) | ((hv >> 10) & M2) | MG, xo3, r3);
+        for (int i = 0; i < 4; i++) x.v[i] = p[i];
+        x.s[0] = lds_s[o / 16u];
+        x.s[1] = lds_s[o / 16u + 1u];
     }
-    const float ds0 = d * (float)sc0, ds1 = d * (float)sc1, ds2 = d * (float)sc2, ds3 = d * (float)sc3;
-    float acc = ds0 * r0 - (1056.0f * ds0) * s[0];
-    acc += ds1 * r1 - (1056.0f * ds1) * s[2];
-    acc += ds2 * r2 - (1056.0f * ds2) * s[4];
-    acc += ds3 * r3 - (1056.0f * ds3) * s[6];
-    return acc;
-}
-
-// ---------------------------------------------------------------- Q8_0 unit
-
-struct XQ8 {
-    uint4 v[4];
+    static RFXQ_DEV float dot(const Raw& r, uint32_t, const XV& x, uint32_t MG) {
+#pragma clang fp contract(off)
+        const uint32_t sh = r.sh;
+        const uint32_t w[9] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w, r.w8};
+        const float d = f16_bits_to_f32(alignbyte(r.w0.x, r.w0.x, sh));
+        float r0 = 0.f, r1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t q = sh ? w[j + 1] : alignbyte(w[j + 1], w[j], 2u);
+            const uint32_t v = q ^ 0x80808080u;
+            r0 = dot2((v & 0x00FF00FFu) | MG, u4_at(x.v, 2 * j), r0);
+            r1 = dot2(((v >> 8) & 0x00FF00FFu) | MG, u4_at(x.v, 2 * j + 1), r1);
+        }
+        return d * fmaf(-1152.0f, x.s[0] + x.s[1], r0 + r1);
+    }
 };
 
-RFXQ_DEV void load_x_q8(const uint32_t* lds_x, uint32_t xoff, XQ8& x) {
-    const uint4* p = reinterpret_cast<const uint4*>(lds_x + xoff / 2u);
-#pragma unroll
-    for (int i = 0; i < 4; i++) x.v[i] = p[i];
-}
+// ---------------------------------------------------------------- row loop
 
-// One 34-byte block (2-byte aligned), never reading past its last byte.
-RFXQ_DEV float q8_0_unit(const uint8_t* blk, const XQ8& x, const float* s) {
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
-    const uint8_t* pa = reinterpret_cast<const uint8_t*>(addr & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(addr & 3u);
-    const u4_t w0 = ld16_a4(pa), w1 = ld16_a4(pa + 16);
-    uint32_t w8;
-    if (sh) w8 = *reinterpret_cast<const uint32_t*>(pa + 32);
-    else w8 = *reinterpret_cast<const uint16_t*>(blk + 32);
-    const uint32_t w[9] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w8};
-    const float d = f16_bits_to_f32(sh ? (w0.x >> 16) : w0.x);
-    float r0 = 0.f, r1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t q = sh ? w[j + 1] : alignbyte(w[j + 1], w[j], 2u);
-        const uint32_t v = q ^ 0x80808080u;
-        r0 = dot2((v & 0x00FF00FFu) | 0x64006400u, u4_at(x.v, 2 * j), r0);
-        r1 = dot2(((v >> 8) & 0x00FF00FFu) | 0x64006400u, u4_at(x.v, 2 * j + 1), r1);
-    }
-    return d * ((r0 + r1) - 1152.0f * (s[0] + s[1]));
-}
+// Rows are covered by lane groups of LPR lanes; lane li owns units li + u*LPR,
+// u < U. The wave's rows are row_begin + wave*RPI + sub + it*4*RPI (sub =
+// lane / LPR, it < n_it). Work items run pass by pass: pass u walks all of
+// the wave's rows with unit li + u*LPR, so a lane only ever holds the x slice
+// of one unit in registers (reloaded from LDS at each pass start). With U > 1
+// the group-reduced partial of each row is carried between passes in LDS by
+// lane li == 0 of the group (always the same thread, so program order is
+// enough) and added in pass order, so the result does not depend on tiling.
+//
+// Loads run T::PF items ahead in a ring: each slot is refilled right after
+// its math. Refills past the wave's last item read at kPastEnd (zeros, no
+// memory traffic) and are never used. Item bounds are wave-uniform scalar branches.
+// Offset for refills past a wave's last item: beyond any weight buffer's
+// range (the host keeps weights below it), so the load returns zeros without
+// fetching anything.
+constexpr uint32_t kPastEnd = 0xFFFFF000u;
 
-// ---------------------------------------------------------------- row loops
-
-template <uint32_t TY, int LPR>
-RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_end, const uint32_t* lds_x,
-                        const float* lds_s) {
+template <typename T, int LPR>
+RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_end, bool restage, uint32_t* lds_x,
+                        float* lds_s, float* lds_p) {
+#pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    constexpr int PF = T::PF;
+    // opaque to the optimiser: keeps the lane-derived values of every type and
+    // LPR variant from being hoisted out of the segment loop (all of them
+    // would then stay live across it)
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t sub = lane / LPR, li = lane % LPR;
-    const uint32_t k = dsc.k;
-    const uint32_t units = TY == TY_Q8_0 ? k / 32u : k / 64u;
+    const uint32_t k = dsc.k, n = dsc.n;
+    const uint32_t units = k / (T::QK / T::UPB);
     const uint32_t U = units / LPR;
-    const uint64_t row_bytes = TY == TY_Q4K ? (uint64_t)(k / 256u) * 144u
-                             : TY == TY_Q6K ? (uint64_t)(k / 256u) * 210u
-                                            : (uint64_t)(k / 32u) * 34u;
-    const uint8_t* __restrict__ w = dsc.w;
-    float* __restrict__ y = dsc.y;
+    const uint32_t row_bytes = (k / T::QK) * T::BB;
+    // dword-aligned V# base (Q6_K / Q8_0 data may start 2 bytes past one), the
+    // remainder added to every offset, range rounded up to whole dwords (the
+    // last dword never crosses a page, so reading all of it is safe)
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(dsc.w);
+    const uint32_t wsh = (uint32_t)(wa & 3u);
+    const rsrc_t wr = make_rsrc(reinterpret_cast<const void*>(wa - wsh), (wsh + n * row_bytes + 3u) & ~3u);
+    const rsrc_t yr = make_rsrc(dsc.y, n * 4u);
+    const uint32_t base0 = row_begin + wave * RPI;
+    const uint32_t stride = 4u * RPI;
+    // wave-uniform (the scalar unit runs the item loop)
+    const uint32_t n_it = __builtin_amdgcn_readfirstlane(base0 < row_end ? (row_end - base0 + stride - 1u) / stride : 0u);
+    const uint32_t n_items = n_it * U;
+    const uint32_t row_step = stride * row_bytes;  // bytes between row iterations
+    const uint32_t unit_step = T::unit_off(LPR);   // bytes between a lane's passes
+    const uint32_t off0 = wsh + (base0 + sub) * row_bytes + T::unit_off(li);
+    // this wave's rows of the segment (wave 0 has the most iterations)
+    const uint32_t n_it_max = row_begin < row_end ? (row_end - row_begin + stride - 1u) / stride : 0u;
+    float* part = lds_p + wave * n_it_max * RPI;
 
-    auto unit_xoff = [&](uint32_t unit) -> uint32_t {
-        if (TY == TY_Q8_0) return unit * 32u;
-        const uint32_t b = unit >> 2, g = unit & 3u;
-        return TY == TY_Q4K ? 256u * b + 64u * g : 256u * b + 128u * (g >> 1) + 16u * (g & 1u);
-    };
-    auto unit_ptr = [&](uint32_t row, uint32_t unit) -> const uint8_t* {
-        const uint64_t off = (uint64_t)row * row_bytes;
-        if (TY == TY_Q8_0) return w + off + (uint64_t)unit * 34u;
-        return w + off + (uint64_t)(unit >> 2) * (TY == TY_Q4K ? 144u : 210u);
+    // next item to load: pass lu, row iteration lit (scalar counters)
+    uint32_t lu = n_it ? 0u : U, lit = 0, loff = off0;
+    auto advance = [&]() {
+        loff += row_step;
+        if (++lit == n_it) {
+            lit = 0;
+            lu++;
+            loff = off0 + lu * unit_step;
+        }
     };
 
-    if (U == 1u) {
-        // The lane's x slice is the same for every row: keep it in registers.
-        const uint32_t unit = li;
-        const uint32_t xoff = unit_xoff(unit);
-        const float* s = lds_s + xoff / 16u;
-        XQ4 x4;
-        XQ6 x6;
-        XQ8 x8;
-        float sv[8];
-        if (TY == TY_Q4K) {
-            load_x_q4k(lds_x, xoff, x4);
-            for (int i = 0; i < 4; i++) sv[i] = s[i];
-        } else if (TY == TY_Q6K) {
-            load_x_q6k(lds_x, xoff, x6);
-            for (int i = 0; i < 8; i++) sv[i] = s[i];
-        } else {
-            load_x_q8(lds_x, xoff, x8);
-            for (int i = 0; i < 2; i++) sv[i] = s[i];
-        }
-        for (uint32_t base = row_begin + wave * RPI; base < row_end; base += 4u * RPI) {
-            const uint32_t row = base + sub;
-            const uint32_t rr = row < row_end ? row : row_end - 1u;
-            const uint8_t* p = unit_ptr(rr, unit);
-            float acc;
-            if (TY == TY_Q4K) {
-                const uint32_t g = unit & 3u;
-                acc = q4k_unit(ld16(p), ld16(p + 16 + 32u * g), ld16(p + 32 + 32u * g), g, x4, sv);
-            } else if (TY == TY_Q6K) {
-                acc = q6k_unit(p, unit & 3u, x6, sv);
-            } else {
-                acc = q8_0_unit(p, x8, sv);
-            }
-            acc = group_sum<LPR>(acc);
-            if (li == 0u && row < row_end) y[row] = acc;
-        }
-    } else {
-        for (uint32_t base = row_begin + wave * RPI; base < row_end; base += 4u * RPI) {
-            const uint32_t row = base + sub;
-            const uint32_t rr = row < row_end ? row : row_end - 1u;
-            float acc = 0.0f;
-            for (uint32_t u = 0; u < U; u++) {
-                const uint32_t unit = li + u * LPR;
-                const uint32_t xoff = unit_xoff(unit);
-                const float* s = lds_s + xoff / 16u;
-                const uint8_t* p = unit_ptr(rr, unit);
-                if (TY == TY_Q4K) {
-                    XQ4 x4;
-                    load_x_q4k(lds_x, xoff, x4);
-                    const uint32_t g = unit & 3u;
-                    acc += q4k_unit(ld16(p), ld16(p + 16 + 32u * g), ld16(p + 32 + 32u * g), g, x4, s);
-                } else if (TY == TY_Q6K) {
-                    XQ6 x6;
-                    load_x_q6k(lds_x, xoff, x6);
-                    acc += q6k_unit(p, unit & 3u, x6, s);
-                } else {
-                    XQ8 x8;
-                    load_x_q8(lds_x, xoff, x8);
-                    acc += q8_0_unit(p, x8, s);
+    XRegs xr;
+    gemv_x_load(dsc.x, k, xr, tid);
+    typename T::Raw r[PF];
+#pragma unroll
+    for (int t = 0; t < PF; t++) {
+        r[t] = T::load(wr, lu < U ? loff : kPastEnd, li + lu * LPR);
+        advance();
+    }
+    if (restage) __syncthreads();  // every wave is done with the previous segment's x
+    gemv_stage_x(dsc.x, k, T::QK == 256u && T::BB == 144u, xr, lds_x, lds_s, tid);
+
+    // f16 1024.0 in both halves, kept in a VGPR: gfx9 VOP3 takes at most one
+    // SGPR/constant, so (v & mask) | magic is one v_and_or_b32 only this way
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+    typename T::XV xv;
+    T::loadx(lds_x, lds_s, li, xv);
+    uint32_t cu = 0, cit = 0;  // item being computed
+    for (uint32_t t0 = 0; t0 < n_items; t0 += PF) {
+#pragma unroll
+        for (int t = 0; t < PF; t++) {
+            if (t0 + t < n_items) {
+                const uint32_t unit = li + cu * LPR;
+                float acc = T::dot(r[t], unit, xv, magic);
+                r[t] = T::load(wr, lu < U ? loff : kPastEnd, li + lu * LPR);
+                advance();
+                acc = group_sum<LPR>(acc);
+                const uint32_t row = base0 + sub + cit * stride;
+                if (li == 0u && row < row_end) {
+                    if (U == 1u) {
+                        bst4f(yr, row * 4u, acc);
+                    } else {
+                        float* p = part + cit * RPI + sub;
+                        if (cu == 0u) *p = acc;
+                        else if (cu + 1u < U) *p += acc;
+                        else bst4f(yr, row * 4u, *p + acc);
+                    }
+                }
+                if (++cit == n_it) {
+                    cit = 0;
+                    if (++cu < U) T::loadx(lds_x, lds_s, li + cu * LPR, xv);
                 }
             }
-            acc = group_sum<LPR>(acc);
-            if (li == 0u && row < row_end) y[row] = acc;
         }
     }
 }
 
-template <uint32_t TY>
-RFXQ_DEV void gemv_dispatch_lpr(const GemvDesc& d, uint32_t rb, uint32_t re, const uint32_t* lx, const float* ls) {
+template <typename T>
+RFXQ_DEV void gemv_dispatch_lpr(const GemvDesc& d, uint32_t rb, uint32_t re, bool rs, uint32_t* lx, float* ls,
+                                float* lp) {
     switch (d.lpr_log2) {
-        case 2: gemv_rows<TY, 4>(d, rb, re, lx, ls); break;
-        case 3: gemv_rows<TY, 8>(d, rb, re, lx, ls); break;
-        case 4: gemv_rows<TY, 16>(d, rb, re, lx, ls); break;
-        case 5: gemv_rows<TY, 32>(d, rb, re, lx, ls); break;
-        default: gemv_rows<TY, 64>(d, rb, re, lx, ls); break;
+        case 2: gemv_rows<T, 4>(d, rb, re, rs, lx, ls, lp); break;
+        case 3: gemv_rows<T, 8>(d, rb, re, rs, lx, ls, lp); break;
+        case 4: gemv_rows<T, 16>(d, rb, re, rs, lx, ls, lp); break;
+        case 5: gemv_rows<T, 32>(d, rb, re, rs, lx, ls, lp); break;
+        default: gemv_rows<T, 64>(d, rb, re, rs, lx, ls, lp); break;
     }
 }
 
-RFXQ_DEV GemvDesc gemv_pick(const GemvArgs& a, uint32_t wg) {
-    if (a.ndesc <= GEMV_INLINE) {
-        GemvDesc d = a.inl[0];
-        if (a.ndesc > 1 && wg >= a.inl[1].wg_begin) d = a.inl[1];
-        if (a.ndesc > 2 && wg >= a.inl[2].wg_begin) d = a.inl[2];
-        if (a.ndesc > 3 && wg >= a.inl[3].wg_begin) d = a.inl[3];
-        return d;
-    }
-    uint32_t lo = 0, hi = a.ndesc - 1u;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi + 1u) >> 1;
-        if (a.table[mid].wg_begin <= wg) lo = mid;
-        else hi = mid - 1u;
-    }
-    return a.table[lo];
+// Rows of a descriptor are handed out in row iterations of 4 * (64 / LPR)
+// rows (one lane group per wave and row). The launch has a fixed number of
+// workgroups (about as many as the chip holds at once); workgroup g walks a
+// contiguous range of the launch's iterations in descriptor order, [first,
+// last) with first = (d0, it0), last = (d1, it1), crossing descriptors where
+// needed (x is restaged in LDS at each crossing). With an iteration table the
+// ranges are balanced by bytes on the host; without one (at most
+// GEMV_INLINE inline descriptors) by iteration count.
+RFXQ_DEV uint32_t gemv_iters(const GemvDesc& d) {
+    const uint32_t rows_iter = 256u >> d.lpr_log2;
+    return (d.n + rows_iter - 1u) / rows_iter;
 }
 
+// (a pointer into the kernel arguments, so a runtime index is a scalar load
+// rather than a register copy of the whole array)
+RFXQ_DEV const GemvDesc* gemv_desc(const GemvArgs& a, uint32_t i) {
+    return a.ndesc > GEMV_INLINE ? a.table + i : &a.inl[0] + i;
+}
+
+// A descriptor read into scalar registers: every field is marked wave-uniform,
+// so the weight buffer's V# stays in SGPRs (a V# the compiler thinks may
+// differ per lane turns each buffer load into a loop over lanes).
+RFXQ_DEV GemvDesc gemv_uniform(const GemvDesc* p) {
+    struct Words {
+        uint32_t v[sizeof(GemvDesc) / 4];
+    };
+    Words w = *reinterpret_cast<const Words*>(p);
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(GemvDesc) / 4; i++) w.v[i] = __builtin_amdgcn_readfirstlane(w.v[i]);
+    return __builtin_bit_cast(GemvDesc, w);
+}
+
+// LDS: [part_floats] row partials (rows with several passes), then x as f16
+// (k * 2 bytes) and the per-16 x sums (k / 4 bytes).
 extern "C" __global__ __launch_bounds__(256) void rfxq_gemv(GemvArgs args) {
     extern __shared__ uint32_t lds[];
-    const GemvDesc d = gemv_pick(args, blockIdx.x);
-    const uint32_t rb = (blockIdx.x - d.wg_begin) * d.rows_per_wg;
-    const uint32_t re = min(d.n, rb + d.rows_per_wg);
-    uint32_t* lds_x = lds;
-    float* lds_s = reinterpret_cast<float*>(lds + d.k / 2u);
-    gemv_stage_x(d.x, d.k, d.type == TY_Q4K, lds_x, lds_s);
-    if (d.type == TY_Q4K) gemv_dispatch_lpr<TY_Q4K>(d, rb, re, lds_x, lds_s);
-    else if (d.type == TY_Q6K) gemv_dispatch_lpr<TY_Q6K>(d, rb, re, lds_x, lds_s);
-    else gemv_dispatch_lpr<TY_Q8_0>(d, rb, re, lds_x, lds_s);
+    uint32_t d0, it0, d1, it1;
+    if (args.ranges) {
+        const uint4 r = args.ranges[blockIdx.x];
+        d0 = __builtin_amdgcn_readfirstlane(r.x);
+        it0 = __builtin_amdgcn_readfirstlane(r.y);
+        d1 = __builtin_amdgcn_readfirstlane(r.z);
+        it1 = __builtin_amdgcn_readfirstlane(r.w);
+    } else {
+        uint32_t total = 0, cnt[GEMV_INLINE];
+        for (uint32_t i = 0; i < args.ndesc; i++) total += cnt[i] = gemv_iters(args.inl[i]);
+        uint32_t g0 = (uint32_t)(((uint64_t)total * blockIdx.x) / gridDim.x);
+        uint32_t g1 = (uint32_t)(((uint64_t)total * (blockIdx.x + 1u)) / gridDim.x);
+        d0 = 0;
+        while (d0 + 1u < args.ndesc && g0 >= cnt[d0]) g0 -= cnt[d0++];
+        d1 = 0;
+        while (d1 + 1u < args.ndesc && g1 > cnt[d1]) g1 -= cnt[d1++];
+        it0 = g0;
+        it1 = g1;
+    }
+    bool restage = false;
+    for (uint32_t di = d0; di <= d1; di++) {
+        const GemvDesc d = gemv_uniform(gemv_desc(args, di));
+        const uint32_t a = di == d0 ? it0 : 0u;
+        const uint32_t b = di == d1 ? it1 : gemv_iters(d);
+        if (a >= b) continue;
+        const uint32_t rows_iter = 256u >> d.lpr_log2;
+        const uint32_t rb = a * rows_iter, re = min(d.n, b * rows_iter);
+        float* lds_p = reinterpret_cast<float*>(lds);
+        uint32_t* lds_x = lds + args.part_floats;
+        float* lds_s = reinterpret_cast<float*>(lds_x + d.k / 2u);
+        if (d.type == TY_Q4K) gemv_dispatch_lpr<Q4K>(d, rb, re, restage, lds_x, lds_s, lds_p);
+        else if (d.type == TY_Q6K) gemv_dispatch_lpr<Q6K>(d, rb, re, restage, lds_x, lds_s, lds_p);
+        else gemv_dispatch_lpr<Q80>(d, rb, re, restage, lds_x, lds_s, lds_p);
+        restage = true;
+    }
 }

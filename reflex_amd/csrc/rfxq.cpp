@@ -65,12 +65,16 @@ struct GemvDesc {
     const float* x;
     float* y;
     uint32_t k, n, type, lpr_log2;
-    uint32_t rows_per_wg, wg_begin, pad0, pad1;
+    uint32_t pad[4];
 };
 constexpr uint32_t kGemvInline = 4;
+struct GemvRange {
+    uint32_t d0, it0, d1, it1;
+};
 struct GemvArgs {
     const GemvDesc* table;
-    uint32_t ndesc, pad;
+    const GemvRange* ranges;
+    uint32_t ndesc, part_floats;
     GemvDesc inl[kGemvInline];
 };
 static_assert(sizeof(GemvDesc) == 56, "GemvDesc layout");
@@ -95,6 +99,8 @@ struct MmqArgs {
 static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
 
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
+
+constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup
 constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 
 // ------------------------------------------------------------------ per-device module
@@ -262,10 +268,22 @@ uint32_t env_u32(const char* name, uint32_t dflt) {
 
 // ------------------------------------------------------------------ GEMV planning
 
-int make_gemv_desc(const Ctx* c, const float* x, const rfxq_weight* w, float* y, GemvDesc* d, uint32_t* wgs,
-                   uint32_t* lds) {
+// One GEMV of a launch: its descriptor and how its rows split into row
+// iterations (4 * 64 / LPR rows: one lane group per wave and row).
+struct GemvItem {
+    GemvDesc d;
+    uint32_t iters, rows_iter;
+    uint64_t iter_bytes;
+    bool passes;  // several units per lane: row partials in LDS
+};
+
+int make_gemv_item(const float* x, const rfxq_weight* w, float* y, GemvItem* it) {
     if (int rc = check_weight(w, "gemv")) return rc;
     const uint32_t k = w->in_features, n = w->out_features;
+    // buffer offsets are 32-bit and 0xFFFFF000 marks "past the end"
+    if (row_bytes(w->ggml_type, k) * n >= 0xFFFFF000ull - 4096u)
+        return fail(RFXQ_ERR_OTHER, "gemv: weight of %llu bytes exceeds the 4 GiB buffer-offset range",
+                    (unsigned long long)(row_bytes(w->ggml_type, k) * n));
     if (k > kMaxGemvK) return fail(RFXQ_ERR_OTHER, "gemv: in_features=%u exceeds %u", k, kMaxGemvK);
     if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemv: x or y is NULL");
     if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemv: x is not 16-byte aligned");
@@ -278,13 +296,8 @@ int make_gemv_desc(const Ctx* c, const float* x, const rfxq_weight* w, float* y,
         // Q8_0 with k/32 not a multiple of 4: not supported by the lane mapping
         return fail(RFXQ_ERR_OTHER, "gemv: %s in_features=%u needs k/32 %% 4 == 0", type_name(w->ggml_type), k);
     }
-    const uint32_t rpi = 64u >> lpr_log2;
-    const uint32_t rows_iter = 4u * rpi;
-    const uint32_t iters_total = (n + rows_iter - 1u) / rows_iter;
-    const uint32_t target = env_u32("RFXQ_GEMV_WGS", 4u * (uint32_t)c->cus);
-    const uint32_t iters = std::max(1u, (iters_total + target - 1u) / target);
-    const uint32_t rows_per_wg = rows_iter * iters;
-    std::memset(d, 0, sizeof *d);
+    std::memset(it, 0, sizeof *it);
+    GemvDesc* d = &it->d;
     d->w = w->data;
     d->x = x;
     d->y = y;
@@ -292,39 +305,106 @@ int make_gemv_desc(const Ctx* c, const float* x, const rfxq_weight* w, float* y,
     d->n = n;
     d->type = w->ggml_type;
     d->lpr_log2 = lpr_log2;
-    d->rows_per_wg = rows_per_wg;
-    *wgs = (n + rows_per_wg - 1u) / rows_per_wg;
-    *lds = k * 2u + k / 4u;
+    it->rows_iter = 256u >> lpr_log2;
+    it->iters = (n + it->rows_iter - 1u) / it->rows_iter;
+    it->iter_bytes = row_bytes(w->ggml_type, k) * it->rows_iter;
+    it->passes = (units >> lpr_log2) > 1u;
     return RFXQ_OK;
 }
 
-int gemv_launch_descs(Ctx* c, GemvDesc* descs, uint32_t count, uint32_t total_wgs, uint32_t lds,
-                      const GemvDesc* table, hipStream_t stream) {
+// Workgroups of a launch: about RFXQ_GEMV_WG_KB (default 128) KB of weights
+// each, so the x staging is amortised and each wave's load ring reaches a
+// steady state; launches too small for 2 workgroups per CU at that size use
+// smaller ranges (down to one iteration).
+uint32_t gemv_grid(const Ctx* c, uint64_t total_iters, uint64_t total_bytes) {
+    const uint64_t kb = std::max<uint32_t>(1u, env_u32("RFXQ_GEMV_WG_KB", 128));
+    uint64_t g = (total_bytes + kb * 1024u - 1u) / (kb * 1024u);
+    g = std::max<uint64_t>(g, 2u * (uint32_t)c->cus);
+    return (uint32_t)std::max<uint64_t>(1u, std::min<uint64_t>(g, total_iters));
+}
+
+// LDS bytes for a launch whose workgroups hold at most `max_iters` iterations
+// of one GEMV: row partials for several-pass rows, then x (f16) and x sums.
+int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_iters, uint32_t* part_floats,
+             uint32_t* lds) {
+    uint32_t part = 0, kmax = 0;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (v[i].passes) part = std::max(part, max_iters[i] * v[i].rows_iter);
+        kmax = std::max(kmax, v[i].d.k);
+    }
+    *part_floats = part;
+    *lds = part * 4u + kmax * 2u + kmax / 4u;
+    if (*lds > kMaxLds) return fail(RFXQ_ERR_OTHER, "gemv: launch needs %u bytes of LDS", *lds);
+    return RFXQ_OK;
+}
+
+// Up to kGemvInline GEMVs in one launch, descriptors inline; the kernel splits
+// the iterations evenly by count over the grid.
+int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t stream) {
+    uint64_t total = 0, bytes = 0;
+    for (const auto& it : v) {
+        total += it.iters;
+        bytes += it.iters * it.iter_bytes;
+    }
+    const uint32_t grid = gemv_grid(c, total, bytes);
+    const uint32_t per_wg = (uint32_t)((total + grid - 1u) / grid);  // no range holds more iterations
+    std::vector<uint32_t> max_iters(v.size());
+    for (size_t i = 0; i < v.size(); i++) max_iters[i] = std::min(per_wg, v[i].iters);
     GemvArgs a;
     std::memset(&a, 0, sizeof a);
-    a.ndesc = count;
-    a.table = table;
-    if (count <= kGemvInline) std::copy(descs, descs + count, a.inl);
-    return launch(c->gemv, total_wgs, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+    uint32_t lds;
+    if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
+    a.ndesc = (uint32_t)v.size();
+    for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
+    return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
 }
 
-// Up to kGemvInline GEMVs per launch, descriptors passed inline.
 int gemv_items(Ctx* c, const rfxq_gemv_item* items, uint32_t count, hipStream_t stream) {
-    for (uint32_t base = 0; base < count; base += kGemvInline) {
-        const uint32_t cnt = std::min(kGemvInline, count - base);
-        GemvDesc d[kGemvInline];
-        uint32_t total = 0, lds = 0;
-        for (uint32_t i = 0; i < cnt; i++) {
-            uint32_t wgs, l;
-            if (int rc = make_gemv_desc(c, items[base + i].x, items[base + i].w, items[base + i].y, &d[i], &wgs, &l))
-                return rc;
-            d[i].wg_begin = total;
-            total += wgs;
-            lds = std::max(lds, l);
+    for (uint32_t i0 = 0; i0 < count; i0 += kGemvInline) {
+        const uint32_t cnt = std::min<uint32_t>(kGemvInline, count - i0);
+        std::vector<GemvItem> v(cnt);
+        for (uint32_t j = 0; j < cnt; j++) {
+            const rfxq_gemv_item& it = items[i0 + j];
+            if (int rc = make_gemv_item(it.x, it.w, it.y, &v[j])) return rc;
         }
-        if (int rc = gemv_launch_descs(c, d, cnt, total, lds, nullptr, stream)) return rc;
+        if (int rc = gemv_launch_inline(c, v, stream)) return rc;
     }
     return RFXQ_OK;
+}
+
+// A plan's ranges, balanced by bytes: workgroup g starts at the first
+// iteration (in descriptor order) whose start lies at or after g/grid of all
+// weight bytes; the last range ends at the end of the last descriptor.
+void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector<GemvRange>* ranges,
+                      std::vector<uint32_t>* max_iters) {
+    uint64_t total = 0;
+    for (const auto& it : v) total += it.iters * it.iter_bytes;
+    std::vector<std::pair<uint32_t, uint32_t>> start(grid + 1u);
+    uint32_t g = 0;
+    uint64_t pos = 0;
+    for (uint32_t d = 0; d < v.size() && g < grid; d++) {
+        for (uint32_t i = 0; i < v[d].iters && g < grid; i++) {
+            while (g < grid && pos >= (total * g + grid - 1u) / grid) start[g++] = {d, i};
+            pos += v[d].iter_bytes;
+        }
+    }
+    while (g < grid) start[g++] = {(uint32_t)v.size() - 1u, v.back().iters};  // empty tail ranges
+    start[grid] = {(uint32_t)v.size() - 1u, v.back().iters};
+    ranges->resize(grid);
+    max_iters->assign(v.size(), 0u);
+    for (uint32_t w = 0; w < grid; w++) {
+        GemvRange r{start[w].first, start[w].second, start[w + 1u].first, start[w + 1u].second};
+        // an end at iteration 0 of a descriptor is the end of the one before
+        while (r.d1 > r.d0 && r.it1 == 0u) {
+            r.d1--;
+            r.it1 = v[r.d1].iters;
+        }
+        (*ranges)[w] = r;
+        for (uint32_t d = r.d0; d <= r.d1; d++) {
+            const uint32_t a = d == r.d0 ? r.it0 : 0u, b = d == r.d1 ? r.it1 : v[d].iters;
+            if (b > a) (*max_iters)[d] = std::max((*max_iters)[d], b - a);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ MMQ planning
@@ -498,9 +578,9 @@ int expert_slice(const rfxq_weight* w, uint32_t e, rfxq_weight* out, const char*
 
 struct rfxq_gemv_plan {
     int device;
-    GemvDesc* table;
-    std::vector<GemvDesc> host;
-    uint32_t total_wgs, lds;
+    void* dev = nullptr;  // descriptor table, then the per-workgroup ranges
+    GemvArgs args;
+    uint32_t grid = 0, lds = 0;
 };
 
 extern "C" {
@@ -583,9 +663,8 @@ int rfxq_gemv_batch(const rfxq_gemv_item* items, uint32_t count, hipStream_t str
     if (int rc = current_ctx(&c)) return rc;
     // validate everything before launching anything
     for (uint32_t i = 0; i < count; i++) {
-        GemvDesc d;
-        uint32_t wgs, lds;
-        if (int rc = make_gemv_desc(c, items[i].x, items[i].w, items[i].y, &d, &wgs, &lds)) return rc;
+        GemvItem it;
+        if (int rc = make_gemv_item(items[i].x, items[i].w, items[i].y, &it)) return rc;
     }
     if (int rc = gemv_items(c, items, count, stream)) return rc;
     return ok();
@@ -601,30 +680,41 @@ int rfxq_gemv_plan_create(const rfxq_gemv_item* items, uint32_t count, int devic
     int rc = load_ctx(device, &c);
     auto plan = std::make_unique<rfxq_gemv_plan>();
     plan->device = device;
-    plan->table = nullptr;
-    plan->total_wgs = 0;
-    plan->lds = 0;
-    plan->host.resize(count);
-    for (uint32_t i = 0; rc == RFXQ_OK && i < count; i++) {
-        uint32_t wgs, lds;
-        rc = make_gemv_desc(c, items[i].x, items[i].w, items[i].y, &plan->host[i], &wgs, &lds);
-        if (rc == RFXQ_OK) {
-            plan->host[i].wg_begin = plan->total_wgs;
-            plan->total_wgs += wgs;
-            plan->lds = std::max(plan->lds, lds);
+    std::vector<GemvItem> v(count);
+    for (uint32_t i = 0; rc == RFXQ_OK && i < count; i++) rc = make_gemv_item(items[i].x, items[i].w, items[i].y, &v[i]);
+    std::vector<GemvRange> ranges;
+    std::vector<uint32_t> max_iters;
+    if (rc == RFXQ_OK) {
+        uint64_t total = 0, bytes = 0;
+        for (const auto& it : v) {
+            total += it.iters;
+            bytes += it.iters * it.iter_bytes;
         }
+        plan->grid = gemv_grid(c, total, bytes);
+        gemv_split_bytes(v, plan->grid, &ranges, &max_iters);
+        std::memset(&plan->args, 0, sizeof plan->args);
+        plan->args.ndesc = count;
+        rc = gemv_lds(v, max_iters, &plan->args.part_floats, &plan->lds);
     }
-    if (rc == RFXQ_OK && count > kGemvInline) {
-        hipError_t e = hipMalloc(reinterpret_cast<void**>(&plan->table), sizeof(GemvDesc) * count);
+    if (rc == RFXQ_OK) {
+        const size_t tb = sizeof(GemvDesc) * count, rbytes = sizeof(GemvRange) * ranges.size();
+        std::vector<uint8_t> host(tb + rbytes);
+        for (uint32_t i = 0; i < count; i++) std::memcpy(host.data() + i * sizeof(GemvDesc), &v[i].d, sizeof(GemvDesc));
+        std::memcpy(host.data() + tb, ranges.data(), rbytes);
+        hipError_t e = hipMalloc(&plan->dev, host.size());
         if (e != hipSuccess) rc = fail(RFXQ_ERR_OUT_OF_MEMORY, "gemv_plan_create: %s", hipGetErrorString(e));
         else {
-            e = hipMemcpy(plan->table, plan->host.data(), sizeof(GemvDesc) * count, hipMemcpyHostToDevice);
+            e = hipMemcpy(plan->dev, host.data(), host.size(), hipMemcpyHostToDevice);
             if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemv_plan_create upload: %s", hipGetErrorString(e));
         }
+        plan->args.table = static_cast<const GemvDesc*>(plan->dev);
+        plan->args.ranges = reinterpret_cast<const GemvRange*>(static_cast<const uint8_t*>(plan->dev) + tb);
+        if (count <= kGemvInline)
+            for (uint32_t i = 0; i < count; i++) plan->args.inl[i] = v[i].d;
     }
     (void)hipSetDevice(prev);
     if (rc != RFXQ_OK) {
-        if (plan->table) (void)hipFree(plan->table);
+        if (plan->dev) (void)hipFree(plan->dev);
         return rc;
     }
     *out = plan.release();
@@ -635,16 +725,14 @@ int rfxq_gemv_plan_run(const rfxq_gemv_plan* plan, hipStream_t stream) {
     if (!plan) return fail(RFXQ_ERR_INVALID_INPUT, "gemv_plan_run: NULL plan");
     Ctx* c;
     if (int rc = load_ctx(plan->device, &c)) return rc;
-    GemvDesc tmp[kGemvInline];
-    const uint32_t n = (uint32_t)plan->host.size();
-    if (n <= kGemvInline) std::copy(plan->host.begin(), plan->host.end(), tmp);
-    if (int rc = gemv_launch_descs(c, tmp, n, plan->total_wgs, plan->lds, plan->table, stream)) return rc;
+    GemvArgs a = plan->args;
+    if (int rc = launch(c->gemv, plan->grid, plan->lds, stream, &a, sizeof a, "rfxq_gemv launch")) return rc;
     return ok();
 }
 
 void rfxq_gemv_plan_destroy(rfxq_gemv_plan* plan) {
     if (!plan) return;
-    if (plan->table) (void)hipFree(plan->table);
+    if (plan->dev) (void)hipFree(plan->dev);
     delete plan;
 }
 

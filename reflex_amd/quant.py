@@ -247,7 +247,8 @@ class GemvPlan:
         self._tensors = items
         h = ctypes.c_void_p()
         dev = items[0][0].device.index or 0
-        _check(lib().rfxq_gemv_plan_create(arr, len(items), dev, ctypes.byref(h)))
+        self._lib = lib()  # kept so that __del__ works during interpreter shutdown
+        _check(self._lib.rfxq_gemv_plan_create(arr, len(items), dev, ctypes.byref(h)))
         self._h = h
 
     def run(self) -> None:
@@ -255,7 +256,7 @@ class GemvPlan:
 
     def __del__(self):
         if getattr(self, "_h", None):
-            lib().rfxq_gemv_plan_destroy(self._h)
+            self._lib.rfxq_gemv_plan_destroy(self._h)
             self._h = None
 
 
