@@ -29,7 +29,7 @@ DEVICE_FLAGS = [
     # packed FP32 instructions stay disabled in every HIP compile of this project
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-variable",
-]
+] + os.environ.get("RFXQ_EXTRA_DEVICE_FLAGS", "").split()
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

@@ -10,6 +10,7 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
 #define RFXQ_DEV static __device__ __forceinline__
 
@@ -19,6 +20,11 @@ enum : uint32_t { TY_Q8_0 = 8, TY_Q4K = 12, TY_Q6K = 14 };
 RFXQ_DEV float f16_bits_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(half_t, (uint16_t)(bits16 & 0xFFFFu));
 }
+
+// Bits of a u32 as f32. Takes its argument by value: __builtin_bit_cast
+// applied directly to an ext-vector element (v.y) reads element 0 in this
+// compiler, so vector elements go through here.
+RFXQ_DEV float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
 
 RFXQ_DEV h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 RFXQ_DEV uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
@@ -56,6 +62,65 @@ RFXQ_DEV u4_t bld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer
 RFXQ_DEV uint32_t bld4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
 RFXQ_DEV void bst4f(rsrc_t r, uint32_t off, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+
+// 32-bit LDS address of a pointer into shared memory
+RFXQ_DEV uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Workgroup barrier that orders LDS only: earlier LDS accesses of the wave are
+// complete, global loads and asynchronous copies may still be in flight
+// (__syncthreads would also wait for those, as they write LDS).
+RFXQ_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS accesses hidden from the compiler's wait counting. A compiler-visible
+// LDS access that may alias a buffer_load ... lds destination makes it wait
+// for every copy in flight (vmcnt(0)); kernels that stream weights through LDS
+// copies use these for their other LDS traffic and order the copies with
+// explicit vmcnt waits. Reads wait for their own data (lgkmcnt(0)); their
+// outputs are early-clobber, as the reads land after later ones issue.
+RFXQ_DEV void lds_st32(uint32_t a, uint32_t v) { asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory"); }
+RFXQ_DEV void lds_st64(uint32_t a, u2_t v) { asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory"); }
+RFXQ_DEV uint32_t lds_ld32(uint32_t a) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return v;
+}
+RFXQ_DEV u2_t lds_ld64(uint32_t a) {
+    u2_t v;
+    asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return v;
+}
+RFXQ_DEV u4_t lds_ld128(uint32_t a) {
+    u4_t v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return v;
+}
+// two 16-byte reads at a and a + 16
+RFXQ_DEV void lds_ld2x128(uint32_t a, u4_t& v0, u4_t& v1) {
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v0), "=&v"(v1)
+                 : "v"(a)
+                 : "memory");
+}
+// four 16-byte reads at a, a + 16, a + 32, a + 48
+RFXQ_DEV void lds_ld4x128(uint32_t a, u4_t& v0, u4_t& v1, u4_t& v2, u4_t& v3) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\t"
+        "ds_read_b128 %2, %4 offset:32\n\tds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+        : "v"(a)
+        : "memory");
+}
+RFXQ_DEV uint4 as_uint4(u4_t v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+// Asynchronous copy global -> LDS (buffer_load ... lds): each lane's `size`
+// bytes from its own buffer offset land at lds_base + lane * size. lds_base
+// must be wave-uniform. Lanes reading past the buffer write zeros.
+#define RFXQ_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
+RFXQ_DEV void dma16(rsrc_t r, void* lds_base, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RFXQ_LDSP(lds_base), 16, off, 0, 0, 0);
 }
 
 RFXQ_DEV uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t shift_bytes) {

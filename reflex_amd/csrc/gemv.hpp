@@ -71,10 +71,7 @@ RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, bool prescale_hi
     const float sc = (prescale_hi && (e & 32u)) ? 0.0625f : 1.0f;
     const h2_t a = {(half_t)(v.x * sc), (half_t)(v.z * sc)};
     const h2_t b = {(half_t)(v.y * sc), (half_t)(v.w * sc)};
-    uint2 st;
-    st.x = h2_bits(a);
-    st.y = h2_bits(b);
-    *reinterpret_cast<uint2*>(lds_x + e / 2u) = st;
+    lds_st64(lds_addr(lds_x) + 2u * e, u2_t{h2_bits(a), h2_bits(b)});
 }
 
 RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
@@ -85,11 +82,11 @@ RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescal
         if (e < k) gemv_x_put(lds_x, e, xr.v[i], prescale_hi);
     }
     for (uint32_t e = 4u * tid + 4096u; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), prescale_hi);
-    __syncthreads();
+    lds_barrier();
     const uint32_t ng = k / 16u;
     for (uint32_t g = tid; g < ng; g += 256u) {
-        const uint4 p0 = *reinterpret_cast<const uint4*>(lds_x + 8u * g);
-        const uint4 p1 = *reinterpret_cast<const uint4*>(lds_x + 8u * g + 4u);
+        u4_t p0, p1;
+        lds_ld2x128(lds_addr(lds_x) + 32u * g, p0, p1);
         const uint32_t one2 = 0x3C003C00u;
         float s = 0.0f;
         s = dot2(p0.x, one2, s);
@@ -100,9 +97,9 @@ RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescal
         s = dot2(p1.y, one2, s);
         s = dot2(p1.z, one2, s);
         s = dot2(p1.w, one2, s);
-        lds_s[g] = s;
+        lds_st32(lds_addr(lds_s) + 4u * g, __builtin_bit_cast(uint32_t, s));
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 RFXQ_DEV uint32_t u4_at(const uint4* a, int j) {
@@ -116,13 +113,14 @@ RFXQ_DEV uint32_t u4_at(const uint4* a, int j) {
 // quarter super-block), 32 for Q8_0 (one block). Each type provides
 //   Raw      the unit's raw bytes as loaded (kept in registers while in flight)
 //   XV       the unit's x values (from LDS) and x sums
-//   load()   issue the global loads of a unit
+//   fetch()  read a unit's bytes from an LDS copy of its row chunk
 //   loadx()  read the unit's x from LDS
 //   dot()    the unit's contribution to the row's dot product
 
 struct Q4K {
     static constexpr uint32_t QK = 256, BB = 144, UPB = 4;  // units per block
-    static constexpr int PF = 2;                            // items in flight per wave
+    static constexpr bool ALIGNED = true;  // blocks (and rows) start 16-byte aligned
+    static constexpr int NJ = 3;           // 1 KB copy instructions per item (64 x 36 B)
     struct Raw {
         u4_t hdr, qa, qb;
     };
@@ -133,19 +131,37 @@ struct Q4K {
     static RFXQ_DEV uint32_t xoff(uint32_t unit) { return 256u * (unit >> 2) + 64u * (unit & 3u); }
     // byte offset of the unit's block within a row
     static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return (unit >> 2) * BB; }
-    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t unit) {
-        const uint32_t q = off + 16u + 32u * (unit & 3u);
-        return Raw{bld16(w, off), bld16(w, q), bld16(w, q + 16u)};
+    // the unit's bytes from its block at slot byte o (16-byte aligned)
+    static RFXQ_DEV Raw fetch(const uint8_t* slot, uint32_t o, uint32_t unit) {
+        const uint32_t a = lds_addr(slot) + o;
+        const uint32_t q = a + 16u + 32u * (unit & 3u);
+        Raw r;
+        asm volatile(
+            "ds_read_b128 %0, %3\n\t"
+            "ds_read_b128 %1, %4\n\t"
+            "ds_read_b128 %2, %4 offset:16\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r.hdr), "=&v"(r.qa), "=&v"(r.qb)
+            : "v"(a), "v"(q)
+            : "memory");
+        return r;
     }
     static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
         const uint32_t o = xoff(unit);
-        const uint4* p = reinterpret_cast<const uint4*>(lds_x + o / 2u);
+        const uint32_t a = lds_addr(lds_x) + 2u * o;
+        u4_t v[8];
+        lds_ld4x128(a, v[0], v[1], v[2], v[3]);
+        lds_ld4x128(a + 64u, v[4], v[5], v[6], v[7]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) x.l[i] = p[i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x.h[i] = p[4 + i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x.s[i] = lds_s[o / 16u + i];
+        for (int i = 0; i < 4; i++) {
+            x.l[i] = as_uint4(v[i]);
+            x.h[i] = as_uint4(v[4 + i]);
+        }
+        const u4_t sm = lds_ld128(lds_addr(lds_s) + 4u * (o / 16u));
+        x.s[0] = as_f32(sm.x);
+        x.s[1] = as_f32(sm.y);
+        x.s[2] = as_f32(sm.z);
+        x.s[3] = as_f32(sm.w);
     }
     // qs bytes [32g, 32g+32) = sub-blocks 2g (low nibbles) and 2g+1 (high).
     // The 6-bit scales/mins of sub-blocks j = 2g, 2g+1 (g = unit & 3, fixed
@@ -185,13 +201,11 @@ struct Q4K {
 
 // 16 bytes at byte offset o of a 2-byte-aligned block: four dwords from the
 // dword-aligned offset below plus one more, realigned by sh = 0 or 2 bytes.
-// Buffer loads return 0 past the end of the weights, so the extra dword is
-// always safe.
 struct Seg {
     u4_t v;
     uint32_t e;
 };
-RFXQ_DEV Seg seg_load(rsrc_t w, uint32_t off4) { return Seg{bld16(w, off4), bld4(w, off4 + 16u)}; }
+
 RFXQ_DEV u4_t seg_align(const Seg& s, uint32_t sh) {
     u4_t r;
     r.x = alignbyte(s.v.y, s.v.x, sh);
@@ -203,7 +217,8 @@ RFXQ_DEV u4_t seg_align(const Seg& s, uint32_t sh) {
 
 struct Q6K {
     static constexpr uint32_t QK = 256, BB = 210, UPB = 4;
-    static constexpr int PF = 2;
+    static constexpr bool ALIGNED = false;  // blocks are 2-byte aligned
+    static constexpr int NJ = 4;            // 64 x 52.5 B plus per-row alignment slack
     struct Raw {
         Seg a, c, h;
         u4_t sw;
@@ -219,26 +234,48 @@ struct Q6K {
         return 256u * (unit >> 2) + 128u * (g >> 1) + 16u * (g & 1u);
     }
     static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return (unit >> 2) * BB; }
-    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t unit) {
+    // dword-aligned reads (the block may start 2 bytes past a dword)
+    static RFXQ_DEV Raw fetch(const uint8_t* slot, uint32_t o, uint32_t unit) {
         const uint32_t g = unit & 3u, n = g >> 1, hs = g & 1u;
-        const uint32_t a4 = off & ~3u;  // blocks are 2-byte aligned
+        const uint32_t a4 = lds_addr(slot) + (o & ~3u);
+        const uint32_t pa = a4 + 64u * n + 16u * hs, ph = a4 + 128u + 32u * n + 16u * hs;
         Raw r;
-        r.sh = off & 3u;
-        r.a = seg_load(w, a4 + 64u * n + 16u * hs);
-        r.c = seg_load(w, a4 + 64u * n + 32u + 16u * hs);
-        r.h = seg_load(w, a4 + 128u + 32u * n + 16u * hs);
-        r.sw = bld16(w, a4 + 192u);  // scales (192..207)
-        r.tail = bld4(w, a4 + 208u); // d (208..209)
+        r.sh = o & 3u;
+        u2_t a01, a23, c01, c23, h01, h23, s01, s23, ae_ce, he_t;
+        asm volatile(
+            "ds_read2_b32 %0, %10 offset1:1\n\t"
+            "ds_read2_b32 %1, %10 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %2, %10 offset0:8 offset1:9\n\t"
+            "ds_read2_b32 %3, %10 offset0:10 offset1:11\n\t"
+            "ds_read2_b32 %4, %11 offset1:1\n\t"
+            "ds_read2_b32 %5, %11 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %6, %12 offset0:48 offset1:49\n\t"
+            "ds_read2_b32 %7, %12 offset0:50 offset1:51\n\t"
+            "ds_read2_b32 %8, %10 offset0:4 offset1:12\n\t"
+            "ds_read2_b32 %9, %11 offset0:4\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(a01), "=&v"(a23), "=&v"(c01), "=&v"(c23), "=&v"(h01), "=&v"(h23), "=&v"(s01), "=&v"(s23),
+              "=&v"(ae_ce), "=&v"(he_t)
+            : "v"(pa), "v"(ph), "v"(a4)
+            : "memory");
+        uint32_t tail;
+        asm volatile("ds_read_b32 %0, %1 offset:208\n\ts_waitcnt lgkmcnt(0)" : "=&v"(tail) : "v"(a4) : "memory");
+        r.a = Seg{u4_t{a01.x, a01.y, a23.x, a23.y}, ae_ce.x};
+        r.c = Seg{u4_t{c01.x, c01.y, c23.x, c23.y}, ae_ce.y};
+        r.h = Seg{u4_t{h01.x, h01.y, h23.x, h23.y}, he_t.x};
+        r.sw = u4_t{s01.x, s01.y, s23.x, s23.y};
+        r.tail = tail;
         return r;
     }
     static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
         const uint32_t o = xoff(unit);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const uint4* p = reinterpret_cast<const uint4*>(lds_x + (o + 32u * t) / 2u);
-            x.r[t][0] = p[0];
-            x.r[t][1] = p[1];
-            x.s[t] = lds_s[o / 16u + 2u * t];
+            u4_t v0, v1;
+            lds_ld2x128(lds_addr(lds_x) + 2u * (o + 32u * t), v0, v1);
+            x.r[t][0] = as_uint4(v0);
+            x.r[t][1] = as_uint4(v1);
+            x.s[t] = __builtin_bit_cast(float, lds_ld32(lds_addr(lds_s) + 4u * (o / 16u + 2u * t)));
         }
     }
     static RFXQ_DEV float dot(const Raw& r, uint32_t unit, const XV& x, uint32_t MG) {
@@ -279,7 +316,8 @@ struct Q6K {
 
 struct Q80 {
     static constexpr uint32_t QK = 32, BB = 34, UPB = 1;
-    static constexpr int PF = 4;
+    static constexpr bool ALIGNED = false;  // blocks are 2-byte aligned
+    static constexpr int NJ = 3;            // 64 x 34 B plus per-row alignment slack
     struct Raw {
         u4_t w0, w1;
         uint32_t w8, sh;
@@ -291,22 +329,34 @@ struct Q80 {
     static RFXQ_DEV uint32_t xoff(uint32_t unit) { return unit * 32u; }
     static RFXQ_DEV uint32_t unit_off(uint32_t unit) { return unit * BB; }
     // one 34-byte block (2-byte aligned): 9 dwords from the dword-aligned offset
-    static RFXQ_DEV Raw load(rsrc_t w, uint32_t off, uint32_t) {
-        const uint32_t a4 = off & ~3u;
+    static RFXQ_DEV Raw fetch(const uint8_t* slot, uint32_t o, uint32_t) {
+        const uint32_t a4 = lds_addr(slot) + (o & ~3u);
         Raw r;
-        r.sh = off & 3u;
-        r.w0 = bld16(w, a4);
-        r.w1 = bld16(w, a4 + 16u);
-        r.w8 = bld4(w, a4 + 32u);
+        r.sh = o & 3u;
+        u2_t d01, d23, d45, d67;
+        asm volatile(
+            "ds_read2_b32 %0, %5 offset1:1\n\t"
+            "ds_read2_b32 %1, %5 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %2, %5 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %3, %5 offset0:6 offset1:7\n\t"
+            "ds_read_b32 %4, %5 offset:32\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(d01), "=&v"(d23), "=&v"(d45), "=&v"(d67), "=&v"(r.w8)
+            : "v"(a4)
+            : "memory");
+        r.w0 = u4_t{d01.x, d01.y, d23.x, d23.y};
+        r.w1 = u4_t{d45.x, d45.y, d67.x, d67.y};
         return r;
     }
     static RFXQ_DEV void loadx(const uint32_t* lds_x, const float* lds_s, uint32_t unit, XV& x) {
         const uint32_t o = xoff(unit);
-        const uint4* p = reinterpret_cast<const uint4*>(lds_x + o / 2u);
+        u4_t v[4];
+        lds_ld4x128(lds_addr(lds_x) + 2u * o, v[0], v[1], v[2], v[3]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) x.v[i] = p[i];
-        x.s[0] = lds_s[o / 16u];
-        x.s[1] = lds_s[o / 16u + 1u];
+        for (int i = 0; i < 4; i++) x.v[i] = as_uint4(v[i]);
+        const u2_t sm = lds_ld64(lds_addr(lds_s) + 4u * (o / 16u));
+        x.s[0] = as_f32(sm.x);
+        x.s[1] = as_f32(sm.y);
     }
     static RFXQ_DEV float dot(const Raw& r, uint32_t, const XV& x, uint32_t MG) {
 #pragma clang fp contract(off)
@@ -327,29 +377,44 @@ struct Q80 {
 
 // ---------------------------------------------------------------- row loop
 
+// Weight ring: each wave owns kRing slots of kSlotBytes in LDS. One item (one
+// unit per lane: RPI rows x the row chunk of LPR units) is copied into a slot
+// by NJ asynchronous 1 KB copies in which consecutive lanes take consecutive
+// 16-byte pieces of the rows (fully coalesced, and no VGPRs held while the
+// copy is in flight); each lane then reads its own unit from the slot. Every
+// slot is its own array, so the compiler's wait counting knows which copy a
+// read depends on and waits for exactly that one.
+constexpr uint32_t kSlotBytes = 4096;
+#ifndef RFXQ_KRING
+#define RFXQ_KRING 2
+#endif
+constexpr int kRing = RFXQ_KRING;
+__shared__ __attribute__((aligned(16))) uint8_t gemv_ring0[4][kSlotBytes];
+__shared__ __attribute__((aligned(16))) uint8_t gemv_ring1[4][kSlotBytes];
+#if RFXQ_KRING > 2
+__shared__ __attribute__((aligned(16))) uint8_t gemv_ring2[4][kSlotBytes];
+#endif
+
+// Offset for copies past a wave's last item: beyond any weight buffer's range
+// (the host keeps weights below it), so the copy writes zeros and fetches
+// nothing.
+constexpr uint32_t kPastEnd = 0xFFFFF000u;
+
 // Rows are covered by lane groups of LPR lanes; lane li owns units li + u*LPR,
 // u < U. The wave's rows are row_begin + wave*RPI + sub + it*4*RPI (sub =
 // lane / LPR, it < n_it). Work items run pass by pass: pass u walks all of
 // the wave's rows with unit li + u*LPR, so a lane only ever holds the x slice
-// of one unit in registers (reloaded from LDS at each pass start). With U > 1
-// the group-reduced partial of each row is carried between passes in LDS by
-// lane li == 0 of the group (always the same thread, so program order is
-// enough) and added in pass order, so the result does not depend on tiling.
-//
-// Loads run T::PF items ahead in a ring: each slot is refilled right after
-// its math. Refills past the wave's last item read at kPastEnd (zeros, no
-// memory traffic) and are never used. Item bounds are wave-uniform scalar branches.
-// Offset for refills past a wave's last item: beyond any weight buffer's
-// range (the host keeps weights below it), so the load returns zeros without
-// fetching anything.
-constexpr uint32_t kPastEnd = 0xFFFFF000u;
-
+// of one unit in registers (reloaded from LDS at each pass start). Row
+// results go to an LDS row buffer by lane li == 0 of the group; with U > 1
+// the partial is carried there between passes (always the same thread, so
+// program order is enough) and added in pass order, so the result does not
+// depend on tiling. The buffer is stored to y, coalesced, at the end.
 template <typename T, int LPR>
 RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_end, bool restage, uint32_t* lds_x,
                         float* lds_s, float* lds_p) {
 #pragma clang fp contract(off)
     constexpr int RPI = 64 / LPR;
-    constexpr int PF = T::PF;
+    constexpr int NJ = T::NJ;
     // opaque to the optimiser: keeps the lane-derived values of every type and
     // LPR variant from being hoisted out of the segment loop (all of them
     // would then stay live across it)
@@ -375,32 +440,65 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
     const uint32_t n_it = __builtin_amdgcn_readfirstlane(base0 < row_end ? (row_end - base0 + stride - 1u) / stride : 0u);
     const uint32_t n_items = n_it * U;
     const uint32_t row_step = stride * row_bytes;  // bytes between row iterations
-    const uint32_t unit_step = T::unit_off(LPR);   // bytes between a lane's passes
-    const uint32_t off0 = wsh + (base0 + sub) * row_bytes + T::unit_off(li);
-    // this wave's rows of the segment (wave 0 has the most iterations)
-    const uint32_t n_it_max = row_begin < row_end ? (row_end - row_begin + stride - 1u) / stride : 0u;
-    float* part = lds_p + wave * n_it_max * RPI;
+    const uint32_t chunk = T::unit_off(LPR);       // one row's bytes of an item
+    const uint32_t out0 = lds_addr(lds_p);  // row results (and partials), by row - row_begin
 
-    // next item to load: pass lu, row iteration lit (scalar counters)
-    uint32_t lu = n_it ? 0u : U, lit = 0, loff = off0;
-    auto advance = [&]() {
-        loff += row_step;
+    // Slot layout: row r of the item at r * ppr * 16 bytes, its chunk copied
+    // from the dword at or below its start (sh = start & 3 bytes of slack).
+    const uint32_t ppr = T::ALIGNED ? chunk / 16u : (chunk + 3u + 15u) / 16u;
+    uint32_t prb[NJ], pc[NJ];
+    bool pv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const uint32_t p = 64u * j + lane, r = p / ppr;
+        pv[j] = r < (uint32_t)RPI;
+        prb[j] = r * row_bytes;
+        pc[j] = 16u * (p - r * ppr);
+    }
+    const uint32_t uo = sub * ppr * 16u + T::unit_off(li);  // this lane's unit in a slot
+#if RFXQ_KRING > 2
+    uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave], gemv_ring2[wave]};
+#else
+    uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave]};
+#endif
+
+    // next item to copy: pass lu, row iteration lit; S = buffer offset of the
+    // item's first row chunk (scalar)
+    const uint32_t S0 = wsh + base0 * row_bytes;
+    uint32_t lu = n_it ? 0u : U, lit = 0, lS = S0;
+    uint32_t slotS[kRing];
+    auto issue = [&](int t) {
+        const bool valid = lu < U;
+        slotS[t] = lS;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            uint32_t g = lS + prb[j];
+            if (!T::ALIGNED) g &= ~3u;
+            g += pc[j];
+#ifndef RFXQ_NOLOAD
+            dma16(wr, ring[t] + 1024 * j, valid && pv[j] ? g : kPastEnd);
+#else
+            asm volatile("" ::"v"(g));
+#endif
+        }
+        lS += row_step;
         if (++lit == n_it) {
             lit = 0;
             lu++;
-            loff = off0 + lu * unit_step;
+            lS = S0 + lu * chunk;
         }
     };
 
+    // Stores share vmcnt with the copies and may complete out of order with
+    // them, which would break the counted waits below: none may be in flight
+    // (the previous segment's are drained here), and results go to LDS and
+    // are stored after the last wait.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     XRegs xr;
     gemv_x_load(dsc.x, k, xr, tid);
-    typename T::Raw r[PF];
 #pragma unroll
-    for (int t = 0; t < PF; t++) {
-        r[t] = T::load(wr, lu < U ? loff : kPastEnd, li + lu * LPR);
-        advance();
-    }
-    if (restage) __syncthreads();  // every wave is done with the previous segment's x
+    for (int t = 0; t < kRing; t++) issue(t);
+    if (restage) lds_barrier();  // every wave is done with the previous segment's x
     gemv_stage_x(dsc.x, k, T::QK == 256u && T::BB == 144u, xr, lds_x, lds_s, tid);
 
     // f16 1024.0 in both halves, kept in a VGPR: gfx9 VOP3 takes at most one
@@ -410,25 +508,30 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
     typename T::XV xv;
     T::loadx(lds_x, lds_s, li, xv);
     uint32_t cu = 0, cit = 0;  // item being computed
-    for (uint32_t t0 = 0; t0 < n_items; t0 += PF) {
+    for (uint32_t t0 = 0; t0 < n_items; t0 += kRing) {
 #pragma unroll
-        for (int t = 0; t < PF; t++) {
+        for (int t = 0; t < kRing; t++) {
             if (t0 + t < n_items) {
                 const uint32_t unit = li + cu * LPR;
-                float acc = T::dot(r[t], unit, xv, magic);
-                r[t] = T::load(wr, lu < U ? loff : kPastEnd, li + lu * LPR);
-                advance();
+                const uint32_t sh = T::ALIGNED ? 0u : ((slotS[t] + sub * row_bytes) & 3u);
+                // the copies are counted in order: slot t's are done once at
+                // most those of the other kRing - 1 slots are outstanding
+                // (stores issued since only make this wait longer)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * NJ) : "memory");
+#ifndef RFXQ_NOMATH
+                float acc = T::dot(T::fetch(ring[t], uo + sh, unit), unit, xv, magic);
+#else
+                const typename T::Raw rr = T::fetch(ring[t], uo + sh, unit);
+                float acc = 0.f;
+                for (uint32_t i = 0; i < sizeof(rr) / 4; i++) acc += as_f32(reinterpret_cast<const uint32_t*>(&rr)[i] & 0x3FFFFFFFu);
+#endif
+                issue(t);  // after the math: the slot's reads are done
                 acc = group_sum<LPR>(acc);
                 const uint32_t row = base0 + sub + cit * stride;
                 if (li == 0u && row < row_end) {
-                    if (U == 1u) {
-                        bst4f(yr, row * 4u, acc);
-                    } else {
-                        float* p = part + cit * RPI + sub;
-                        if (cu == 0u) *p = acc;
-                        else if (cu + 1u < U) *p += acc;
-                        else bst4f(yr, row * 4u, *p + acc);
-                    }
+                    const uint32_t pa = out0 + 4u * (row - row_begin);
+                    if (cu > 0u) acc = __builtin_bit_cast(float, lds_ld32(pa)) + acc;
+                    lds_st32(pa, __builtin_bit_cast(uint32_t, acc));
                 }
                 if (++cit == n_it) {
                     cit = 0;
@@ -437,6 +540,12 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             }
         }
     }
+    // no copy may land in LDS after the workgroup is gone (or in the next
+    // segment's reads)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    for (uint32_t i = tid; i < row_end - row_begin; i += 256u)
+        bst4f(yr, (row_begin + i) * 4u, __builtin_bit_cast(float, lds_ld32(out0 + 4u * i)));
 }
 
 template <typename T>
@@ -483,7 +592,7 @@ RFXQ_DEV GemvDesc gemv_uniform(const GemvDesc* p) {
     return __builtin_bit_cast(GemvDesc, w);
 }
 
-// LDS: [part_floats] row partials (rows with several passes), then x as f16
+// LDS: [part_floats] row results of the current segment, then x as f16
 // (k * 2 bytes) and the per-16 x sums (k / 4 bytes).
 extern "C" __global__ __launch_bounds__(256) void rfxq_gemv(GemvArgs args) {
     extern __shared__ uint32_t lds[];

@@ -100,7 +100,7 @@ static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
 
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
-constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup
+constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 48 KB weight ring)
 constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 
 // ------------------------------------------------------------------ per-device module
@@ -324,14 +324,16 @@ uint32_t gemv_grid(const Ctx* c, uint64_t total_iters, uint64_t total_bytes) {
 }
 
 // LDS bytes for a launch whose workgroups hold at most `max_iters` iterations
-// of one GEMV: row partials for several-pass rows, then x (f16) and x sums.
+// of one GEMV: a row buffer (results and several-pass partials; a multiple of
+// 4 floats so x stays 16-byte aligned), then x (f16) and x sums.
 int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_iters, uint32_t* part_floats,
              uint32_t* lds) {
     uint32_t part = 0, kmax = 0;
     for (size_t i = 0; i < v.size(); i++) {
-        if (v[i].passes) part = std::max(part, max_iters[i] * v[i].rows_iter);
+        part = std::max(part, max_iters[i] * v[i].rows_iter);
         kmax = std::max(kmax, v[i].d.k);
     }
+    part = (part + 3u) & ~3u;
     *part_floats = part;
     *lds = part * 4u + kmax * 2u + kmax / 4u;
     if (*lds > kMaxLds) return fail(RFXQ_ERR_OTHER, "gemv: launch needs %u bytes of LDS", *lds);
