@@ -19,7 +19,10 @@
 //         y += da[m,s] * d[n] * D
 //   Q8_0: y += da[m,s] * d[n,s] * D
 // The constant term of a Q4_K super-block is four f32 MFMAs (32x32x2, K = 2
-// of the 8 sub-blocks each) into the same f32 accumulators.
+// of the 8 sub-blocks each) into the same f32 accumulators. The scale
+// products da[m,s] * dw[n,s] come from an f16 MFMA per tile and block
+// (scale_products), so the per-element epilogue is one convert and one FMA:
+// the VALU, not the int8 matrix core, bounds this kernel.
 //
 // Tile: 128 (M) x 128 (N) per 256-thread workgroup; each wave owns 64 x 64 =
 // 2 x 2 MFMA tiles. Activation scales for the tile's 128 rows are staged in
@@ -59,14 +62,30 @@ RFXQ_DEV v16i_t mfma_i8(v4i_t a, v4i_t b) {
 
 RFXQ_DEV v4i_t as_v4i(u4_t v) { return __builtin_bit_cast(v4i_t, v); }
 
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+RFXQ_DEV h8_t as_h8(u4_t v) { return __builtin_bit_cast(h8_t, v); }
+
+// Scale products S[m,n] = da[m] * dw[n] of one 32-block for a 32x32 tile, in
+// the int8 MFMA's accumulator layout, from one f16 MFMA (32x32x16): lanes
+// 0-31 carry K-slots 0-7 of row / column l%32, lanes 32-63 slots 8-15 (zero).
+// Every product is exact in f32 (f16 x f16), and the sum over slots is of
+// at most 6 such terms. This replaces a VALU multiply per output element and
+// block; the epilogue is then one convert and one FMA.
+RFXQ_DEV v16f_t scale_products(u4_t a, u4_t b) {
+    const v16f_t z = {};
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(a), as_h8(b), z, 0, 0, 0);
+}
+
+// f16 bits of x twice in one dword
+RFXQ_DEV uint32_t h2_dup(uint32_t bits16) { return (bits16 & 0xFFFFu) * 0x00010001u; }
+
 // ---------------------------------------------------------------- weights
 
-// Q4_K: (scale, min) pairs of sub-blocks 2g and 2g+1 from the 16-byte header
-// (get_scale_min_k4, src/dequant.rs:39-47), as d*sc and dmin*m.
-RFXQ_DEV void q4k_pair_scales(const u4_t hdr, uint32_t g, float& dsc0, float& dsc1) {
+// Q4_K: integer 6-bit scales of sub-blocks 2g and 2g+1 (get_scale_min_k4,
+// src/dequant.rs:39-47)
+RFXQ_DEV void q4k_pair_sc(const u4_t hdr, uint32_t g, uint32_t& sc1, uint32_t& sc2) {
     const uint32_t sh = (g & 1u) * 16u;
     const uint32_t a = hdr.y >> sh, c = hdr.w >> sh;
-    uint32_t sc1, sc2;
     if (g < 2u) {
         sc1 = a & 63u;
         sc2 = (a >> 8) & 63u;
@@ -74,9 +93,18 @@ RFXQ_DEV void q4k_pair_scales(const u4_t hdr, uint32_t g, float& dsc0, float& ds
         sc1 = (c & 0xFu) | ((a >> 2) & 0x30u);
         sc2 = ((c >> 8) & 0xFu) | ((a >> 10) & 0x30u);
     }
-    const float d = f16_bits_to_f32(hdr.x);
-    dsc0 = d * (float)sc1;
-    dsc1 = d * (float)sc2;
+}
+
+// B operand of scale_products for a Q4_K sub-block: slot k (k < 6) holds
+// d * 2^k if bit k of the 6-bit scale is set, else 0, so the slots sum to
+// d * sc exactly. d2[t] = (d * 4^t, d * 2 * 4^t) as f16 pairs.
+RFXQ_DEV u4_t q4k_scale_operand(const uint32_t d2[3], uint32_t sc) {
+    u4_t b;
+    b.x = d2[0] & (((sc & 1u) ? 0xFFFFu : 0u) | ((sc & 2u) ? 0xFFFF0000u : 0u));
+    b.y = d2[1] & (((sc & 4u) ? 0xFFFFu : 0u) | ((sc & 8u) ? 0xFFFF0000u : 0u));
+    b.z = d2[2] & (((sc & 16u) ? 0xFFFFu : 0u) | ((sc & 32u) ? 0xFFFF0000u : 0u));
+    b.w = 0u;
+    return b;
 }
 
 // Constant part of the centered Q4_K weights, c_s = 8*(d*sc_s) - dmin*m_s
@@ -107,8 +135,8 @@ RFXQ_DEV u4_t nib_hi(u4_t v) { return (v >> 4) & 0x0F0F0F0Fu; }
 RFXQ_DEV u4_t center8(u4_t q) { return ((q | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
 // Q8_0: one 34-byte block (2-byte aligned, never read past its end); returns
-// the lane's 16 quants (K half h) and d.
-RFXQ_DEV u4_t load_q8_0_half(const uint8_t* blk, uint32_t h, float& d) {
+// the lane's 16 quants (K half h) and the f16 bits of d.
+RFXQ_DEV u4_t load_q8_0_half(const uint8_t* blk, uint32_t h, uint32_t& dbits) {
     const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
     const uint8_t* pa = reinterpret_cast<const uint8_t*>(addr & ~(uintptr_t)3);
     const uint32_t sh = (uint32_t)(addr & 3u);
@@ -116,7 +144,7 @@ RFXQ_DEV u4_t load_q8_0_half(const uint8_t* blk, uint32_t h, float& d) {
     uint32_t w8;
     if (sh) w8 = *reinterpret_cast<const uint32_t*>(pa + 32);
     else w8 = *reinterpret_cast<const uint16_t*>(blk + 32);
-    d = f16_bits_to_f32(sh ? (w0.x >> 16) : w0.x);
+    dbits = (sh ? (w0.x >> 16) : w0.x) & 0xFFFFu;
     // qs dword j = bytes [2+4j, 6+4j) of the block; the lane needs j = 4h..4h+3,
     // i.e. dwords W0..W4 = w[4h .. 4h+4] of the dword-aligned read.
     const uint32_t W0 = h ? w1.x : w0.x, W1 = h ? w1.y : w0.y, W2 = h ? w1.z : w0.z, W3 = h ? w1.w : w0.w;
@@ -162,6 +190,7 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave & 1u, wn = wave >> 1;
     const uint32_t h = lane >> 5, l32 = lane & 31u;
+    const uint32_t lo_mask = h ? 0u : 0xFFFFFFFFu;  // scale-product K-slots live in lanes 0-31
 
     const uint32_t ks = t_local % ds.splits;
     const uint32_t rest = t_local / ds.splits;
@@ -204,6 +233,29 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
 
+    // Software pipeline: the activation operands of the next block pair (and,
+    // for Q4_K, its weight quants and the next super-block's header) are
+    // loaded while the current pair's MFMAs and epilogue run.
+    u4_t a_nx[2][2], qv_nx[2], hdr_nx[2];
+    auto load_a = [&](uint32_t sbx, uint32_t gx, u4_t a[2][2]) {
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) a[e][i] = ld16(arow[i] + 256u * sbx + 32u * (2u * gx + e));
+    };
+    auto load_q4 = [&](uint32_t sbx, uint32_t gx, u4_t q[2]) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) q[j] = ld16(brow[j] + (uint64_t)sbx * 144u + 16u + 32u * gx + 16u * h);
+    };
+    if (sb0 < sb1) {
+        load_a(sb0, 0u, a_nx);
+        if (TY == TY_Q4K) {
+            load_q4(sb0, 0u, qv_nx);
+#pragma unroll
+            for (int j = 0; j < 2; j++) hdr_nx[j] = ld16(brow[j] + (uint64_t)sb0 * 144u);
+        }
+    }
+
     for (uint32_t sb = sb0; sb < sb1; sb++) {
         // ---- activation scales of the tile's 128 rows: da as f32 [s][row], s_a as f16 [row][s]
         {
@@ -226,10 +278,13 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
         uint32_t q6sh[2];
         const uint8_t* q6pa[2];
         uint32_t q6sc[2][4];
-        float q6d[2];
+        uint32_t q6dbits[2];
         if (TY == TY_Q4K) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) hdr[j] = ld16(brow[j] + (uint64_t)sb * 144u);
+            for (int j = 0; j < 2; j++) {
+                hdr[j] = hdr_nx[j];
+                if (sb + 1u < sb1) hdr_nx[j] = ld16(brow[j] + (uint64_t)(sb + 1u) * 144u);
+            }
         } else if (TY == TY_Q6K) {
 #pragma unroll
             for (int j = 0; j < 2; j++) {
@@ -245,23 +300,53 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                 q6sc[j][1] = alignbyte(sw.z, sw.y, q6sh[j]);
                 q6sc[j][2] = alignbyte(sw.w, sw.z, q6sh[j]);
                 q6sc[j][3] = alignbyte(tail, sw.w, q6sh[j]);
-                q6d[j] = f16_bits_to_f32(q6sh[j] ? (tail >> 16) : tail);
+                q6dbits[j] = (q6sh[j] ? (tail >> 16) : tail) & 0xFFFFu;
+            }
+        }
+
+        // B operands of the scale products (lanes 32-63 carry zero K-slots)
+        uint32_t d2[2][3];  // Q4_K: (d, 2d), (4d, 8d), (16d, 32d) as f16 pairs
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            if (TY == TY_Q4K) {
+                const float d = f16_bits_to_f32(hdr[j].x);
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    const h2_t v = {(half_t)(d * (float)(1u << (2 * t))), (half_t)(d * (float)(2u << (2 * t)))};
+                    d2[j][t] = h2_bits(v) & lo_mask;
+                }
             }
         }
 
 #pragma unroll 1
         for (uint32_t g = 0; g < 4; g++) {
+            // this step's prefetched operands; issue the next step's loads
+            u4_t a_cur[2][2], qv_cur[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) a_cur[e][i] = a_nx[e][i];
+#pragma unroll
+            for (int j = 0; j < 2; j++) qv_cur[j] = qv_nx[j];
+            {
+                const bool last_g = g == 3u;
+                const uint32_t sbn = last_g ? sb + 1u : sb, gn = last_g ? 0u : g + 1u;
+                if (sbn < sb1) {
+                    load_a(sbn, gn, a_nx);
+                    if (TY == TY_Q4K) load_q4(sbn, gn, qv_nx);
+                }
+            }
             // per 32-block pair (2g, 2g+1): B operands and weight scales
             u4_t bw[2][2];
-            float wsc[2][2];
+            uint32_t wsb[2][2];  // Q4_K: 6-bit sub-block scale; Q6_K / Q8_0: f16 bits of d
             int scl[2][2], sch[2][2];  // Q6_K: scales of the two 16-runs
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 if (TY == TY_Q4K) {
-                    const u4_t qv = ld16(brow[j] + (uint64_t)sb * 144u + 16u + 32u * g + 16u * h);
+                    const u4_t qv = qv_cur[j];
                     bw[j][0] = center8(nib_lo(qv));
                     bw[j][1] = center8(nib_hi(qv));
-                    q4k_pair_scales(hdr[j], g, wsc[j][0], wsc[j][1]);
+                    q4k_pair_sc(hdr[j], g, wsb[j][0], wsb[j][1]);
                 } else if (TY == TY_Q6K) {
                     const uint32_t n = g >> 1, t0 = 2u * (g & 1u);
                     const u4_t qla = seg16_mmq(q6pa[j], 64u * n + 16u * h, q6sh[j]);
@@ -275,12 +360,13 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                     sch[j][0] = sbyte(wv, 1);
                     scl[j][1] = sbyte(wv, 2);
                     sch[j][1] = sbyte(wv, 3);
-                    wsc[j][0] = q6d[j];
-                    wsc[j][1] = q6d[j];
+                    wsb[j][0] = q6dbits[j];
+                    wsb[j][1] = q6dbits[j];
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 2; e++)
-                        bw[j][e] = load_q8_0_half(brow[j] + (uint64_t)(8u * sb + 2u * g + e) * 34u, h, wsc[j][e]);
+                    for (int e = 0; e < 2; e++) {
+                        bw[j][e] = load_q8_0_half(brow[j] + (uint64_t)(8u * sb + 2u * g + e) * 34u, h, wsb[j][e]);
+                    }
                 }
             }
 #pragma unroll
@@ -288,18 +374,21 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                 const uint32_t s = 2u * g + e;
                 v4i_t a[2];
 #pragma unroll
-                for (int i = 0; i < 2; i++) a[i] = as_v4i(ld16(arow[i] + 256u * sb + 32u * s));
+                for (int i = 0; i < 2; i++) a[i] = as_v4i(a_cur[e][i]);
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
-                    const float* dap = lds_da + s * MMQ_BM + 64u * wm + 32u * i + 4u * h;
-                    float da[16];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const float4 v = *reinterpret_cast<const float4*>(dap + 8u * q);
-                        da[4 * q + 0] = v.x;
-                        da[4 * q + 1] = v.y;
-                        da[4 * q + 2] = v.z;
-                        da[4 * q + 3] = v.w;
+                    // scale-product A operand: this lane's row's activation scale
+                    // (f16), in slots 0-5 for Q4_K (against d * 2^k), slot 0 otherwise
+                    u4_t sa = {0u, 0u, 0u, 0u};
+                    if (!DOTS) {
+                        const float da = lds_da[s * MMQ_BM + 64u * wm + 32u * i + l32];
+                        const uint32_t dab = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)da) & lo_mask;
+                        if (TY == TY_Q4K) {
+                            const uint32_t p = h2_dup(dab);
+                            sa = u4_t{p, p, p, 0u};
+                        } else {
+                            sa.x = dab;
+                        }
                     }
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
@@ -322,9 +411,11 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                                     ds.dots_out[((uint64_t)row * ds.n + col) * nkb + 8u * sb + s] = D[r];
                             }
                         } else {
-                            const float ws = wsc[j][e];
+                            const u4_t sbo = TY == TY_Q4K ? q4k_scale_operand(d2[j], wsb[j][e])
+                                                          : u4_t{wsb[j][e] & lo_mask, 0u, 0u, 0u};
+                            const v16f_t S = scale_products(sa, sbo);
 #pragma unroll
-                            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)D[r], da[r] * ws, acc[i][j][r]);
+                            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)D[r], S[r], acc[i][j][r]);
                         }
                     }
                 }
@@ -381,19 +472,22 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
     return a.table[lo];
 }
 
-#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS)                                            \
-    extern "C" __global__ __launch_bounds__(256) void NAME(MmqArgs args) {    \
+// The GEMM kernels are held to 2 waves per SIMD (no spills at this budget) so
+// that one wave's epilogue overlaps another's MFMAs and loads; the block-dot
+// test hooks keep the default budget.
+#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS, WPE)                                       \
+    extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
         __shared__ float lds_da[8 * MMQ_BM];                                  \
         __shared__ float lds_sx[MMQ_BM * 8];                                  \
         const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
         mmq_tile<TY, DOTS>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx);       \
     }
-RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1)
 
 // y[i] = sum_z ws[z][i], added in split order (deterministic).
 extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float* __restrict__ ws,
