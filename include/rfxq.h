@@ -129,6 +129,29 @@ uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows);
 int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
               uint64_t workspace_bytes, hipStream_t stream);
 
+/* One GEMM of a grouped launch: y[rows, N] = x[rows, K] . W^T. */
+typedef struct rfxq_gemm_item {
+    const float* x;
+    const rfxq_weight* w;
+    float* y;
+} rfxq_gemm_item;
+typedef struct rfxq_gemm_plan rfxq_gemm_plan;
+
+/* Grouped prefill GEMMs of one row count: the projections that share an
+ * input (Model::gemm called for attn_q / attn_k / attn_v on the same normed
+ * rows, src/model/dense.rs:1345-1347, and ffn_gate / ffn_up, :1476-1477) as
+ * one quantization per distinct x and one MMQ launch per weight type. Same
+ * per-item results as rfxq_gemm with REFLEX_QUANT_MMA_SPLITS=1. Uses the
+ * library workspace of the current device. */
+int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, hipStream_t stream);
+
+/* rfxq_gemm_batch with descriptor tables and activation workspace built once
+ * (on `device`) and replayed by rfxq_gemm_plan_run. */
+int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, int device,
+                          rfxq_gemm_plan** out);
+int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream);
+void rfxq_gemm_plan_destroy(rfxq_gemm_plan* plan);
+
 /* Test hook (the role of q{4,6}k_mma_dequant_check_kernel,
  * src/kernels_cuda/gemm_q_mma.cu:791-838): the MMQ kernel's int32 dot product
  * of every (row, output, 32-block): dots[rows][N][K/32]. For Q6_K the two

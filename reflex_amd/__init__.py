@@ -49,6 +49,10 @@ SIGNATURES = {
     "rfxq_gemv_plan_create": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _I, ctypes.POINTER(_P)]),
     "rfxq_gemv_plan_run": (_I, [_P, _P]),
     "rfxq_gemv_plan_destroy": (None, [_P]),
+    "rfxq_gemm_batch": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _U32, _P]),
+    "rfxq_gemm_plan_create": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _U32, _I, ctypes.POINTER(_P)]),
+    "rfxq_gemm_plan_run": (_I, [_P, _P]),
+    "rfxq_gemm_plan_destroy": (None, [_P]),
     "rfxq_quantize_q8_1": (_I, [_P, _U32, _U32, _P, _P, _P]),
     "rfxq_gemm_workspace_size": (_U64, [_WP, _U32]),
     "rfxq_gemm": (_I, [_P, _U64, _WP, _U32, _P, _P, _U64, _P]),

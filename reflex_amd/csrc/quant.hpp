@@ -17,16 +17,14 @@
 #pragma once
 #include "common.hpp"
 
-extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,
-                                                                    const int32_t* __restrict__ src_rows,
-                                                                    uint32_t rows, uint32_t k,
-                                                                    int8_t* __restrict__ xq, uint32_t ldq,
-                                                                    uint32_t* __restrict__ xds) {
+// Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
+// wave_global); 8 lanes per 32-block.
+RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
+                              uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
+                              uint32_t* __restrict__ xds, uint64_t wave_global, uint64_t nwaves) {
     const uint32_t nblk = k / 32u;
     const uint64_t total = (uint64_t)rows * nblk;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint64_t wave_global = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint64_t nwaves = ((uint64_t)gridDim.x * blockDim.x) >> 6;
     for (uint64_t b0 = wave_global * 8u; b0 < total; b0 += nwaves * 8u) {
         const uint64_t bi = b0 + (lane >> 3);
         const bool valid = bi < total;
@@ -61,4 +59,36 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
             }
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,
+                                                                    const int32_t* __restrict__ src_rows,
+                                                                    uint32_t rows, uint32_t k,
+                                                                    int8_t* __restrict__ xq, uint32_t ldq,
+                                                                    uint32_t* __restrict__ xds) {
+    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6,
+                    ((uint64_t)gridDim.x * blockDim.x) >> 6);
+}
+
+// Several activations in one launch (grouped GEMMs): workgroups
+// [wg_begin, wg_begin + wgs) of the grid take activation i.
+struct QuantDesc {
+    const float* x;
+    int8_t* xq;
+    uint32_t* xds;
+    uint32_t rows, k, wg_begin, wgs;
+};
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1_multi(const QuantDesc* __restrict__ table,
+                                                                          uint32_t ndesc) {
+    uint32_t lo = 0, hi = ndesc - 1u;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) >> 1;
+        if (table[mid].wg_begin <= blockIdx.x) lo = mid;
+        else hi = mid - 1u;
+    }
+    const QuantDesc d = table[lo];
+    const uint32_t wg = blockIdx.x - d.wg_begin;
+    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6,
+                    ((uint64_t)d.wgs * blockDim.x) >> 6);
 }

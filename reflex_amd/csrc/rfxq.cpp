@@ -109,7 +109,7 @@ struct Ctx {
     int device = -1;
     int cus = 256;
     hipModule_t mod = nullptr;
-    hipFunction_t gemv = nullptr, quant = nullptr, reduce = nullptr;
+    hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {};
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
@@ -142,6 +142,7 @@ int load_ctx(int device, Ctx** out) {
         const char* name;
     } fns[] = {
         {&c->gemv, "rfxq_gemv"},
+        {&c->quant_multi, "rfxq_quantize_q8_1_multi"},
         {&c->quant, "rfxq_quantize_q8_1"},
         {&c->reduce, "rfxq_splitk_reduce"},
         {&c->mmq[0], "rfxq_mmq_q4k"},
@@ -523,6 +524,84 @@ int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float
     return RFXQ_OK;
 }
 
+// ------------------------------------------------------------------ grouped GEMMs
+
+// GEMMs of one row count over several weights, grouped: each distinct
+// activation (by address) is quantized once, and each weight type runs as one
+// MMQ launch over all of its GEMMs (no split-K: a group has tiles enough).
+struct GemmGroup {
+    struct Act {
+        const float* x;
+        uint32_t k;
+        uint64_t off_xq, off_xds;
+    };
+    std::vector<Act> acts;
+    std::vector<MmqDesc> descs[3];  // per type_index
+    uint32_t wgs[3] = {0, 0, 0};
+    uint64_t ws_bytes = 0;
+};
+
+int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g) {
+    if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
+    for (uint32_t i = 0; i < count; i++) {
+        const rfxq_gemm_item& it = items[i];
+        if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
+        if (!it.x || !it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: item %u has a NULL x or y", i);
+        if (reinterpret_cast<uintptr_t>(it.x) % 16u)
+            return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not 16-byte aligned", i);
+        const uint32_t k = it.w->in_features;
+        size_t ai = 0;
+        while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
+        if (ai == g->acts.size()) {
+            GemmGroup::Act act{it.x, k, 0, 0};
+            act.off_xq = g->ws_bytes;
+            act.off_xds = act.off_xq + align256((uint64_t)rows * k);
+            g->ws_bytes = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+            g->acts.push_back(act);
+        } else if (g->acts[ai].k != k) {
+            return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
+        }
+        MmqDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.w = it.w->data;
+        d.xq = reinterpret_cast<const int8_t*>(g->acts[ai].off_xq);   // offsets until the workspace is known
+        d.xds = reinterpret_cast<const uint32_t*>(g->acts[ai].off_xds);
+        d.y = it.y;
+        d.m = rows;
+        d.n = it.w->out_features;
+        d.k = k;
+        d.type = it.w->ggml_type;
+        d.ldq = k;
+        d.ldy = d.n;
+        d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
+        d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
+        d.splits = 1;
+        d.sb_per_split = k / 256u;
+        const uint32_t t = type_index(d.type);
+        d.wg_begin = g->wgs[t];
+        g->wgs[t] += d.tiles_m * d.tiles_n;
+        g->descs[t].push_back(d);
+    }
+    return RFXQ_OK;
+}
+
+// workspace offsets -> addresses
+void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
+    for (auto& v : g->descs)
+        for (MmqDesc& d : v) {
+            d.xq = reinterpret_cast<const int8_t*>(ws + reinterpret_cast<uintptr_t>(d.xq));
+            d.xds = reinterpret_cast<const uint32_t*>(ws + reinterpret_cast<uintptr_t>(d.xds));
+        }
+}
+
+int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
+    for (const auto& a : g.acts)
+        if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k, reinterpret_cast<int8_t*>(ws + a.off_xq),
+                                  reinterpret_cast<uint32_t*>(ws + a.off_xds), stream))
+            return rc;
+    return RFXQ_OK;
+}
+
 // ------------------------------------------------------------------ router (src/moe.rs:47-98)
 
 int route_top_k(const float* logits, uint32_t n, uint32_t k, bool normalize, uint32_t* idx, float* w) {
@@ -577,6 +656,24 @@ int expert_slice(const rfxq_weight* w, uint32_t e, rfxq_weight* out, const char*
 }  // namespace
 
 // ====================================================================== C ABI
+
+struct QuantDesc {
+    const float* x;
+    int8_t* xq;
+    uint32_t* xds;
+    uint32_t rows, k, wg_begin, wgs;
+};
+static_assert(sizeof(QuantDesc) == 40, "QuantDesc layout");
+
+struct rfxq_gemm_plan {
+    int device;
+    uint32_t rows;
+    void* dev = nullptr;  // quantized activations, one descriptor table per weight type, the quantize table
+    GemmGroup g;
+    MmqDesc* table[3] = {nullptr, nullptr, nullptr};
+    QuantDesc* qtable = nullptr;
+    uint32_t qgrid = 0;
+};
 
 struct rfxq_gemv_plan {
     int device;
@@ -778,6 +875,119 @@ int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t row
     if (int rc = current_ctx(&c)) return rc;
     if (int rc = gemm_impl(c, x, w, rows, y, workspace, workspace_bytes, stream)) return rc;
     return ok();
+}
+
+int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, hipStream_t stream) {
+    if (count == 0) return ok();
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    GemmGroup g;
+    if (int rc = build_gemm_group(items, count, rows, &g)) return rc;
+    void* ws = nullptr;
+    if (int rc = ctx_workspace(c, g.ws_bytes, &ws)) return rc;
+    bind_gemm_group(&g, static_cast<uint8_t*>(ws));
+    if (int rc = run_gemm_quant(c, g, static_cast<uint8_t*>(ws), rows, stream)) return rc;
+    // descriptors inline, kMmqInline per launch
+    for (uint32_t t = 0; t < 3; t++) {
+        auto& v = g.descs[t];
+        for (size_t i0 = 0; i0 < v.size(); i0 += kMmqInline) {
+            const uint32_t cnt = (uint32_t)std::min<size_t>(kMmqInline, v.size() - i0);
+            MmqDesc d[kMmqInline];
+            uint32_t wg = 0;
+            for (uint32_t j = 0; j < cnt; j++) {
+                d[j] = v[i0 + j];
+                d[j].wg_begin = wg;
+                wg += d[j].tiles_m * d[j].tiles_n;
+            }
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream)) return rc;
+        }
+    }
+    return ok();
+}
+
+int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, int device,
+                          rfxq_gemm_plan** out) {
+    if (!out) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_plan_create: out is NULL");
+    *out = nullptr;
+    int prev = 0;
+    HIPCHK(hipGetDevice(&prev), "hipGetDevice");
+    HIPCHK(hipSetDevice(device), "hipSetDevice");
+    Ctx* c = nullptr;
+    int rc = load_ctx(device, &c);
+    auto plan = std::make_unique<rfxq_gemm_plan>();
+    plan->device = device;
+    plan->rows = rows;
+    if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g);
+    uint64_t tables = 0;
+    if (rc == RFXQ_OK) {
+        tables = align256(plan->g.acts.size() * sizeof(QuantDesc));
+        for (const auto& v : plan->g.descs) tables += align256(v.size() * sizeof(MmqDesc));
+        hipError_t e = hipMalloc(&plan->dev, std::max<uint64_t>(1u, plan->g.ws_bytes + tables));
+        if (e != hipSuccess) rc = fail(RFXQ_ERR_OUT_OF_MEMORY, "gemm_plan_create: %s", hipGetErrorString(e));
+    }
+    if (rc == RFXQ_OK) {
+        uint8_t* base = static_cast<uint8_t*>(plan->dev);
+        bind_gemm_group(&plan->g, base);
+        uint64_t off = plan->g.ws_bytes;
+        for (uint32_t t = 0; t < 3 && rc == RFXQ_OK; t++) {
+            const auto& v = plan->g.descs[t];
+            plan->table[t] = reinterpret_cast<MmqDesc*>(base + off);
+            if (!v.empty()) {
+                hipError_t e = hipMemcpy(plan->table[t], v.data(), v.size() * sizeof(MmqDesc), hipMemcpyHostToDevice);
+                if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemm_plan_create upload: %s", hipGetErrorString(e));
+            }
+            off += align256(v.size() * sizeof(MmqDesc));
+        }
+        // one quantize launch for all activations
+        std::vector<QuantDesc> q;
+        for (const auto& a : plan->g.acts) {
+            const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
+            q.push_back(QuantDesc{a.x, reinterpret_cast<int8_t*>(base + a.off_xq),
+                                  reinterpret_cast<uint32_t*>(base + a.off_xds), rows, a.k, plan->qgrid, wgs});
+            plan->qgrid += wgs;
+        }
+        plan->qtable = reinterpret_cast<QuantDesc*>(base + off);
+        if (rc == RFXQ_OK) {
+            hipError_t e = hipMemcpy(plan->qtable, q.data(), q.size() * sizeof(QuantDesc), hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemm_plan_create upload: %s", hipGetErrorString(e));
+        }
+    }
+    (void)hipSetDevice(prev);
+    if (rc != RFXQ_OK) {
+        if (plan->dev) (void)hipFree(plan->dev);
+        return rc;
+    }
+    *out = plan.release();
+    return ok();
+}
+
+int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
+    if (!plan) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_plan_run: NULL plan");
+    Ctx* c;
+    if (int rc = load_ctx(plan->device, &c)) return rc;
+    struct {
+        const QuantDesc* table;
+        uint32_t ndesc, pad;
+    } qa = {plan->qtable, (uint32_t)plan->g.acts.size(), 0};
+    if (int rc = launch(c->quant_multi, plan->qgrid, 0, stream, &qa, sizeof qa, "rfxq_quantize_q8_1_multi launch"))
+        return rc;
+    for (uint32_t t = 0; t < 3; t++) {
+        const auto& v = plan->g.descs[t];
+        if (v.empty()) continue;
+        MmqDesc tmp[kMmqInline];
+        const uint32_t n = (uint32_t)v.size();
+        if (n <= kMmqInline) std::copy(v.begin(), v.end(), tmp);
+        if (int rc = launch_mmq(c, v[0].type, tmp, n, n <= kMmqInline ? nullptr : plan->table[t], plan->g.wgs[t],
+                                false, stream))
+            return rc;
+    }
+    return ok();
+}
+
+void rfxq_gemm_plan_destroy(rfxq_gemm_plan* plan) {
+    if (!plan) return;
+    if (plan->dev) (void)hipFree(plan->dev);
+    delete plan;
 }
 
 int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, const rfxq_weight* w, int32_t* dots,

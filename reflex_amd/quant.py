@@ -21,7 +21,7 @@ __all__ = [
     "ReflexError", "GgmlError", "GpuError", "OutOfMemoryError", "InvalidInputError",
     "GgmlType", "ggml_type_block_dims", "Weight", "QuantArena",
     "dequantize", "gemv", "gemv_to", "gemv_q4k", "gemv_q6k", "gemv_q8_0", "gemv_batch", "GemvPlan",
-    "gemm", "gemm_workspace_size", "quantize_q8_1", "mmq_block_dots",
+    "gemm", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
     "route_top_k", "route_top_k_with_norm", "quant_expert_weight", "expert_gemv", "expert_gemm",
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
 ]
@@ -283,6 +283,38 @@ def gemm(x: torch.Tensor, w: Weight, rows: int, workspace: torch.Tensor | None =
         _check(lib().rfxq_gemm(x.data_ptr(), x.numel(), w.cref(), rows, y.data_ptr(), _ptr(workspace),
                                workspace.numel() if workspace is not None else 0, _stream()))
     return y
+
+
+def gemm_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int) -> None:
+    """Grouped prefill GEMMs of one row count (the q/k/v and gate/up ``Model::gemm``
+    calls on one input, dense.rs:1345-1347, 1476-1477): one quantization per
+    distinct x, one MMQ launch per weight type. Items are (x, w, y)."""
+    if not items:
+        return
+    arr, _keep = _items(items)
+    with _dev(items[0][0]):
+        _check(lib().rfxq_gemm_batch(arr, len(items), rows, _stream()))
+
+
+class GemmPlan:
+    """gemm_batch with its tables and activation workspace built once."""
+
+    def __init__(self, items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int):
+        arr, self._keep = _items(items)
+        self._tensors = items
+        h = ctypes.c_void_p()
+        dev = items[0][0].device.index or 0
+        self._lib = lib()  # kept so that __del__ works during interpreter shutdown
+        _check(self._lib.rfxq_gemm_plan_create(arr, len(items), rows, dev, ctypes.byref(h)))
+        self._h = h
+
+    def run(self) -> None:
+        _check(lib().rfxq_gemm_plan_run(self._h, _stream()))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._lib.rfxq_gemm_plan_destroy(self._h)
+            self._h = None
 
 
 def mmq_block_dots(xq: torch.Tensor, xds: torch.Tensor, rows: int, w: Weight) -> torch.Tensor:

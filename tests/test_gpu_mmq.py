@@ -183,3 +183,46 @@ def test_gemm_caller_workspace(rq, orc):
     assert orc.rel_err_row_l2(y, orc.mmq_model_reference(Q6K, w_np, n, k, x)) < 3e-5
     with pytest.raises(rq.ReflexError):
         rq.gemm(_dev(x), w, m, workspace=ws[:100])
+
+
+def test_gemm_batch_and_plan_match_single_gemms(rq, orc):
+    """Grouped GEMMs (shared activations quantized once, one launch per weight
+    type) give the single-GEMM results bit for bit (no split-K on either side)."""
+    rows = 300
+    shapes = [(Q4K, 768, 1024), (Q4K, 256, 1024), (Q6K, 256, 1024), (Q8_0, 512, 1024), (Q4K, 640, 2048)]
+    xa = _dev(synth.activations(rows * 1024, 71))
+    xb = _dev(synth.activations(rows * 2048, 72))
+    ws, items = [], []
+    for i, (ty, n, k) in enumerate(shapes):
+        w = _weight(rq, ty, synth.weights(ty, n, k, 80 + i), n, k)
+        ws.append(w)
+        items.append((xa if k == 1024 else xb, w, torch.empty(rows * n, device=DEV)))
+    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
+    try:
+        singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
+    finally:
+        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
+    rq.gemm_batch(items, rows)
+    for (x, w, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)
+    for _, _, y in items:
+        y.zero_()
+    plan = rq.GemmPlan(items, rows)
+    for _ in range(2):
+        plan.run()
+        for (x, w, y), ref in zip(items, singles):
+            assert np.array_equal(y.cpu().numpy(), ref)
+    # model-reference parity of one grouped result
+    n, k = shapes[2][1], shapes[2][2]
+    model = orc.mmq_model_reference(Q6K, synth.weights(Q6K, n, k, 82), n, k,
+                                    synth.activations(rows * 1024, 71).reshape(rows, k))
+    assert orc.rel_err_row_l2(items[2][2].cpu().numpy().reshape(rows, n), model) < 3e-5
+
+
+def test_gemm_batch_errors(rq):
+    x = _dev(synth.activations(64 * 1024, 3))
+    w1 = _weight(rq, Q4K, synth.weights(Q4K, 256, 1024, 1), 256, 1024)
+    w2 = _weight(rq, Q4K, synth.weights(Q4K, 256, 512, 2), 256, 512)
+    y = torch.empty(64 * 256, device=DEV)
+    with pytest.raises(rq.ReflexError):
+        rq.gemm_batch([(x, w1, y), (x, w2, y)], 64)   # one x with two in_features
