@@ -42,7 +42,14 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="skip prefill, 8B and CPU legs")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only replay the fused GEMV plan and a calibration copy (for rocprofv3 --pmc runs)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, WRITE_SIZE) of a "
+                         "--traffic-probe run into profiles/gemv_decode06b_traffic.json")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is design-only", file=sys.stderr)
@@ -96,6 +103,18 @@ def main() -> int:
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps  # ms per step
+
+    if args.traffic_probe:
+        # 5 launches of each plan copy, then a plain copy of COPY_BYTES (the
+        # counters' calibration: its algorithmic bytes are known exactly)
+        for i in range(5 * args.copies):
+            plans[i % args.copies].run()
+        src = torch.empty(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1.0, out=dst)  # an elementwise kernel: reads and writes COPY_BYTES
+        torch.cuda.synchronize()
+        return 0
 
     # headline: one fused launch per step
     ms = timed(lambda i: plans[i % args.copies].run(), args.steps, args.warmup)
@@ -157,6 +176,45 @@ def main() -> int:
     if not args.quick and not args.no_cpu:
         result["cpu_baseline"] = cpu_leg(host_w, layer, L, np)
     print(json.dumps(result), flush=True)
+    return 0
+
+
+COPY_BYTES = 256 << 20
+
+
+def traffic_summary(fetch_csv: str, write_csv: str) -> int:
+    """HBM bytes per rfxq_gemv launch from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by the factor that makes the calibration copy's
+    counter equal its known bytes (COPY_BYTES read, COPY_BYTES written)."""
+    import csv
+    import statistics
+
+    def per_kernel(path):
+        vals = {}
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            key = "gemv" if name == "rfxq_gemv" else ("copy" if "elementwise" in name.lower() else None)
+            if key:
+                vals.setdefault(key, []).append(float(r["Counter_Value"]) * 1024.0)
+        return {k: statistics.median(v) for k, v in vals.items()}
+
+    f, w = per_kernel(fetch_csv), per_kernel(write_csv)
+    f_scale, w_scale = COPY_BYTES / f["copy"], COPY_BYTES / w["copy"]
+    out = {
+        "kernel": "rfxq_gemv", "workload": "qwen3-0.6b decode GEMV set, one fused launch",
+        "fetch_bytes_raw": f["gemv"], "write_bytes_raw": w["gemv"],
+        "fetch_scale": f_scale, "write_scale": w_scale,
+        "bytes_per_launch": f["gemv"] * f_scale + w["gemv"] * w_scale,
+        "algorithmic_bytes_per_launch": None,
+    }
+    from reflex_amd import synth
+    layer = synth.QWEN3_06B_LAYER
+    out["algorithmic_bytes_per_launch"] = sum(synth.weight_bytes(ty, n, k) + 4 * k + 4 * n
+                                              for _, ty, n, k in layer) * synth.QWEN3_06B_LAYERS
+    path = os.path.join(ROOT, "profiles", "gemv_decode06b_traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out))
     return 0
 
 
