@@ -52,7 +52,6 @@ struct MmqArgs {
     MmqDesc inl[MMQ_INLINE];
 };
 
-#define MMQ_BM 128
 #define MMQ_BN 128
 
 RFXQ_DEV v16i_t mfma_i8(v4i_t a, v4i_t b) {
@@ -98,13 +97,23 @@ RFXQ_DEV void q4k_pair_sc(const u4_t hdr, uint32_t g, uint32_t& sc1, uint32_t& s
 // B operand of scale_products for a Q4_K sub-block: slot k (k < 6) holds
 // d * 2^k if bit k of the 6-bit scale is set, else 0, so the slots sum to
 // d * sc exactly. d2[t] = (d * 4^t, d * 2 * 4^t) as f16 pairs.
-RFXQ_DEV u4_t q4k_scale_operand(const uint32_t d2[3], uint32_t sc) {
-    u4_t b;
-    b.x = d2[0] & (((sc & 1u) ? 0xFFFFu : 0u) | ((sc & 2u) ? 0xFFFF0000u : 0u));
-    b.y = d2[1] & (((sc & 4u) ? 0xFFFFu : 0u) | ((sc & 8u) ? 0xFFFF0000u : 0u));
-    b.z = d2[2] & (((sc & 16u) ? 0xFFFFu : 0u) | ((sc & 32u) ? 0xFFFF0000u : 0u));
-    b.w = 0u;
-    return b;
+// The bit masks come from a 64-entry LDS table (mmq_scale_masks), one read
+// instead of six bit tests.
+RFXQ_DEV u4_t q4k_scale_operand(const uint32_t d2[3], uint32_t sc, const u4_t* masks) {
+    const u4_t m = masks[sc];
+    return u4_t{d2[0] & m.x, d2[1] & m.y, d2[2] & m.z, 0u};
+}
+
+// masks[sc] for sc in [0, 64): f16 lane k of the three dwords is all ones
+// when bit k of sc is set
+RFXQ_DEV void mmq_fill_scale_masks(u4_t* masks) {
+    const uint32_t sc = threadIdx.x;
+    if (sc < 64u) {
+        auto pair = [&](uint32_t k) {
+            return ((sc >> k) & 1u ? 0xFFFFu : 0u) | ((sc >> (k + 1u)) & 1u ? 0xFFFF0000u : 0u);
+        };
+        masks[sc] = u4_t{pair(0), pair(2), pair(4), 0u};
+    }
 }
 
 // Constant part of the centered Q4_K weights, c_s = 8*(d*sc_s) - dmin*m_s
@@ -131,8 +140,9 @@ RFXQ_DEV void q4k_offsets(const u4_t hdr, uint32_t h, float c[4]) {
 
 RFXQ_DEV u4_t nib_lo(u4_t v) { return v & 0x0F0F0F0Fu; }
 RFXQ_DEV u4_t nib_hi(u4_t v) { return (v >> 4) & 0x0F0F0F0Fu; }
-// bytes q in [0, 15] -> q - 8 as int8 (no borrow between bytes)
-RFXQ_DEV u4_t center8(u4_t q) { return ((q | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+// bytes q in [0, 15] -> q - 8 as int8: q + 0x78 stays below 0x100 (no carry
+// between bytes), and flipping bit 7 maps it to q - 8 in two's complement
+RFXQ_DEV u4_t center8(u4_t q) { return (q + 0x78787878u) ^ 0x80808080u; }
 
 // Q8_0: one 34-byte block (2-byte aligned, never read past its end); returns
 // the lane's 16 quants (K half h) and the f16 bits of d.
@@ -185,8 +195,10 @@ RFXQ_DEV u4_t q6_codes(u4_t ql, u4_t qh, uint32_t t) {
 
 RFXQ_DEV int sbyte(uint32_t w, uint32_t byte) { return (int)(int8_t)(w >> (8u * byte)); }
 
-template <uint32_t TY, bool DOTS>
-RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float* lds_sx) {
+// MI: 32-row MFMA tiles per wave along M (the workgroup tile is 64*MI x 128)
+template <uint32_t TY, bool DOTS, int MI>
+RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float* lds_sx, u4_t* lds_masks) {
+    constexpr uint32_t BM = 64u * MI, WM = 32u * MI;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave & 1u, wn = wave >> 1;
     const uint32_t h = lane >> 5, l32 = lane & 31u;
@@ -195,7 +207,8 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
     const uint32_t ks = t_local % ds.splits;
     const uint32_t rest = t_local / ds.splits;
     const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
-    const uint32_t m0 = tm * MMQ_BM, n0 = tn * MMQ_BN;
+    const uint32_t m0 = tm * BM, n0 = tn * MMQ_BN;
+    if (TY == TY_Q4K && !DOTS) mmq_fill_scale_masks(lds_masks);  // ready after the first barrier
     const uint32_t nsb = ds.k / 256u;
     const uint32_t sb0 = ks * ds.sb_per_split;
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
@@ -203,10 +216,10 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
     const uint64_t row_bytes = TY == TY_Q4K ? (uint64_t)nsb * 144u : TY == TY_Q6K ? (uint64_t)nsb * 210u
                                                                                  : (uint64_t)nkb * 34u;
 
-    const uint8_t* arow[2];
+    const uint8_t* arow[MI];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        uint32_t m = m0 + 64u * wm + 32u * i + l32;
+    for (int i = 0; i < MI; i++) {
+        uint32_t m = m0 + WM * wm + 32u * i + l32;
         m = m < ds.m ? m : ds.m - 1u;
         const uint32_t src = ds.rows ? (uint32_t)ds.rows[m] : m;
         arow[i] = reinterpret_cast<const uint8_t*>(ds.xq) + (uint64_t)src * ds.ldq + 16u * h;
@@ -218,30 +231,33 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
         n = n < ds.n ? n : ds.n - 1u;
         brow[j] = ds.w + (uint64_t)n * row_bytes;
     }
-    const uint32_t st_r = tid >> 1, st_part = tid & 1u;
-    const uint32_t* st_src;
-    {
-        uint32_t m = m0 + st_r;
+    // activation-scale staging: BM rows x 2 halves of a super-block's 8 blocks
+    constexpr int ST = (2 * BM + 255) / 256;
+    const uint32_t* st_src[ST];
+#pragma unroll
+    for (int q = 0; q < ST; q++) {
+        const uint32_t r2 = tid + 256u * q;
+        uint32_t m = m0 + (r2 >> 1);
         m = m < ds.m ? m : ds.m - 1u;
         const uint32_t src = ds.rows ? (uint32_t)ds.rows[m] : m;
-        st_src = ds.xds + (uint64_t)src * nkb + 4u * st_part;
+        st_src[q] = ds.xds + (uint64_t)src * nkb + 4u * (r2 & 1u);
     }
 
-    v16f_t acc[2][2];
+    v16f_t acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = v16f_t{};
 
     // Software pipeline: the activation operands of the next block pair (and,
     // for Q4_K, its weight quants and the next super-block's header) are
     // loaded while the current pair's MFMAs and epilogue run.
-    u4_t a_nx[2][2], qv_nx[2], hdr_nx[2];
-    auto load_a = [&](uint32_t sbx, uint32_t gx, u4_t a[2][2]) {
+    u4_t a_nx[2][MI], qv_nx[2], hdr_nx[2];
+    auto load_a = [&](uint32_t sbx, uint32_t gx, u4_t a[2][MI]) {
 #pragma unroll
         for (int e = 0; e < 2; e++)
 #pragma unroll
-            for (int i = 0; i < 2; i++) a[e][i] = ld16(arow[i] + 256u * sbx + 32u * (2u * gx + e));
+            for (int i = 0; i < MI; i++) a[e][i] = ld16(arow[i] + 256u * sbx + 32u * (2u * gx + e));
     };
     auto load_q4 = [&](uint32_t sbx, uint32_t gx, u4_t q[2]) {
 #pragma unroll
@@ -258,12 +274,16 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 
     for (uint32_t sb = sb0; sb < sb1; sb++) {
         // ---- activation scales of the tile's 128 rows: da as f32 [s][row], s_a as f16 [row][s]
-        {
-            const u4_t v = *reinterpret_cast<const u4_t*>(st_src + 8u * sb);
-            lds_da[(4u * st_part + 0u) * MMQ_BM + st_r] = f16_bits_to_f32(v.x);
-            lds_da[(4u * st_part + 1u) * MMQ_BM + st_r] = f16_bits_to_f32(v.y);
-            lds_da[(4u * st_part + 2u) * MMQ_BM + st_r] = f16_bits_to_f32(v.z);
-            lds_da[(4u * st_part + 3u) * MMQ_BM + st_r] = f16_bits_to_f32(v.w);
+#pragma unroll
+        for (int q = 0; q < ST; q++) {
+            const uint32_t r2 = tid + 256u * q;
+            if (r2 >= 2u * BM) break;
+            const uint32_t st_r = r2 >> 1, st_part = r2 & 1u;
+            const u4_t v = *reinterpret_cast<const u4_t*>(st_src[q] + 8u * sb);
+            lds_da[(4u * st_part + 0u) * BM + st_r] = f16_bits_to_f32(v.x);
+            lds_da[(4u * st_part + 1u) * BM + st_r] = f16_bits_to_f32(v.y);
+            lds_da[(4u * st_part + 2u) * BM + st_r] = f16_bits_to_f32(v.z);
+            lds_da[(4u * st_part + 3u) * BM + st_r] = f16_bits_to_f32(v.w);
             // block activation sums d * s (s = sum(x)/d in f16), f32 [row][s]
             float4 sx;
             sx.x = f16_bits_to_f32(v.x) * f16_bits_to_f32(v.x >> 16);
@@ -321,11 +341,11 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll 1
         for (uint32_t g = 0; g < 4; g++) {
             // this step's prefetched operands; issue the next step's loads
-            u4_t a_cur[2][2], qv_cur[2];
+            u4_t a_cur[2][MI], qv_cur[2];
 #pragma unroll
             for (int e = 0; e < 2; e++)
 #pragma unroll
-                for (int i = 0; i < 2; i++) a_cur[e][i] = a_nx[e][i];
+                for (int i = 0; i < MI; i++) a_cur[e][i] = a_nx[e][i];
 #pragma unroll
             for (int j = 0; j < 2; j++) qv_cur[j] = qv_nx[j];
             {
@@ -372,16 +392,16 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const uint32_t s = 2u * g + e;
-                v4i_t a[2];
+                v4i_t a[MI];
 #pragma unroll
-                for (int i = 0; i < 2; i++) a[i] = as_v4i(a_cur[e][i]);
+                for (int i = 0; i < MI; i++) a[i] = as_v4i(a_cur[e][i]);
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
+                for (int i = 0; i < MI; i++) {
                     // scale-product A operand: this lane's row's activation scale
                     // (f16), in slots 0-5 for Q4_K (against d * 2^k), slot 0 otherwise
                     u4_t sa = {0u, 0u, 0u, 0u};
                     if (!DOTS) {
-                        const float da = lds_da[s * MMQ_BM + 64u * wm + 32u * i + l32];
+                        const float da = lds_da[s * BM + WM * wm + 32u * i + l32];
                         const uint32_t dab = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)da) & lo_mask;
                         if (TY == TY_Q4K) {
                             const uint32_t p = h2_dup(dab);
@@ -406,12 +426,12 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                             const uint32_t col = n0 + 64u * wn + 32u * j + l32;
 #pragma unroll
                             for (int r = 0; r < 16; r++) {
-                                const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+                                const uint32_t row = m0 + WM * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
                                 if (row < ds.m && col < ds.n)
                                     ds.dots_out[((uint64_t)row * ds.n + col) * nkb + 8u * sb + s] = D[r];
                             }
                         } else {
-                            const u4_t sbo = TY == TY_Q4K ? q4k_scale_operand(d2[j], wsb[j][e])
+                            const u4_t sbo = TY == TY_Q4K ? q4k_scale_operand(d2[j], wsb[j][e], lds_masks)
                                                           : u4_t{wsb[j][e] & lo_mask, 0u, 0u, 0u};
                             const v16f_t S = scale_products(sa, sbo);
 #pragma unroll
@@ -428,8 +448,8 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll
             for (int j = 0; j < 2; j++) q4k_offsets(hdr[j], h, cw[j]);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const float* sxp = lds_sx + (64u * wm + 32u * i + l32) * 8u + h;
+            for (int i = 0; i < MI; i++) {
+                const float* sxp = lds_sx + (WM * wm + 32u * i + l32) * 8u + h;
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     const float sx = sxp[2 * t];
@@ -445,13 +465,13 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
     if (DOTS) return;
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const uint32_t col = n0 + 64u * wn + 32u * j + l32;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const uint32_t row = m0 + 64u * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
+                const uint32_t row = m0 + WM * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
                 if (row < ds.m && col < ds.n) y[(uint64_t)row * ds.ldy + col] = acc[i][j][r];
             }
         }
@@ -474,20 +494,22 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
 
 // The GEMM kernels are held to 2 waves per SIMD (no spills at this budget) so
 // that one wave's epilogue overlaps another's MFMAs and loads; the block-dot
-// test hooks keep the default budget.
-#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS, WPE)                                       \
+// test hooks keep the default budget. (MI = 4, 256-row tiles, needs more than
+// the 256 registers of 2 waves per SIMD and spills.)
+#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS, WPE, MI)                                   \
     extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
-        __shared__ float lds_da[8 * MMQ_BM];                                  \
-        __shared__ float lds_sx[MMQ_BM * 8];                                  \
+        __shared__ float lds_da[8 * 64 * MI];                                 \
+        __shared__ float lds_sx[64 * MI * 8];                                 \
+        __shared__ u4_t lds_masks[64];                                        \
         const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
-        mmq_tile<TY, DOTS>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx);       \
+        mmq_tile<TY, DOTS, MI>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx, lds_masks); \
     }
-RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1, 2)
 
 // y[i] = sum_z ws[z][i], added in split order (deterministic).
 extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float* __restrict__ ws,
