@@ -43,6 +43,8 @@ typedef uint32_t u4a4_t __attribute__((ext_vector_type(4), aligned(4)));
 RFXQ_DEV u4_t ld16(const void* p) { return *(const RFXQ_GLOBAL u4_t*)p; }
 // Four dwords from a dword-aligned global address.
 RFXQ_DEV u4_t ld16_a4(const void* p) { return *(const RFXQ_GLOBAL u4a4_t*)p; }
+// Two dwords from an 8-byte-aligned global address.
+RFXQ_DEV u2_t ld8(const void* p) { return *(const RFXQ_GLOBAL u2_t*)p; }
 RFXQ_DEV uint32_t ld4(const void* p) { return *(const RFXQ_GLOBAL uint32_t*)p; }
 RFXQ_DEV uint32_t ld2(const void* p) { return *(const RFXQ_GLOBAL uint16_t*)p; }
 typedef float f4v_t __attribute__((ext_vector_type(4)));

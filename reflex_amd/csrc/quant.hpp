@@ -19,9 +19,12 @@
 
 // Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
 // wave_global); 8 lanes per 32-block.
+// xh (optional): the same int8 values as f16, each group of four stored
+// pair-permuted (q0, q2), (q1, q3) -- the A operand of the f16-MFMA MMQ.
 RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
                               uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
-                              uint32_t* __restrict__ xds, uint64_t wave_global, uint64_t nwaves) {
+                              uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint64_t wave_global,
+                              uint64_t nwaves) {
     const uint32_t nblk = k / 32u;
     const uint64_t total = (uint64_t)rows * nblk;
     const uint32_t lane = threadIdx.x & 63u;
@@ -48,7 +51,14 @@ RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const i
         if (valid) {
             const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
                                     ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
-            *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
+            if (xq) *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
+            if (xh) {
+                const h2_t a = {(half_t)q0, (half_t)q2}, b = {(half_t)q1, (half_t)q3};
+                uint2 hv;
+                hv.x = h2_bits(a);
+                hv.y = h2_bits(b);
+                *reinterpret_cast<uint2*>(xh + (uint64_t)row * k + 32u * blk + 4u * part) = hv;
+            }
             if (part == 0u) {
                 const uint32_t dbits = __builtin_bit_cast(uint16_t, (half_t)d);
                 // round the product to f32 first (no fused single-rounding mixed mad)
@@ -65,9 +75,10 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
                                                                     const int32_t* __restrict__ src_rows,
                                                                     uint32_t rows, uint32_t k,
                                                                     int8_t* __restrict__ xq, uint32_t ldq,
-                                                                    uint32_t* __restrict__ xds) {
-    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6,
-                    ((uint64_t)gridDim.x * blockDim.x) >> 6);
+                                                                    uint32_t* __restrict__ xds,
+                                                                    uint16_t* __restrict__ xh) {
+    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, xh,
+                    ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
 }
 
 // Several activations in one launch (grouped GEMMs): workgroups
@@ -76,6 +87,7 @@ struct QuantDesc {
     const float* x;
     int8_t* xq;
     uint32_t* xds;
+    uint16_t* xh;  // optional f16 copy
     uint32_t rows, k, wg_begin, wgs;
 };
 
@@ -89,6 +101,21 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1_multi(const
     }
     const QuantDesc d = table[lo];
     const uint32_t wg = blockIdx.x - d.wg_begin;
-    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6,
-                    ((uint64_t)d.wgs * blockDim.x) >> 6);
+    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, d.xh,
+                    ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6, ((uint64_t)d.wgs * blockDim.x) >> 6);
+}
+
+// int8 activations -> the pair-permuted f16 layout of quant_q8_1_rows' xh
+// (for the block-dot test hook of the f16-MFMA kernel)
+extern "C" __global__ __launch_bounds__(256) void rfxq_i8_to_f16_perm(const int8_t* __restrict__ xq,
+                                                                     uint16_t* __restrict__ xh, uint64_t n4) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * 256u) {
+        const uint32_t w = reinterpret_cast<const uint32_t*>(xq)[i];
+        const h2_t a = {(half_t)(int8_t)(w & 0xFFu), (half_t)(int8_t)((w >> 16) & 0xFFu)};
+        const h2_t b = {(half_t)(int8_t)((w >> 8) & 0xFFu), (half_t)(int8_t)(w >> 24)};
+        uint2 hv;
+        hv.x = h2_bits(a);
+        hv.y = h2_bits(b);
+        reinterpret_cast<uint2*>(xh)[i] = hv;
+    }
 }

@@ -111,6 +111,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {};
+    hipFunction_t mmqh_q4k = nullptr, dotsh_q4k = nullptr, i8_to_f16 = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     void* ws = nullptr;
@@ -151,6 +152,9 @@ int load_ctx(int device, Ctx** out) {
         {&c->dots[0], "rfxq_mmq_dots_q4k"},
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
+        {&c->mmqh_q4k, "rfxq_mmqh_q4k"},
+        {&c->dotsh_q4k, "rfxq_mmqh_dots_q4k"},
+        {&c->i8_to_f16, "rfxq_i8_to_f16_perm"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
         {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
         {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
@@ -414,9 +418,13 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 
 uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
 
+// Q4_K prefill GEMMs on the f16-MFMA kernel (exact integer block dots, no
+// per-element convert) instead of the int8-MFMA one: REFLEX_MMQ_F16=1.
+bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 0) != 0; }
+
 struct GemmPlan {
     uint32_t splits, sb_per_split, tiles_m, tiles_n;
-    uint64_t off_xds, off_part, total;
+    uint64_t off_xds, off_xh, off_part, total;
 };
 
 GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
@@ -433,7 +441,8 @@ GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
     p.sb_per_split = (nsb + splits - 1u) / splits;
     p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
     p.off_xds = align256((uint64_t)rows * k);
-    p.off_part = p.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+    p.off_xh = p.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+    p.off_part = p.off_xh + (mmq_f16() ? align256((uint64_t)rows * k * 2u) : 0u);
     p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
     return p;
 }
@@ -444,7 +453,7 @@ uint32_t quant_grid(uint64_t blocks) {
 }
 
 int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
-                 int8_t* xq, uint32_t* xds, hipStream_t stream) {
+                 int8_t* xq, uint32_t* xds, hipStream_t stream, uint16_t* xh = nullptr) {
     struct {
         const float* x;
         uint32_t ldx, pad0;
@@ -453,19 +462,23 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
         int8_t* xq;
         uint32_t ldq, pad1;
         uint32_t* xds;
-    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds};
+        uint16_t* xh;
+    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds, xh};
     return launch(c->quant, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
                   "rfxq_quantize_q8_1 launch");
 }
 
+// f16: Q4_K descriptors point at the f16 activation copy (ldq = 2k bytes)
+// and run on the f16-MFMA kernel
 int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
-               bool dots, hipStream_t stream) {
+               bool dots, hipStream_t stream, bool f16 = false) {
     MmqArgs a;
     std::memset(&a, 0, sizeof a);
     a.ndesc = count;
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : c->mmq[type_index(ty)];
+    if (f16 && ty == RFXQ_TYPE_Q4_K) f = dots ? c->dotsh_q4k : c->mmqh_q4k;
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
 }
 
@@ -491,25 +504,27 @@ int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float
     int8_t* xq = reinterpret_cast<int8_t*>(base);
     uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
     float* part = reinterpret_cast<float*>(base + p.off_part);
-    if (int rc = launch_quant(c, x, k, nullptr, rows, k, xq, xds, stream)) return rc;
+    const bool f16 = mmq_f16() && w->ggml_type == RFXQ_TYPE_Q4_K;
+    uint16_t* xh = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xh) : nullptr;
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, xds, stream, xh)) return rc;
     MmqDesc d;
     std::memset(&d, 0, sizeof d);
     d.w = w->data;
-    d.xq = xq;
+    d.xq = f16 ? reinterpret_cast<const int8_t*>(xh) : xq;
     d.xds = xds;
     d.y = p.splits > 1 ? part : y;
     d.m = rows;
     d.n = n;
     d.k = k;
     d.type = w->ggml_type;
-    d.ldq = k;
+    d.ldq = f16 ? 2u * k : k;
     d.ldy = n;
     d.tiles_m = p.tiles_m;
     d.tiles_n = p.tiles_n;
     d.splits = p.splits;
     d.sb_per_split = p.sb_per_split;
     const uint32_t wgs = p.tiles_m * p.tiles_n * p.splits;
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream)) return rc;
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, f16)) return rc;
     if (p.splits > 1) {
         struct {
             const float* ws;
@@ -533,8 +548,9 @@ struct GemmGroup {
     struct Act {
         const float* x;
         uint32_t k;
-        uint64_t off_xq, off_xds;
+        uint64_t off_xq, off_xds, off_xh;  // off_xh: f16 copy (f16 mode)
     };
+    bool f16 = false;
     std::vector<Act> acts;
     std::vector<MmqDesc> descs[3];  // per type_index
     uint32_t wgs[3] = {0, 0, 0};
@@ -543,6 +559,7 @@ struct GemmGroup {
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
+    g->f16 = mmq_f16();
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
@@ -553,25 +570,28 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
-            GemmGroup::Act act{it.x, k, 0, 0};
+            GemmGroup::Act act{it.x, k, 0, 0, 0};
             act.off_xq = g->ws_bytes;
             act.off_xds = act.off_xq + align256((uint64_t)rows * k);
-            g->ws_bytes = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+            act.off_xh = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
+            g->ws_bytes = act.off_xh + (g->f16 ? align256((uint64_t)rows * k * 2u) : 0u);
             g->acts.push_back(act);
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
         }
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
+        const bool f16 = g->f16 && it.w->ggml_type == RFXQ_TYPE_Q4_K;
         d.w = it.w->data;
-        d.xq = reinterpret_cast<const int8_t*>(g->acts[ai].off_xq);   // offsets until the workspace is known
+        // offsets until the workspace is known
+        d.xq = reinterpret_cast<const int8_t*>(f16 ? g->acts[ai].off_xh : g->acts[ai].off_xq);
         d.xds = reinterpret_cast<const uint32_t*>(g->acts[ai].off_xds);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
         d.k = k;
         d.type = it.w->ggml_type;
-        d.ldq = k;
+        d.ldq = f16 ? 2u * k : k;
         d.ldy = d.n;
         d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
         d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
@@ -597,7 +617,8 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
 int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
     for (const auto& a : g.acts)
         if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k, reinterpret_cast<int8_t*>(ws + a.off_xq),
-                                  reinterpret_cast<uint32_t*>(ws + a.off_xds), stream))
+                                  reinterpret_cast<uint32_t*>(ws + a.off_xds), stream,
+                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr))
             return rc;
     return RFXQ_OK;
 }
@@ -661,9 +682,10 @@ struct QuantDesc {
     const float* x;
     int8_t* xq;
     uint32_t* xds;
+    uint16_t* xh;
     uint32_t rows, k, wg_begin, wgs;
 };
-static_assert(sizeof(QuantDesc) == 40, "QuantDesc layout");
+static_assert(sizeof(QuantDesc) == 48, "QuantDesc layout");
 
 struct rfxq_gemm_plan {
     int device;
@@ -899,7 +921,7 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream)) return rc;
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16)) return rc;
         }
     }
     return ok();
@@ -943,7 +965,9 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
         for (const auto& a : plan->g.acts) {
             const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
             q.push_back(QuantDesc{a.x, reinterpret_cast<int8_t*>(base + a.off_xq),
-                                  reinterpret_cast<uint32_t*>(base + a.off_xds), rows, a.k, plan->qgrid, wgs});
+                                  reinterpret_cast<uint32_t*>(base + a.off_xds),
+                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr, rows, a.k,
+                                  plan->qgrid, wgs});
             plan->qgrid += wgs;
         }
         plan->qtable = reinterpret_cast<QuantDesc*>(base + off);
@@ -978,7 +1002,7 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
         const uint32_t n = (uint32_t)v.size();
         if (n <= kMmqInline) std::copy(v.begin(), v.end(), tmp);
         if (int rc = launch_mmq(c, v[0].type, tmp, n, n <= kMmqInline ? nullptr : plan->table[t], plan->g.wgs[t],
-                                false, stream))
+                                false, stream, plan->g.f16))
             return rc;
     }
     return ok();
@@ -1012,7 +1036,22 @@ int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, co
     d.splits = 1;
     d.sb_per_split = d.k / 256u;
     d.dots_out = dots;
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, d.tiles_m * d.tiles_n, true, stream)) return rc;
+    const bool f16 = mmq_f16() && w->ggml_type == RFXQ_TYPE_Q4_K;
+    if (f16) {  // the f16 kernel reads the pair-permuted f16 copy of xq
+        void* ws = nullptr;
+        const uint64_t n4 = (uint64_t)rows * d.k / 4u;
+        if (int rc = ctx_workspace(c, n4 * 8u, &ws)) return rc;
+        struct {
+            const int8_t* xq;
+            uint16_t* xh;
+            uint64_t n4;
+        } a = {xq, static_cast<uint16_t*>(ws), n4};
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>((n4 + 255u) / 256u, 8192u);
+        if (int rc = launch(c->i8_to_f16, blocks, 0, stream, &a, sizeof a, "rfxq_i8_to_f16_perm launch")) return rc;
+        d.xq = static_cast<const int8_t*>(ws);
+        d.ldq = 2u * d.k;
+    }
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, d.tiles_m * d.tiles_n, true, stream, f16)) return rc;
     return ok();
 }
 

@@ -226,3 +226,62 @@ def test_gemm_batch_errors(rq):
     y = torch.empty(64 * 256, device=DEV)
     with pytest.raises(rq.ReflexError):
         rq.gemm_batch([(x, w1, y), (x, w2, y)], 64)   # one x with two in_features
+
+
+# ------------------------------------------------------------------ f16-MFMA Q4_K kernel
+
+@pytest.fixture
+def f16_mode(monkeypatch):
+    """Q4_K GEMMs on the f16-MFMA kernel (REFLEX_MMQ_F16=1): int8 activations and
+    centered 4-bit codes are exact in f16, so its block dots are the same
+    integers and its outputs the same bits as the int8-MFMA kernel's."""
+    monkeypatch.setenv("REFLEX_MMQ_F16", "1")
+    yield
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 8, 512), (37, 70, 512), (130, 129, 768), (1, 300, 256)])
+def test_mmq_f16_block_dots_bit_exact(rq, orc, f16_mode, m, n, k):
+    w_np = orc.synthetic(Q4K, k, n, 31 + m)
+    x = orc.activations(m * k, 5 + n).reshape(m, k) * 3
+    xq, xds = rq.quantize_q8_1(_dev(x), m, k)
+    got = rq.mmq_block_dots(xq, xds, m, _weight(rq, Q4K, w_np, n, k)).cpu().numpy()
+    assert np.array_equal(got, orc.block_dots(Q4K, w_np, n, k, xq.cpu().numpy()))
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 200, 1024), (33, 200, 1024), (129, 1000, 2048), (512, 1024, 1024),
+                                   (513, 3072, 1024)])
+def test_gemm_f16_kernel_matches_int8_kernel(rq, orc, monkeypatch, m, n, k):
+    w_np = synth.weights(Q4K, n, k, 90 + m)
+    x = synth.activations(m * k, 91 + m).reshape(m, k)
+    w = _weight(rq, Q4K, w_np, n, k)
+    y8 = rq.gemm(_dev(x), w, m).cpu().numpy()
+    monkeypatch.setenv("REFLEX_MMQ_F16", "1")
+    yh = rq.gemm(_dev(x), w, m).cpu().numpy()
+    assert np.array_equal(yh, y8)
+    _check_gemm(rq, orc, Q4K, m, n, k, w_np, x, np.arange(0, m, max(1, m // 16)))
+
+
+def test_gemm_f16_plan_matches_single_gemms(rq, f16_mode):
+    rows = 300
+    shapes = [(Q4K, 768, 1024), (Q6K, 256, 1024), (Q4K, 640, 2048)]
+    xa = _dev(synth.activations(rows * 1024, 73))
+    xb = _dev(synth.activations(rows * 2048, 74))
+    items = []
+    for i, (ty, n, k) in enumerate(shapes):
+        w = _weight(rq, ty, synth.weights(ty, n, k, 85 + i), n, k)
+        items.append((xa if k == 1024 else xb, w, torch.empty(rows * n, device=DEV)))
+    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
+    try:
+        singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
+    finally:
+        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
+    rq.gemm_batch(items, rows)
+    for (_, _, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)
+    plan = rq.GemmPlan(items, rows)
+    for _ in range(2):
+        for _, _, y in items:
+            y.zero_()
+        plan.run()
+        for (_, _, y), ref in zip(items, singles):
+            assert np.array_equal(y.cpu().numpy(), ref)
