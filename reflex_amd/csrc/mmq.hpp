@@ -75,32 +75,6 @@ RFXQ_DEV v16f_t scale_products(u4_t a, u4_t b) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(a), as_h8(b), z, 0, 0, 0);
 }
 
-// D += A . B on f16 operands (32x32x16); used with exactly representable
-// integers (int8 activations, 4-bit codes), so D holds the exact integer dot
-RFXQ_DEV v16f_t mfma_h(u4_t a, u4_t b, v16f_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(a), as_h8(b), c, 0, 0, 0);
-}
-
-// Q4_K codes of one 16-k MFMA step as f16, centered (q - 8), in the
-// pair-permuted slot order of the activations: from the step's 8 qs bytes
-// (v0, v1), low nibbles (sub-block 2g) or high nibbles (2g + 1). A nibble is
-// masked into the mantissa of 1024.0 (1024 + q, or 1024 + 16q for the high
-// one), then shifted exactly to q - 8 by one packed f16 op.
-RFXQ_DEV u4_t q4k_codes_f16(uint32_t v0, uint32_t v1, bool hi, uint32_t MG) {
-    const uint32_t m = hi ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t w[4] = {(v0 & m) | MG, ((v0 >> 8) & m) | MG, (v1 & m) | MG, ((v1 >> 8) & m) | MG};
-    u4_t r;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const h2_t x = as_h2(w[t]);
-        const h2_t y = hi ? __builtin_elementwise_fma(x, h2_t{(half_t)0.0625f, (half_t)0.0625f},
-                                                      h2_t{(half_t)-72.0f, (half_t)-72.0f})
-                          : x + h2_t{(half_t)-1032.0f, (half_t)-1032.0f};
-        r[t] = h2_bits(y);
-    }
-    return r;
-}
-
 // f16 bits of x twice in one dword
 RFXQ_DEV uint32_t h2_dup(uint32_t bits16) { return (bits16 & 0xFFFFu) * 0x00010001u; }
 
@@ -222,19 +196,13 @@ RFXQ_DEV u4_t q6_codes(u4_t ql, u4_t qh, uint32_t t) {
 RFXQ_DEV int sbyte(uint32_t w, uint32_t byte) { return (int)(int8_t)(w >> (8u * byte)); }
 
 // MI: 32-row MFMA tiles per wave along M (the workgroup tile is 64*MI x 128).
-// F16 (Q4_K): the block dots run on f16 MFMAs (two 32x32x16 steps per block)
-// over exact integer operands -- xq as f16 (desc.xq then points to the f16
-// copy, row stride ldq bytes) and centered codes as f16 -- so they arrive in
-// f32 already and the epilogue is a single FMA per element.
-template <uint32_t TY, bool DOTS, int MI, bool F16 = false>
+template <uint32_t TY, bool DOTS, int MI>
 RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float* lds_sx, u4_t* lds_masks) {
     constexpr uint32_t BM = 64u * MI, WM = 32u * MI;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave & 1u, wn = wave >> 1;
     const uint32_t h = lane >> 5, l32 = lane & 31u;
     const uint32_t lo_mask = h ? 0u : 0xFFFFFFFFu;  // scale-product K-slots live in lanes 0-31
-    uint32_t magic = 0u;  // F16: f16 1024.0 in both halves, in a VGPR (one v_and_or_b32 per pair)
-    if (F16) asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
     const uint32_t ks = t_local % ds.splits;
     const uint32_t rest = t_local / ds.splits;
@@ -254,7 +222,7 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
         uint32_t m = m0 + WM * wm + 32u * i + l32;
         m = m < ds.m ? m : ds.m - 1u;
         const uint32_t src = ds.rows ? (uint32_t)ds.rows[m] : m;
-        arow[i] = reinterpret_cast<const uint8_t*>(ds.xq) + (uint64_t)src * ds.ldq + 16u * h;  // F16: k 8h.. as f16
+        arow[i] = reinterpret_cast<const uint8_t*>(ds.xq) + (uint64_t)src * ds.ldq + 16u * h;
     }
     const uint8_t* brow[2];
 #pragma unroll
@@ -284,35 +252,17 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
     // Software pipeline: the activation operands of the next block pair (and,
     // for Q4_K, its weight quants and the next super-block's header) are
     // loaded while the current pair's MFMAs and epilogue run.
-    constexpr int AT = F16 ? 2 : 1;  // A registers per block: int8 one 16-B run, f16 two 16-k steps
-    u4_t a_nx[2][MI][AT], qv_nx[2], hdr_nx[2];
-    auto load_a = [&](uint32_t sbx, uint32_t gx, u4_t a[2][MI][AT]) {
+    u4_t a_nx[2][MI], qv_nx[2], hdr_nx[2];
+    auto load_a = [&](uint32_t sbx, uint32_t gx, u4_t a[2][MI]) {
 #pragma unroll
         for (int e = 0; e < 2; e++)
 #pragma unroll
-            for (int i = 0; i < MI; i++) {
-                const uint32_t s = 2u * gx + e;
-                if (F16) {
-                    a[e][i][0] = ld16(arow[i] + 512u * sbx + 64u * s);
-                    a[e][i][AT - 1] = ld16(arow[i] + 512u * sbx + 64u * s + 32u);
-                } else {
-                    a[e][i][0] = ld16(arow[i] + 256u * sbx + 32u * s);
-                }
-            }
+            for (int i = 0; i < MI; i++) a[e][i] = ld16(arow[i] + 256u * sbx + 32u * (2u * gx + e));
     };
-    // Q4_K quants of group gx: int8 path 16 bytes [16h, +16); F16 path the
-    // bytes of its two 16-k steps, [8h, +8) and [16 + 8h, +8)
+    // Q4_K quants of group gx: 16 bytes [16h, +16)
     auto load_q4 = [&](uint32_t sbx, uint32_t gx, u4_t q[2]) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint8_t* g0 = brow[j] + (uint64_t)sbx * 144u + 16u + 32u * gx;
-            if (F16) {
-                const u2_t lo = ld8(g0 + 8u * h), hi = ld8(g0 + 16u + 8u * h);
-                q[j] = u4_t{lo.x, lo.y, hi.x, hi.y};
-            } else {
-                q[j] = ld16(g0 + 16u * h);
-            }
-        }
+        for (int j = 0; j < 2; j++) q[j] = ld16(brow[j] + (uint64_t)sbx * 144u + 16u + 32u * gx + 16u * h);
     };
     if (sb0 < sb1) {
         load_a(sb0, 0u, a_nx);
@@ -392,13 +342,11 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll 1
         for (uint32_t g = 0; g < 4; g++) {
             // this step's prefetched operands; issue the next step's loads
-            u4_t a_cur[2][MI][AT], qv_cur[2];
+            u4_t a_cur[2][MI], qv_cur[2];
 #pragma unroll
             for (int e = 0; e < 2; e++)
 #pragma unroll
-                for (int i = 0; i < MI; i++)
-#pragma unroll
-                    for (int t = 0; t < AT; t++) a_cur[e][i][t] = a_nx[e][i][t];
+                for (int i = 0; i < MI; i++) a_cur[e][i] = a_nx[e][i];
 #pragma unroll
             for (int j = 0; j < 2; j++) qv_cur[j] = qv_nx[j];
             {
@@ -417,10 +365,8 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
             for (int j = 0; j < 2; j++) {
                 if (TY == TY_Q4K) {
                     const u4_t qv = qv_cur[j];
-                    if (!F16) {
-                        bw[j][0] = center8(nib_lo(qv));
-                        bw[j][1] = center8(nib_hi(qv));
-                    }
+                    bw[j][0] = center8(nib_lo(qv));
+                    bw[j][1] = center8(nib_hi(qv));
                     q4k_pair_sc(hdr[j], g, wsb[j][0], wsb[j][1]);
                 } else if (TY == TY_Q6K) {
                     const uint32_t n = g >> 1, t0 = 2u * (g & 1u);
@@ -449,7 +395,7 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                 const uint32_t s = 2u * g + e;
                 v4i_t a[MI];
 #pragma unroll
-                for (int i = 0; i < MI; i++) a[i] = as_v4i(a_cur[e][i][0]);
+                for (int i = 0; i < MI; i++) a[i] = as_v4i(a_cur[e][i]);
                 // scale-product A operands: each row tile's activation scale
                 // (f16), in slots 0-5 for Q4_K (against d * 2^k), slot 0 otherwise
                 u4_t sa[MI];
@@ -469,12 +415,6 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                 }
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    // F16: this column tile's code operands for both 16-k steps
-                    u4_t bh0 = {}, bh1 = {};
-                    if (F16) {
-                        bh0 = q4k_codes_f16(qv_cur[j].x, qv_cur[j].y, e == 1, magic);
-                        bh1 = q4k_codes_f16(qv_cur[j].z, qv_cur[j].w, e == 1, magic);
-                    }
                     u4_t sbo = {};
                     if (!DOTS)
                         sbo = TY == TY_Q4K ? q4k_scale_operand(d2[j], wsb[j][e], lds_masks)
@@ -482,11 +422,7 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 #pragma unroll
                     for (int i = 0; i < MI; i++) {
                         v16i_t D;
-                        v16f_t Dh;
-                        if (F16) {
-                            Dh = mfma_h(a_cur[e][i][0], bh0, v16f_t{});
-                            Dh = mfma_h(a_cur[e][i][AT - 1], bh1, Dh);
-                        } else if (TY == TY_Q6K) {
+                        if (TY == TY_Q6K) {
                             const u4_t z = {0u, 0u, 0u, 0u};
                             const v16i_t D0 = mfma_i8(a[i], as_v4i(h ? z : bw[j][e]));
                             const v16i_t D1 = mfma_i8(a[i], as_v4i(h ? bw[j][e] : z));
@@ -502,13 +438,13 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
                                 const uint32_t row = m0 + WM * wm + 32u * i + 8u * (r >> 2) + 4u * h + (r & 3);
                                 if (row < ds.m && col < ds.n)
                                     ds.dots_out[((uint64_t)row * ds.n + col) * nkb + 8u * sb + s] =
-                                        F16 ? (int32_t)Dh[r] : D[r];
+                                        D[r];
                             }
                         } else {
                             const v16f_t S = scale_products(sa[i], sbo);
 #pragma unroll
                             for (int r = 0; r < 16; r++)
-                                acc[i][j][r] = fmaf(F16 ? Dh[r] : (float)D[r], S[r], acc[i][j][r]);
+                                acc[i][j][r] = fmaf((float)D[r], S[r], acc[i][j][r]);
                         }
                     }
                 }
@@ -569,22 +505,20 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
 // that one wave's epilogue overlaps another's MFMAs and loads; the block-dot
 // test hooks keep the default budget. (MI = 4, 256-row tiles, needs more than
 // the 256 registers of 2 waves per SIMD and spills.)
-#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS, WPE, MI, F16)                              \
+#define RFXQ_MMQ_ENTRY(NAME, TY, DOTS, WPE, MI)                              \
     extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
         __shared__ float lds_da[8 * 64 * MI];                                 \
         __shared__ float lds_sx[64 * MI * 8];                                 \
         __shared__ u4_t lds_masks[64];                                        \
         const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
-        mmq_tile<TY, DOTS, MI, F16>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx, lds_masks); \
+        mmq_tile<TY, DOTS, MI>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx, lds_masks); \
     }
-RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1, 2, false)
-RFXQ_MMQ_ENTRY(rfxq_mmqh_q4k, TY_Q4K, false, 2, 2, true)
-RFXQ_MMQ_ENTRY(rfxq_mmqh_dots_q4k, TY_Q4K, true, 1, 2, true)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1, 2)
+RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1, 2)
 
 // y[i] = sum_z ws[z][i], added in split order (deterministic).
 extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float* __restrict__ ws,

@@ -19,12 +19,14 @@
 
 // Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
 // wave_global); 8 lanes per 32-block.
-// xh (optional): the same int8 values as f16, each group of four stored
-// pair-permuted (q0, q2), (q1, q3) -- the A operand of the f16-MFMA MMQ.
+// Optional layouts for the f16-MFMA Q4_K kernel (mmq2.hpp):
+//   xh  [rows][k] f16: the int8 values, each group of four stored (q0, q2), (q1, q3)
+//   xsc [rows][k/256][24] u16: per super-block d[8], then Sx = d*s split
+//       exactly into f16 hi[8] and lo[8] (hi = f16(Sx), lo = f16(Sx - hi))
 RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
                               uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
-                              uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint64_t wave_global,
-                              uint64_t nwaves) {
+                              uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint16_t* __restrict__ xsc,
+                              uint64_t wave_global, uint64_t nwaves) {
     const uint32_t nblk = k / 32u;
     const uint64_t total = (uint64_t)rows * nblk;
     const uint32_t lane = threadIdx.x & 63u;
@@ -65,7 +67,16 @@ RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const i
                 float sid = sum * id;
                 asm volatile("" : "+v"(sid));
                 const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)sid);
-                xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
+                if (xds) xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
+                if (xsc) {
+                    const float sx = f16_bits_to_f32(dbits) * f16_bits_to_f32(sbits);  // exact in f32
+                    const half_t hi = (half_t)sx;
+                    const half_t lo = (half_t)(sx - (float)hi);
+                    uint16_t* rec = xsc + ((uint64_t)row * (nblk / 8u) + blk / 8u) * 24u + (blk & 7u);
+                    rec[0] = (uint16_t)dbits;
+                    rec[8] = __builtin_bit_cast(uint16_t, hi);
+                    rec[16] = __builtin_bit_cast(uint16_t, lo);
+                }
             }
         }
     }
@@ -76,8 +87,9 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
                                                                     uint32_t rows, uint32_t k,
                                                                     int8_t* __restrict__ xq, uint32_t ldq,
                                                                     uint32_t* __restrict__ xds,
-                                                                    uint16_t* __restrict__ xh) {
-    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, xh,
+                                                                    uint16_t* __restrict__ xh,
+                                                                    uint16_t* __restrict__ xsc) {
+    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, xh, xsc,
                     ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
 }
 
@@ -87,7 +99,8 @@ struct QuantDesc {
     const float* x;
     int8_t* xq;
     uint32_t* xds;
-    uint16_t* xh;  // optional f16 copy
+    uint16_t* xh;   // optional f16 copy
+    uint16_t* xsc;  // optional super-block scale records
     uint32_t rows, k, wg_begin, wgs;
 };
 
@@ -101,21 +114,6 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1_multi(const
     }
     const QuantDesc d = table[lo];
     const uint32_t wg = blockIdx.x - d.wg_begin;
-    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, d.xh,
+    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, d.xh, d.xsc,
                     ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6, ((uint64_t)d.wgs * blockDim.x) >> 6);
-}
-
-// int8 activations -> the pair-permuted f16 layout of quant_q8_1_rows' xh
-// (for the block-dot test hook of the f16-MFMA kernel)
-extern "C" __global__ __launch_bounds__(256) void rfxq_i8_to_f16_perm(const int8_t* __restrict__ xq,
-                                                                     uint16_t* __restrict__ xh, uint64_t n4) {
-    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * 256u) {
-        const uint32_t w = reinterpret_cast<const uint32_t*>(xq)[i];
-        const h2_t a = {(half_t)(int8_t)(w & 0xFFu), (half_t)(int8_t)((w >> 16) & 0xFFu)};
-        const h2_t b = {(half_t)(int8_t)((w >> 8) & 0xFFu), (half_t)(int8_t)(w >> 24)};
-        uint2 hv;
-        hv.x = h2_bits(a);
-        hv.y = h2_bits(b);
-        reinterpret_cast<uint2*>(xh)[i] = hv;
-    }
 }

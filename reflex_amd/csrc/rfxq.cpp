@@ -111,7 +111,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {};
-    hipFunction_t mmqh_q4k = nullptr, dotsh_q4k = nullptr, i8_to_f16 = nullptr;
+    hipFunction_t mmq2_q4k = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     void* ws = nullptr;
@@ -152,9 +152,7 @@ int load_ctx(int device, Ctx** out) {
         {&c->dots[0], "rfxq_mmq_dots_q4k"},
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
-        {&c->mmqh_q4k, "rfxq_mmqh_q4k"},
-        {&c->dotsh_q4k, "rfxq_mmqh_dots_q4k"},
-        {&c->i8_to_f16, "rfxq_i8_to_f16_perm"},
+        {&c->mmq2_q4k, "rfxq_mmq2_q4k"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
         {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
         {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
@@ -203,10 +201,10 @@ int ctx_workspace(Ctx* c, uint64_t bytes, void** out) {
 }
 
 int launch(hipFunction_t f, uint32_t grid, uint32_t lds, hipStream_t stream, void* args, size_t args_size,
-           const char* what) {
+           const char* what, uint32_t threads = 256) {
     void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
                    HIP_LAUNCH_PARAM_END};
-    HIPCHK(hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, lds, stream, nullptr, cfg), what);
+    HIPCHK(hipModuleLaunchKernel(f, grid, 1, 1, threads, 1, 1, lds, stream, nullptr, cfg), what);
     return RFXQ_OK;
 }
 
@@ -418,13 +416,28 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 
 uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
 
-// Q4_K prefill GEMMs on the f16-MFMA kernel (exact integer block dots, no
-// per-element convert) instead of the int8-MFMA one: REFLEX_MMQ_F16=1.
-bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 0) != 0; }
+// Q4_K prefill GEMMs run on the f16-MFMA kernel (rfxq_mmq2_q4k: exact integer
+// block dots, one FMA per element and block) unless REFLEX_MMQ_F16=0 selects
+// the int8-MFMA kernel. Gathered rows (MoE) always take the int8 kernel.
+constexpr uint32_t kMmq2Threads = 256;  // rfxq_mmq2_q4k workgroup
+bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 1) != 0; }
+
+// rfxq_mmq2_q4k for this GEMM: f16 mode, Q4_K, and every buffer offset of the
+// kernel's copies (rows and columns rounded up to the 128 tile) fits in 32 bits
+bool use_mmq2(const rfxq_weight* w, uint32_t rows) {
+    if (!mmq_f16() || w->ggml_type != RFXQ_TYPE_Q4_K) return false;
+    const uint64_t lim = 0xF0000000ull;
+    const uint64_t k = w->in_features, n = w->out_features;
+    return (n + 128u) * (k / 256u) * 144u < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
+}
+
+// bytes of the f16 activation copy and of the super-block scale records
+uint64_t xh_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * k * 2u); }
+uint64_t xsc_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * (k / 256u) * 48u); }
 
 struct GemmPlan {
     uint32_t splits, sb_per_split, tiles_m, tiles_n;
-    uint64_t off_xds, off_xh, off_part, total;
+    uint64_t off_xds, off_xh, off_xsc, off_part, total;
 };
 
 GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
@@ -442,7 +455,9 @@ GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
     p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
     p.off_xds = align256((uint64_t)rows * k);
     p.off_xh = p.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
-    p.off_part = p.off_xh + (mmq_f16() ? align256((uint64_t)rows * k * 2u) : 0u);
+    const bool f16 = mmq_f16();
+    p.off_xsc = p.off_xh + (f16 ? xh_bytes(rows, k) : 0u);
+    p.off_part = p.off_xsc + (f16 ? xsc_bytes(rows, k) : 0u);
     p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
     return p;
 }
@@ -453,7 +468,7 @@ uint32_t quant_grid(uint64_t blocks) {
 }
 
 int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
-                 int8_t* xq, uint32_t* xds, hipStream_t stream, uint16_t* xh = nullptr) {
+                 int8_t* xq, uint32_t* xds, hipStream_t stream, uint16_t* xh = nullptr, uint16_t* xsc = nullptr) {
     struct {
         const float* x;
         uint32_t ldx, pad0;
@@ -463,13 +478,14 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
         uint32_t ldq, pad1;
         uint32_t* xds;
         uint16_t* xh;
-    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds, xh};
+        uint16_t* xsc;
+    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds, xh, xsc};
     return launch(c->quant, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
                   "rfxq_quantize_q8_1 launch");
 }
 
-// f16: Q4_K descriptors point at the f16 activation copy (ldq = 2k bytes)
-// and run on the f16-MFMA kernel
+// f16: Q4_K descriptors carry the f16 activations (xq, ldq = 2k bytes) and
+// the scale records (xds) and run on rfxq_mmq2_q4k
 int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
                bool dots, hipStream_t stream, bool f16 = false) {
     MmqArgs a;
@@ -478,7 +494,8 @@ int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDes
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && ty == RFXQ_TYPE_Q4_K) f = dots ? c->dotsh_q4k : c->mmqh_q4k;
+    if (f16 && ty == RFXQ_TYPE_Q4_K && !dots)
+        return launch(c->mmq2_q4k, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq2 launch", kMmq2Threads);
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
 }
 
@@ -504,14 +521,16 @@ int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float
     int8_t* xq = reinterpret_cast<int8_t*>(base);
     uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
     float* part = reinterpret_cast<float*>(base + p.off_part);
-    const bool f16 = mmq_f16() && w->ggml_type == RFXQ_TYPE_Q4_K;
+    const bool f16 = use_mmq2(w, rows);
     uint16_t* xh = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xh) : nullptr;
-    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, xds, stream, xh)) return rc;
+    uint16_t* xsc = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xsc) : nullptr;
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, f16 ? nullptr : xds, stream, xh, xsc))
+        return rc;
     MmqDesc d;
     std::memset(&d, 0, sizeof d);
     d.w = w->data;
     d.xq = f16 ? reinterpret_cast<const int8_t*>(xh) : xq;
-    d.xds = xds;
+    d.xds = f16 ? reinterpret_cast<const uint32_t*>(xsc) : xds;
     d.y = p.splits > 1 ? part : y;
     d.m = rows;
     d.n = n;
@@ -548,7 +567,7 @@ struct GemmGroup {
     struct Act {
         const float* x;
         uint32_t k;
-        uint64_t off_xq, off_xds, off_xh;  // off_xh: f16 copy (f16 mode)
+        uint64_t off_xq, off_xds, off_xh, off_xsc;  // off_xh, off_xsc: f16 mode
     };
     bool f16 = false;
     std::vector<Act> acts;
@@ -559,7 +578,10 @@ struct GemmGroup {
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
+    // f16 kernel for the group's Q4_K GEMMs only if every one of them can take it
     g->f16 = mmq_f16();
+    for (uint32_t i = 0; i < count; i++)
+        if (items[i].w && items[i].w->ggml_type == RFXQ_TYPE_Q4_K && !use_mmq2(items[i].w, rows)) g->f16 = false;
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
@@ -570,11 +592,12 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
-            GemmGroup::Act act{it.x, k, 0, 0, 0};
+            GemmGroup::Act act{it.x, k, 0, 0, 0, 0};
             act.off_xq = g->ws_bytes;
             act.off_xds = act.off_xq + align256((uint64_t)rows * k);
             act.off_xh = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
-            g->ws_bytes = act.off_xh + (g->f16 ? align256((uint64_t)rows * k * 2u) : 0u);
+            act.off_xsc = act.off_xh + (g->f16 ? xh_bytes(rows, k) : 0u);
+            g->ws_bytes = act.off_xsc + (g->f16 ? xsc_bytes(rows, k) : 0u);
             g->acts.push_back(act);
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
@@ -585,7 +608,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         d.w = it.w->data;
         // offsets until the workspace is known
         d.xq = reinterpret_cast<const int8_t*>(f16 ? g->acts[ai].off_xh : g->acts[ai].off_xq);
-        d.xds = reinterpret_cast<const uint32_t*>(g->acts[ai].off_xds);
+        d.xds = reinterpret_cast<const uint32_t*>(f16 ? g->acts[ai].off_xsc : g->acts[ai].off_xds);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
@@ -618,7 +641,8 @@ int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipSt
     for (const auto& a : g.acts)
         if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k, reinterpret_cast<int8_t*>(ws + a.off_xq),
                                   reinterpret_cast<uint32_t*>(ws + a.off_xds), stream,
-                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr))
+                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr,
+                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xsc) : nullptr))
             return rc;
     return RFXQ_OK;
 }
@@ -683,9 +707,10 @@ struct QuantDesc {
     int8_t* xq;
     uint32_t* xds;
     uint16_t* xh;
+    uint16_t* xsc;
     uint32_t rows, k, wg_begin, wgs;
 };
-static_assert(sizeof(QuantDesc) == 48, "QuantDesc layout");
+static_assert(sizeof(QuantDesc) == 56, "QuantDesc layout");
 
 struct rfxq_gemm_plan {
     int device;
@@ -966,7 +991,8 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
             const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
             q.push_back(QuantDesc{a.x, reinterpret_cast<int8_t*>(base + a.off_xq),
                                   reinterpret_cast<uint32_t*>(base + a.off_xds),
-                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr, rows, a.k,
+                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr,
+                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xsc) : nullptr, rows, a.k,
                                   plan->qgrid, wgs});
             plan->qgrid += wgs;
         }
@@ -1036,22 +1062,7 @@ int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, co
     d.splits = 1;
     d.sb_per_split = d.k / 256u;
     d.dots_out = dots;
-    const bool f16 = mmq_f16() && w->ggml_type == RFXQ_TYPE_Q4_K;
-    if (f16) {  // the f16 kernel reads the pair-permuted f16 copy of xq
-        void* ws = nullptr;
-        const uint64_t n4 = (uint64_t)rows * d.k / 4u;
-        if (int rc = ctx_workspace(c, n4 * 8u, &ws)) return rc;
-        struct {
-            const int8_t* xq;
-            uint16_t* xh;
-            uint64_t n4;
-        } a = {xq, static_cast<uint16_t*>(ws), n4};
-        const uint32_t blocks = (uint32_t)std::min<uint64_t>((n4 + 255u) / 256u, 8192u);
-        if (int rc = launch(c->i8_to_f16, blocks, 0, stream, &a, sizeof a, "rfxq_i8_to_f16_perm launch")) return rc;
-        d.xq = static_cast<const int8_t*>(ws);
-        d.ldq = 2u * d.k;
-    }
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, d.tiles_m * d.tiles_n, true, stream, f16)) return rc;
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, d.tiles_m * d.tiles_n, true, stream)) return rc;
     return ok();
 }
 
