@@ -67,22 +67,14 @@ RFXQ_DEV void gemv_x_load(const float* __restrict__ x, uint32_t k, XRegs& xr, ui
     }
 }
 
-RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, bool prescale_hi) {
-    const float sc = (prescale_hi && (e & 32u)) ? 0.0625f : 1.0f;
+RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, bool prescale_hi, float scale) {
+    const float sc = (prescale_hi && (e & 32u)) ? 0.0625f * scale : scale;
     const h2_t a = {(half_t)(v.x * sc), (half_t)(v.z * sc)};
     const h2_t b = {(half_t)(v.y * sc), (half_t)(v.w * sc)};
     lds_st64(lds_addr(lds_x) + 2u * e, u2_t{h2_bits(a), h2_bits(b)});
 }
 
-RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
-                           uint32_t* lds_x, float* lds_s, uint32_t tid) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t e = 4u * tid + 1024u * i;
-        if (e < k) gemv_x_put(lds_x, e, xr.v[i], prescale_hi);
-    }
-    for (uint32_t e = 4u * tid + 4096u; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), prescale_hi);
-    lds_barrier();
+RFXQ_DEV void gemv_x_sums(const uint32_t* lds_x, float* lds_s, uint32_t k, uint32_t tid) {
     const uint32_t ng = k / 16u;
     for (uint32_t g = tid; g < ng; g += 256u) {
         u4_t p0, p1;
@@ -99,7 +91,57 @@ RFXQ_DEV void gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescal
         s = dot2(p1.w, one2, s);
         lds_st32(lds_addr(lds_s) + 4u * g, __builtin_bit_cast(uint32_t, s));
     }
+}
+
+// Returns the factor that undoes a range scaling of x: activations whose
+// magnitude reaches 2^15 would overflow f16, so in that (rare) case x is
+// staged again multiplied by an exact power of two 2^-s and row results are
+// multiplied by 2^s when stored; otherwise it is 1 and nothing changes.
+// lds_p (the row results, free while staging) carries the waves' maxima.
+RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
+                            uint32_t* lds_x, float* lds_s, float* lds_p, uint32_t tid) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t e = 4u * tid + 1024u * i;
+        if (e < k) {
+            gemv_x_put(lds_x, e, xr.v[i], prescale_hi, 1.0f);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xr.v[i].x), fabsf(xr.v[i].y)), fmaxf(fabsf(xr.v[i].z), fabsf(xr.v[i].w))));
+        }
+    }
+    for (uint32_t e = 4u * tid + 4096u; e < k; e += 1024u) {
+        const float4 v = ldf4(x + e);
+        gemv_x_put(lds_x, e, v, prescale_hi, 1.0f);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#ifndef RFXQ_GEMV_NORANGE
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    if ((tid & 63u) == 0u) lds_st32(lds_addr(lds_p) + 4u * (tid >> 6), __builtin_bit_cast(uint32_t, amax));
+#endif
     lds_barrier();
+#ifndef RFXQ_GEMV_NORANGE
+    {
+        const u4_t m4 = lds_ld128(lds_addr(lds_p));
+        amax = fmaxf(fmaxf(as_f32(m4.x), as_f32(m4.y)), fmaxf(as_f32(m4.z), as_f32(m4.w)));
+    }
+#else
+    amax = 0.0f;
+#endif
+    gemv_x_sums(lds_x, lds_s, k, tid);
+    lds_barrier();
+    float inv = 1.0f;
+    if (amax >= 32768.0f && amax <= 3.0e38f) {  // workgroup-uniform
+        int ex;
+        (void)frexpf(amax, &ex);  // amax < 2^ex
+        const float scale = ldexpf(1.0f, 14 - ex);
+        inv = ldexpf(1.0f, ex - 14);
+        for (uint32_t e = 4u * tid; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), prescale_hi, scale);
+        lds_barrier();
+        gemv_x_sums(lds_x, lds_s, k, tid);
+        lds_barrier();
+    }
+    return inv;
 }
 
 RFXQ_DEV uint32_t u4_at(const uint4* a, int j) {
@@ -499,7 +541,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
 #pragma unroll
     for (int t = 0; t < kRing; t++) issue(t);
     if (restage) lds_barrier();  // every wave is done with the previous segment's x
-    gemv_stage_x(dsc.x, k, T::QK == 256u && T::BB == 144u, xr, lds_x, lds_s, tid);
+    const float y_scale = gemv_stage_x(dsc.x, k, T::QK == 256u && T::BB == 144u, xr, lds_x, lds_s, lds_p, tid);
 
     // f16 1024.0 in both halves, kept in a VGPR: gfx9 VOP3 takes at most one
     // SGPR/constant, so (v & mask) | magic is one v_and_or_b32 only this way
@@ -518,14 +560,14 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
                 // most those of the other kRing - 1 slots are outstanding
                 // (stores issued since only make this wait longer)
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * NJ) : "memory");
-#ifndef RFXQ_NOMATH
-                float acc = T::dot(T::fetch(ring[t], uo + sh, unit), unit, xv, magic);
-#else
                 const typename T::Raw rr = T::fetch(ring[t], uo + sh, unit);
+                issue(t);  // the slot's reads are done (fetch waits for them): refill it during the math
+#ifndef RFXQ_NOMATH
+                float acc = T::dot(rr, unit, xv, magic);
+#else
                 float acc = 0.f;
                 for (uint32_t i = 0; i < sizeof(rr) / 4; i++) acc += as_f32(reinterpret_cast<const uint32_t*>(&rr)[i] & 0x3FFFFFFFu);
 #endif
-                issue(t);  // after the math: the slot's reads are done
                 acc = group_sum<LPR>(acc);
                 const uint32_t row = base0 + sub + cit * stride;
                 if (li == 0u && row < row_end) {
@@ -545,7 +587,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     for (uint32_t i = tid; i < row_end - row_begin; i += 256u)
-        bst4f(yr, (row_begin + i) * 4u, __builtin_bit_cast(float, lds_ld32(out0 + 4u * i)));
+        bst4f(yr, (row_begin + i) * 4u, __builtin_bit_cast(float, lds_ld32(out0 + 4u * i)) * y_scale);
 }
 
 template <typename T>

@@ -516,6 +516,10 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
 RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2, 2)
 RFXQ_MMQ_ENTRY(rfxq_mmq_q6k, TY_Q6K, false, 2, 2)
 RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0, TY_Q8_0, false, 2, 2)
+// 64-row tiles for short row groups (MoE experts at tens of rows each)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q4k_m64, TY_Q4K, false, 2, 1)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q6k_m64, TY_Q6K, false, 2, 1)
+RFXQ_MMQ_ENTRY(rfxq_mmq_q8_0_m64, TY_Q8_0, false, 2, 1)
 RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q4k, TY_Q4K, true, 1, 2)
 RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q6k, TY_Q6K, true, 1, 2)
 RFXQ_MMQ_ENTRY(rfxq_mmq_dots_q8_0, TY_Q8_0, true, 1, 2)

@@ -5,9 +5,10 @@
 // Inputs are the same Q8_1 activations as the int8 kernel, in two derived
 // layouts written by the quantizer: xh, the int8 values as f16 (group of four
 // stored (q0, q2), (q1, q3)), and xsc, one 48-byte record per row and
-// super-block: da[8] (the blocks' f16 scales), then Sx split exactly into
-// f16 hi[8] and lo[8] (Sx = da * s, the block's activation sum, f32-exact;
-// hi = f16(Sx), lo = f16(Sx - hi)).
+// super-block: da[8] (the blocks' f16 scales), then Sx' = Sx * 2^-6 split
+// exactly into f16 hi[8] and lo[8] (Sx = da * s, the block's activation sum,
+// f32-exact; hi = f16(Sx'), lo = f16(Sx' - hi); the 2^-6 keeps sums up to 4e6
+// in range and is undone by the 2^6 in the integer scale operands).
 //
 // For a Q4_K super-block with d, dmin, 6-bit (sc_b, m_b) and codes q:
 //   w = d*sc_b*(q - 8) + (8*d*sc_b - dmin*m_b)
@@ -95,14 +96,15 @@ RFXQ_DEV v16f_t mfma16(u4_t a, u4_t b, v16f_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(a), as_h8(b), c, 0, 0, 0);
 }
 
-// 8 integers < 1024 (two per dword, low half first) as f16 pairs
+// two small integers (exact in f16) as an f16 pair, low half first
 RFXQ_DEV uint32_t int_pair_f16(uint32_t lo, uint32_t hi) {
-    const h2_t x = as_h2(lo | (hi << 16) | 0x64006400u);  // 1024 + v, exact
-    return h2_bits(x + h2_t{(half_t)-1024.0f, (half_t)-1024.0f});
+    const h2_t x = {(half_t)(float)lo, (half_t)(float)hi};
+    return h2_bits(x);
 }
 
 // Q4_K scales of sub-blocks 0..7 (get_scale_min_k4, src/dequant.rs:39-47) as
-// the A operands of the super-block constant MFMAs: 8*sc_b and m_b, f16
+// the A operands of the super-block constant MFMAs: 8*sc_b*2^6 and m_b*2^6,
+// f16 (exact: at most 6 significant bits), against the activations' Sx*2^-6
 RFXQ_DEV void q4k_const_operands(const u4_t hdr, u4_t& usc, u4_t& um) {
     uint32_t sc[8], m[8];
 #pragma unroll
@@ -114,8 +116,8 @@ RFXQ_DEV void q4k_const_operands(const u4_t hdr, u4_t& usc, u4_t& um) {
     }
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        usc[p] = int_pair_f16(8u * sc[2 * p], 8u * sc[2 * p + 1]);
-        um[p] = int_pair_f16(m[2 * p], m[2 * p + 1]);
+        usc[p] = int_pair_f16(512u * sc[2 * p], 512u * sc[2 * p + 1]);
+        um[p] = int_pair_f16(64u * m[2 * p], 64u * m[2 * p + 1]);
     }
 }
 

@@ -21,8 +21,8 @@
 // wave_global); 8 lanes per 32-block.
 // Optional layouts for the f16-MFMA Q4_K kernel (mmq2.hpp):
 //   xh  [rows][k] f16: the int8 values, each group of four stored (q0, q2), (q1, q3)
-//   xsc [rows][k/256][24] u16: per super-block d[8], then Sx = d*s split
-//       exactly into f16 hi[8] and lo[8] (hi = f16(Sx), lo = f16(Sx - hi))
+//   xsc [rows][k/256][24] u16: per super-block d[8], then Sx' = d*s*2^-6
+//       split exactly into f16 hi[8] and lo[8] (hi = f16(Sx'), lo = f16(Sx' - hi))
 RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
                               uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
                               uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint16_t* __restrict__ xsc,
@@ -69,7 +69,8 @@ RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const i
                 const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)sid);
                 if (xds) xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
                 if (xsc) {
-                    const float sx = f16_bits_to_f32(dbits) * f16_bits_to_f32(sbits);  // exact in f32
+                    // Sx * 2^-6 (exact): keeps block sums up to 4e6 inside f16's range
+                    const float sx = f16_bits_to_f32(dbits) * f16_bits_to_f32(sbits) * 0.015625f;
                     const half_t hi = (half_t)sx;
                     const half_t lo = (half_t)(sx - (float)hi);
                     uint16_t* rec = xsc + ((uint64_t)row * (nblk / 8u) + blk / 8u) * 24u + (blk & 7u);

@@ -101,7 +101,8 @@ static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
 constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 48 KB weight ring)
-constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
+constexpr uint32_t kMaxGemvK = 16384;
+constexpr uint32_t kMoeGemvRows = 4;  // moe_ffn_grouped: up to this many tokens run as GEMVs  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 
 // ------------------------------------------------------------------ per-device module
 
@@ -110,16 +111,31 @@ struct Ctx {
     int cus = 256;
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
-    hipFunction_t mmq[3] = {}, dots[3] = {};
+    hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
     hipFunction_t mmq2_q4k = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
+    // device area for per-call descriptor tables (grow-only, separate from ws)
+    void* tab = nullptr;
+    uint64_t tab_bytes = 0;
+    // pinned host staging for stream-ordered table uploads: a ring of buffers,
+    // each reused once the copy that last read it has completed
+    struct Stage {
+        void* host = nullptr;
+        size_t bytes = 0;
+        hipEvent_t done = nullptr;
+        bool pending = false;
+    };
+    Stage stage[4];
+    uint32_t stage_next = 0;
 };
 
 std::mutex g_mu;
 std::map<int, std::unique_ptr<Ctx>> g_ctx;
+
+uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
 
 int type_index(uint32_t ty) { return ty == RFXQ_TYPE_Q4_K ? 0 : ty == RFXQ_TYPE_Q6_K ? 1 : 2; }
 
@@ -149,6 +165,9 @@ int load_ctx(int device, Ctx** out) {
         {&c->mmq[0], "rfxq_mmq_q4k"},
         {&c->mmq[1], "rfxq_mmq_q6k"},
         {&c->mmq[2], "rfxq_mmq_q8_0"},
+        {&c->mmq64[0], "rfxq_mmq_q4k_m64"},
+        {&c->mmq64[1], "rfxq_mmq_q6k_m64"},
+        {&c->mmq64[2], "rfxq_mmq_q8_0_m64"},
         {&c->dots[0], "rfxq_mmq_dots_q4k"},
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
@@ -171,6 +190,54 @@ int load_ctx(int device, Ctx** out) {
     }
     *out = c.get();
     g_ctx[device] = std::move(c);
+    return RFXQ_OK;
+}
+
+// Grow-only device area for per-call tables; growth waits for the device
+// (earlier launches may still read the old area).
+int ctx_tables(Ctx* c, uint64_t bytes, void** out) {
+    if (bytes > c->tab_bytes) {
+        if (c->tab) {
+            HIPCHK(hipDeviceSynchronize(), "hipDeviceSynchronize before table area growth");
+            HIPCHK(hipFree(c->tab), "hipFree(table area)");
+            c->tab = nullptr;
+            c->tab_bytes = 0;
+        }
+        const uint64_t sz = std::max<uint64_t>(bytes, 64u << 10);
+        hipError_t e = hipMalloc(&c->tab, sz);
+        if (e != hipSuccess) return fail(RFXQ_ERR_OUT_OF_MEMORY, "table area alloc of %llu bytes: %s",
+                                         (unsigned long long)sz, hipGetErrorString(e));
+        c->tab_bytes = sz;
+    }
+    *out = c->tab;
+    return RFXQ_OK;
+}
+
+// Stream-ordered upload of `bytes` from host memory to `dst` through a pinned
+// staging buffer: returns once the data is staged, without waiting for the
+// stream (the reference's per-expert pageable copies synchronise).
+int stage_upload(Ctx* c, void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return RFXQ_OK;
+    Ctx::Stage& s = c->stage[c->stage_next];
+    c->stage_next = (c->stage_next + 1u) % 4u;
+    if (s.pending) {
+        HIPCHK(hipEventSynchronize(s.done), "staging buffer reuse");
+        s.pending = false;
+    }
+    if (!s.done) HIPCHK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming), "hipEventCreate");
+    if (bytes > s.bytes) {
+        if (s.host) HIPCHK(hipHostFree(s.host), "hipHostFree");
+        s.host = nullptr;
+        s.bytes = 0;
+        const size_t sz = std::max<size_t>(bytes, 64u << 10);
+        hipError_t e = hipHostMalloc(&s.host, sz, hipHostMallocDefault);
+        if (e != hipSuccess) return fail(RFXQ_ERR_OUT_OF_MEMORY, "pinned staging alloc: %s", hipGetErrorString(e));
+        s.bytes = sz;
+    }
+    std::memcpy(s.host, src, bytes);
+    HIPCHK(hipMemcpyAsync(dst, s.host, bytes, hipMemcpyHostToDevice, stream), "table upload");
+    HIPCHK(hipEventRecord(s.done, stream), "hipEventRecord");
+    s.pending = true;
     return RFXQ_OK;
 }
 
@@ -293,7 +360,8 @@ int make_gemv_item(const float* x, const rfxq_weight* w, float* y, GemvItem* it)
     if (reinterpret_cast<uintptr_t>(y) % 4u) return fail(RFXQ_ERR_OTHER, "gemv: y is not 4-byte aligned");
     const uint32_t units = w->ggml_type == RFXQ_TYPE_Q8_0 ? k / 32u : k / 64u;
     uint32_t lpr_log2 = 0;
-    while (lpr_log2 < 6 && (units % (2u << lpr_log2)) == 0) lpr_log2++;
+    const uint32_t lpr_max = std::min<uint32_t>(6u, env_u32("RFXQ_GEMV_LPR_LOG2_MAX", 6));
+    while (lpr_log2 < lpr_max && (units % (2u << lpr_log2)) == 0) lpr_log2++;
     if (lpr_log2 < 2) lpr_log2 = 2;  // >= 4 lanes per row (units is always a multiple of 4 here)
     if (units % (1u << lpr_log2)) {
         // Q8_0 with k/32 not a multiple of 4: not supported by the lane mapping
@@ -336,7 +404,7 @@ int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_it
         part = std::max(part, max_iters[i] * v[i].rows_iter);
         kmax = std::max(kmax, v[i].d.k);
     }
-    part = (part + 3u) & ~3u;
+    part = (std::max(part, 4u) + 3u) & ~3u;  // at least 4: the x staging keeps the waves' maxima there
     *part_floats = part;
     *lds = part * 4u + kmax * 2u + kmax / 4u;
     if (*lds > kMaxLds) return fail(RFXQ_ERR_OTHER, "gemv: launch needs %u bytes of LDS", *lds);
@@ -364,7 +432,48 @@ int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t strea
     return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
 }
 
+void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector<GemvRange>* ranges,
+                      std::vector<uint32_t>* max_iters);
+
+// One launch over any number of GEMVs: descriptors and byte-balanced ranges
+// uploaded (stream-ordered) into the context's table area at byte `at`
+int gemv_launch_table(Ctx* c, const std::vector<GemvItem>& v, uint64_t at, hipStream_t stream) {
+    uint64_t total = 0, bytes = 0;
+    for (const auto& it : v) {
+        total += it.iters;
+        bytes += it.iters * it.iter_bytes;
+    }
+    const uint32_t grid = gemv_grid(c, total, bytes);
+    std::vector<GemvRange> ranges;
+    std::vector<uint32_t> max_iters;
+    gemv_split_bytes(v, grid, &ranges, &max_iters);
+    GemvArgs a;
+    std::memset(&a, 0, sizeof a);
+    uint32_t lds;
+    if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
+    const size_t tb = align256(sizeof(GemvDesc) * v.size()), rb = sizeof(GemvRange) * ranges.size();
+    std::vector<uint8_t> host(tb + rb, 0);
+    for (size_t i = 0; i < v.size(); i++) std::memcpy(host.data() + i * sizeof(GemvDesc), &v[i].d, sizeof(GemvDesc));
+    std::memcpy(host.data() + tb, ranges.data(), rb);
+    void* area;
+    if (int rc = ctx_tables(c, at + host.size(), &area)) return rc;
+    uint8_t* dst = static_cast<uint8_t*>(area) + at;
+    if (int rc = stage_upload(c, dst, host.data(), host.size(), stream)) return rc;
+    a.ndesc = (uint32_t)v.size();
+    a.table = reinterpret_cast<const GemvDesc*>(dst);
+    a.ranges = reinterpret_cast<const GemvRange*>(dst + tb);
+    if (v.size() <= kGemvInline)
+        for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
+    return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+}
+
 int gemv_items(Ctx* c, const rfxq_gemv_item* items, uint32_t count, hipStream_t stream) {
+    if (count > kGemvInline) {  // one launch over a descriptor table
+        std::vector<GemvItem> v(count);
+        for (uint32_t j = 0; j < count; j++)
+            if (int rc = make_gemv_item(items[j].x, items[j].w, items[j].y, &v[j])) return rc;
+        return gemv_launch_table(c, v, 0, stream);
+    }
     for (uint32_t i0 = 0; i0 < count; i0 += kGemvInline) {
         const uint32_t cnt = std::min<uint32_t>(kGemvInline, count - i0);
         std::vector<GemvItem> v(cnt);
@@ -414,7 +523,6 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 
 // ------------------------------------------------------------------ MMQ planning
 
-uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
 
 // Q4_K prefill GEMMs run on the f16-MFMA kernel (rfxq_mmq2_q4k: exact integer
 // block dots, one FMA per element and block) unless REFLEX_MMQ_F16=0 selects
@@ -486,15 +594,16 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
 
 // f16: Q4_K descriptors carry the f16 activations (xq, ldq = 2k bytes) and
 // the scale records (xds) and run on rfxq_mmq2_q4k
+// m64: the descriptors are tiled by 64 rows (rfxq_mmq_*_m64)
 int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
-               bool dots, hipStream_t stream, bool f16 = false) {
+               bool dots, hipStream_t stream, bool f16 = false, bool m64 = false) {
     MmqArgs a;
     std::memset(&a, 0, sizeof a);
     a.ndesc = count;
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
-    hipFunction_t f = dots ? c->dots[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && ty == RFXQ_TYPE_Q4_K && !dots)
+    hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
+    if (f16 && ty == RFXQ_TYPE_Q4_K && !dots && !m64)
         return launch(c->mmq2_q4k, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq2 launch", kMmq2Threads);
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
 }
@@ -654,30 +763,34 @@ int route_top_k(const float* logits, uint32_t n, uint32_t k, bool normalize, uin
     if (k == 0 || k > n) return fail(RFXQ_ERR_OTHER, "route_top_k: k (%u) must be in 1..=%u (logits.len())", k, n);
     float maxl = -INFINITY;
     for (uint32_t i = 0; i < n; i++) maxl = std::max(maxl, logits[i]);
-    std::vector<float> probs(n);
+    thread_local std::vector<float> probs;
+    thread_local std::vector<uint32_t> best;
+    probs.resize(n);
     float sum = 0.0f;
-    for (uint32_t i = 0; i < n; i++) {
-        probs[i] = std::exp(logits[i] - maxl);
-    }
+    for (uint32_t i = 0; i < n; i++) probs[i] = std::exp(logits[i] - maxl);
     for (uint32_t i = 0; i < n; i++) sum += probs[i];
     if (!std::isfinite(sum) || sum <= 0.0f)
         return fail(RFXQ_ERR_OTHER, "route_top_k: softmax sum is non-finite or non-positive (%g)", (double)sum);
     for (uint32_t i = 0; i < n; i++) probs[i] = probs[i] / sum;
-    std::vector<uint32_t> order(n);
-    for (uint32_t i = 0; i < n; i++) order[i] = i;
-    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
-        if (probs[a] > probs[b]) return true;
-        if (probs[a] < probs[b]) return false;
-        return a < b;
-    });
+    // the k best in (probability descending, index ascending) order: the
+    // first k of a stable sort, by insertion into a sorted list of k
+    best.clear();
+    for (uint32_t i = 0; i < n; i++) {
+        const float p = probs[i];
+        if (best.size() == k && !(p > probs[best.back()])) continue;  // ties keep the lower index
+        uint32_t pos = (uint32_t)best.size();
+        while (pos > 0 && p > probs[best[pos - 1]]) pos--;
+        best.insert(best.begin() + pos, i);
+        if (best.size() > k) best.pop_back();
+    }
     float top_sum = 0.0f;
-    for (uint32_t t = 0; t < k; t++) top_sum += probs[order[t]];
+    for (uint32_t t = 0; t < k; t++) top_sum += probs[best[t]];
     if (normalize && (!std::isfinite(top_sum) || top_sum <= 0.0f))
         return fail(RFXQ_ERR_OTHER, "route_top_k: top-%u probability mass is non-finite or non-positive (%g)", k,
                     (double)top_sum);
     for (uint32_t t = 0; t < k; t++) {
-        idx[t] = order[t];
-        w[t] = normalize ? probs[order[t]] / top_sum : probs[order[t]];
+        idx[t] = best[t];
+        w[t] = normalize ? probs[best[t]] / top_sum : probs[best[t]];
     }
     return RFXQ_OK;
 }
@@ -1197,6 +1310,61 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     }
     off[expert_count] = p;
 
+    // Few tokens (decode): every routed pair is a GEMV of its expert's
+    // slices (gate and up in one launch, down in another): weights are read
+    // once per pair at HBM rate instead of through 128-row MMQ tiles.
+    if (rows <= kMoeGemvRows) {
+        const uint64_t g_gate = 0;
+        const uint64_t g_up = g_gate + align256((uint64_t)P * ffn * 4u);
+        const uint64_t g_down = g_up + align256((uint64_t)P * ffn * 4u);
+        const uint64_t g_ci = g_down + align256((uint64_t)P * hidden * 4u);
+        const uint64_t g_cw = g_ci + align256((uint64_t)rows * top_k * 4u);
+        const uint64_t g_total = g_cw + align256((uint64_t)rows * top_k * 4u);
+        void* ws;
+        if (int rc = ctx_workspace(c, g_total, &ws)) return rc;
+        uint8_t* B = static_cast<uint8_t*>(ws);
+        float* gout = reinterpret_cast<float*>(B + g_gate);
+        float* uout = reinterpret_cast<float*>(B + g_up);
+        float* dout = reinterpret_cast<float*>(B + g_down);
+        std::vector<rfxq_weight> gs(expert_count), us(expert_count), ds(expert_count);
+        std::vector<GemvItem> gu, dn;
+        for (uint32_t e = 0; e < expert_count; e++) {
+            if (off[e + 1] == off[e]) continue;
+            expert_slice(gate, e, &gs[e], "moe_ffn_grouped");
+            expert_slice(up, e, &us[e], "moe_ffn_grouped");
+            expert_slice(down, e, &ds[e], "moe_ffn_grouped");
+            for (uint32_t q = off[e]; q < off[e + 1]; q++) {
+                const float* xr = x + (uint64_t)pair_row[q] * hidden;
+                GemvItem a, b, d;
+                if (int rc = make_gemv_item(xr, &gs[e], gout + (uint64_t)q * ffn, &a)) return rc;
+                if (int rc = make_gemv_item(xr, &us[e], uout + (uint64_t)q * ffn, &b)) return rc;
+                if (int rc = make_gemv_item(gout + (uint64_t)q * ffn, &ds[e], dout + (uint64_t)q * hidden, &d))
+                    return rc;
+                gu.push_back(a);
+                gu.push_back(b);
+                dn.push_back(d);
+            }
+        }
+        std::vector<uint8_t> host(g_total - g_ci, 0);
+        std::memcpy(host.data(), comb_idx.data(), comb_idx.size() * 4u);
+        std::memcpy(host.data() + (g_cw - g_ci), comb_w.data(), comb_w.size() * 4u);
+        if (int rc = stage_upload(c, B + g_ci, host.data(), host.size(), stream)) return rc;
+        if (int rc = gemv_launch_table(c, gu, 0, stream)) return rc;
+        if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
+        if (int rc = gemv_launch_table(c, dn, 0, stream)) return rc;
+        struct {
+            const float* po;
+            const int32_t* idx;
+            const float* w;
+            float* out;
+            uint32_t tokens, k, hidden, pad;
+        } a = {dout, reinterpret_cast<const int32_t*>(B + g_ci), reinterpret_cast<const float*>(B + g_cw), out,
+               rows, top_k, hidden, 0};
+        const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
+        if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
+        return ok();
+    }
+
     // workspace layout
     const uint64_t o_xq = 0;
     const uint64_t o_xds = o_xq + align256((uint64_t)rows * hidden);
@@ -1227,7 +1395,12 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     float* d_cw = reinterpret_cast<float*>(B + o_cw);
     MmqDesc* d_desc = reinterpret_cast<MmqDesc*>(B + o_desc);
 
-    // descriptor tables: [gate+up descs][down descs]
+    // descriptor tables: [gate+up descs][down descs]; experts averaging at
+    // most 48 routed rows take 64-row tiles
+    uint32_t used = 0;
+    for (uint32_t e = 0; e < expert_count; e++) used += off[e + 1] > off[e];
+    const bool m64 = used && P <= 48u * used;
+    const uint32_t bm = m64 ? 64u : kMmqBM;
     std::vector<MmqDesc> descs;
     uint32_t wg_gu = 0;
     auto add = [&](const rfxq_weight* w, uint32_t e, const int8_t* q, const uint32_t* s, const int32_t* rws,
@@ -1247,7 +1420,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         d.type = ew.ggml_type;
         d.ldq = ldq;
         d.ldy = n;
-        d.tiles_m = (m + kMmqBM - 1u) / kMmqBM;
+        d.tiles_m = (m + bm - 1u) / bm;
         d.tiles_n = (n + kMmqBN - 1u) / kMmqBN;
         d.splits = 1;
         d.sb_per_split = d.k / 256u;
@@ -1271,23 +1444,25 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     }
     const uint32_t n_dn = (uint32_t)descs.size() - n_gu;
 
-    // one upload of all tables (stream-ordered; the reference copies per expert)
+    // one upload of all tables (stream-ordered through pinned staging; the
+    // reference copies per expert)
     std::vector<uint8_t> host(total - o_tab, 0);
     std::memcpy(host.data() + (o_pr - o_tab), pair_row.data(), (size_t)P * 4u);
     std::memcpy(host.data() + (o_ci - o_tab), comb_idx.data(), comb_idx.size() * 4u);
     std::memcpy(host.data() + (o_cw - o_tab), comb_w.data(), comb_w.size() * 4u);
     std::memcpy(host.data() + (o_desc - o_tab), descs.data(), descs.size() * sizeof(MmqDesc));
-    HIPCHK(hipMemcpyAsync(B + o_tab, host.data(), host.size(), hipMemcpyHostToDevice, stream),
-           "moe_ffn_grouped table upload");
+    if (int rc = stage_upload(c, B + o_tab, host.data(), host.size(), stream)) return rc;
 
     if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
     if (n_gu) {
-        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream)) return rc;
+        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, false, m64))
+            return rc;
     }
     if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
     if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
     if (n_dn) {
-        if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream))
+        if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
+                                false, m64))
             return rc;
     }
     {
@@ -1301,8 +1476,6 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
         if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
     }
-    // The host staging vector dies with this frame: make sure the copy is done.
-    HIPCHK(hipStreamSynchronize(stream), "moe_ffn_grouped sync");
     return ok();
 }
 

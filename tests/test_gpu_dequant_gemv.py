@@ -179,3 +179,31 @@ def test_gemv_errors_raise(rq):
     w = _weight(rq, Q4K, synth.weights(Q4K, 8, 512, 3), 8, 512)
     with pytest.raises(rq.ReflexError):
         rq.gemv(torch.zeros(511, device=DEV), w)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("scale", [3e4, 1e6])
+def test_gemv_activations_beyond_f16_range(rq, orc, ty, scale):
+    """x is staged as f16: activations of 3e4..1e6 (MoE SiLU*up outputs reach
+    such values) are staged with an exact power-of-two scale that the row
+    results undo, so the error bound is the same as for N(0,1) inputs."""
+    n, k = 300, 2048
+    w_np = orc.synthetic(ty, k, n, 77)
+    x = synth.activations(k, 78) * np.float32(scale)
+    _check_gemv(rq, orc, ty, n, k, w_np, x)
+
+
+def test_gemv_batch_table_launch(rq, orc):
+    """More GEMVs than fit in the kernel arguments run as one launch over an
+    uploaded descriptor table, each equal to its single call bit for bit."""
+    items, singles = [], []
+    for i in range(9):
+        ty = [Q4K, Q6K, Q8_0][i % 3]
+        n, k = [(256, 512), (130, 1024), (64, 2048)][i % 3]
+        w = _weight(rq, ty, orc.synthetic(ty, k, n, 90 + i), n, k)
+        x = _dev(synth.activations(k, 100 + i))
+        singles.append(rq.gemv(x, w).cpu().numpy())
+        items.append((x, w, torch.full((n,), 7.0, device=DEV)))
+    rq.gemv_batch(items)
+    for (_, _, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)

@@ -292,3 +292,14 @@ def test_gemm_f16_plan_matches_single_gemms(rq, f16_mode):
         plan.run()
         for (_, _, y), ref in zip(items, singles):
             assert np.array_equal(y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("f16", ["1", "0"])
+def test_gemm_large_activations(rq, orc, monkeypatch, f16):
+    """Activations of ~3e3 (32-block sums near 1e5, beyond f16's range as
+    plain values): both Q4_K kernels stay within the model bound."""
+    monkeypatch.setenv("REFLEX_MMQ_F16", f16)
+    m, n, k = 64, 256, 1024
+    w_np = synth.weights(Q4K, n, k, 33)
+    x = synth.activations(m * k, 34).reshape(m, k) * np.float32(3000.0) + np.float32(2500.0)
+    _check_gemm(rq, orc, Q4K, m, n, k, w_np, x)

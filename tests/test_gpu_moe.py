@@ -90,3 +90,40 @@ def test_moe_ffn_grouped_deterministic(rq, orc):
     a, _, _ = _moe_case(rq, orc, 32, 16, 512, 256, 4, 300)
     b, _, _ = _moe_case(rq, orc, 32, 16, 512, 256, 4, 300)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("tokens", [1, 3])
+def test_moe_ffn_grouped_decode_gemv_path(rq, orc, tokens):
+    """Up to 4 tokens run every routed pair as GEMVs (activations rounded to f16
+    only, no int8 stage): within 1e-3 of the host reference at config 5 shapes."""
+    y, ref, routes = _moe_case(rq, orc, tokens, 128, 2048, 768, 8, 400 + tokens)
+    assert len(routes) == tokens
+    e = orc.rel_err_row_l2(y, ref)
+    print(f"decode MoE {tokens} tokens: row-L2 error {e:.2e}")
+    assert e < 1e-3
+
+
+def test_moe_ffn_grouped_back_to_back(rq, orc):
+    """Calls queue on the stream without host synchronisation (tables go
+    through a ring of pinned staging buffers): ten calls with different
+    routings, then one sync, each equal to the same call run alone."""
+    experts, hidden, ffn, top_k = 16, 512, 256, 4
+    gate = synth.weights(Q4K, experts * ffn, hidden, 11)
+    up = synth.weights(Q4K, experts * ffn, hidden, 12)
+    down = synth.weights(Q4K, experts * hidden, ffn, 13)
+    W = lambda a, i, o: rq.Weight(rq.GgmlType.Q4K, _dev(a), [i, o, experts])  # noqa: E731
+    wg, wu, wd = W(gate, hidden, ffn), W(up, hidden, ffn), W(down, ffn, hidden)
+    cases = []
+    for i in range(10):
+        tokens = [1, 2, 40, 3, 64][i % 5]
+        x = _dev(synth.activations(tokens * hidden, 50 + i))
+        logits = synth.normals(60 + i, tokens * experts).reshape(tokens, experts)
+        cases.append((tokens, x, logits, torch.empty(tokens * hidden, device=DEV)))
+    for tokens, x, logits, out in cases:
+        rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, top_k, True, 1.0, wg, wu, wd, out)
+    torch.cuda.synchronize()
+    for tokens, x, logits, out in cases:
+        alone = torch.empty_like(out)
+        rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, top_k, True, 1.0, wg, wu, wd, alone)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), alone.cpu().numpy())
