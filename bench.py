@@ -37,8 +37,8 @@ def log(*a):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="skip prefill, 8B and CPU legs")
     ap.add_argument("--no-cpu", action="store_true")
@@ -130,7 +130,7 @@ def main() -> int:
             rq.gemv_batch([(xs[layer[p][3]], ws[(li, p)], ys[(li, p)]) for p in (4, 5)])
             rq.gemv_to(xs[layer[6][3]], ws[(li, 6)], ys[(li, 6)])
 
-    ms_l = timed(layered, max(5, args.steps // 5), 2)
+    ms_l = timed(layered, 10, 2)
     gbs_l = step_bytes / (ms_l * 1e-3) / 1e9
     log(f"decode GEMV set (112 dependent launches): {ms_l * 1e3:.1f} us/step  {gbs_l:.0f} GB/s")
 
@@ -171,6 +171,7 @@ def main() -> int:
 
     if not args.quick:
         result["prefill"] = prefill_leg(rq, synth, torch, np, dev, timed)
+        result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
     del plans, copies
     torch.cuda.empty_cache()
     if not args.quick and not args.no_cpu:
@@ -216,6 +217,40 @@ def traffic_summary(fetch_csv: str, write_csv: str) -> int:
         json.dump(out, fh, indent=1)
     print(json.dumps(out))
     return 0
+
+
+def moe_leg(rq, synth, torch, np, dev, timed):
+    """Qwen3-MoE-style grouped expert FFN (config 5): 128 experts, hidden 2048,
+    FFN 768, Q4_K gate/up/down, routed top-8 (softmax, renormalised) by seeded
+    N(0,1) logits. Prefill: 512 tokens (4096 routed pairs); decode: 1 token.
+    A step is one moe_ffn_grouped call (host routing from host logits, one
+    table upload, quantize / grouped GEMMs / SiLU*up / combine launches, no
+    host synchronisation). HBM-bound: GB/s counts the weight bytes of the
+    experts the step routes to."""
+    cfg = synth.MOE
+    E, H, F, K = cfg["experts"], cfg["hidden"], cfg["ffn"], cfg["top_k"]
+    W = lambda p, i, o: rq.Weight.from_blocks(cfg["ty"], synth.weights(cfg["ty"], E * o, i, synth.seed_for(5, 0, p)),  # noqa: E731
+                                              i, o, expert_count=E, device=dev)
+    gate, up, down = W(0, H, F), W(1, H, F), W(2, F, H)
+    per_expert = 3 * F * H * 144 // 256
+    out = {}
+    for tag, tokens in (("prefill_512", cfg["tokens"]), ("decode_1", 1)):
+        x = torch.from_numpy(synth.activations(tokens * H, synth.seed_for(5, 0, 3))).to(dev)
+        logits = synth.normals(synth.seed_for(5, 0, 4), tokens * E).reshape(tokens, E)
+        y = torch.empty(tokens * H, device=dev)
+        used = len({e for t in range(tokens) for e, _ in rq.route_top_k(logits[t], K)})
+        steps = 20 if tokens > 1 else 100
+        ms = timed(lambda i: rq.moe_ffn_grouped(x, tokens, H, logits, E, K, True, 1.0, gate, up, down, y), steps, 3)
+        wbytes = used * per_expert
+        ops = tokens * K * 2 * 3 * F * H
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        out[tag] = {"ms_per_step": round(ms, 4), "experts_used": used, "weight_mb": round(wbytes / 1e6, 1),
+                    "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                    "tops": round(ops / (ms * 1e-3) / 1e12, 2)}
+        print(f"moe {tag}: {ms * 1e3:.1f} us/step  {gbs:.0f} GB/s of routed expert weights "
+              f"({gbs / HBM_PEAK_GBS:.1%} of HBM), {used} experts", file=sys.stderr, flush=True)
+    del gate, up, down
+    return out
 
 
 def prefill_leg(rq, synth, torch, np, dev, timed):

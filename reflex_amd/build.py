@@ -65,7 +65,7 @@ def build(verbose: bool = False) -> str:
     _run(["gcc", "-c", embed_s, "-o", embed_o], verbose)
     tmp = LIB + ".tmp"
     _run([
-        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall", "-Wextra", "-Wno-unused-parameter",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
         os.path.join(CSRC, "rfxq.cpp"), embed_o,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp,

@@ -1283,16 +1283,27 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
 
-    // host routing and grouping (dense.rs:1523-1530)
-    std::vector<std::vector<std::pair<uint32_t, float>>> groups(expert_count);
-    std::vector<uint32_t> idx(top_k);
-    std::vector<float> wts(top_k);
-    for (uint32_t r = 0; r < rows; r++) {
-        if (int rc = route_top_k(router_logits_host + (uint64_t)r * expert_count, expert_count, top_k,
-                                 normalize != 0, idx.data(), wts.data()))
-            return rc;
-        for (uint32_t t = 0; t < top_k; t++) groups[idx[t]].push_back({r, wts[t] * weight_scale});
+    // host routing (dense.rs:1523-1530), tokens in parallel (each routes
+    // alone; a failing token is routed again on this thread for the message)
+    std::vector<uint32_t> ridx((uint64_t)rows * top_k);
+    std::vector<float> rwts((uint64_t)rows * top_k);
+    int64_t bad = -1;
+#pragma omp parallel for schedule(static) if (rows >= 64)
+    for (int64_t r = 0; r < (int64_t)rows; r++) {
+        if (route_top_k(router_logits_host + (uint64_t)r * expert_count, expert_count, top_k, normalize != 0,
+                        ridx.data() + (uint64_t)r * top_k, rwts.data() + (uint64_t)r * top_k) != RFXQ_OK) {
+#pragma omp critical
+            if (bad < 0 || r < bad) bad = r;
+        }
     }
+    if (bad >= 0)
+        return route_top_k(router_logits_host + (uint64_t)bad * expert_count, expert_count, top_k, normalize != 0,
+                           ridx.data() + (uint64_t)bad * top_k, rwts.data() + (uint64_t)bad * top_k);
+    // grouping by expert, tokens in order
+    std::vector<std::vector<std::pair<uint32_t, float>>> groups(expert_count);
+    for (uint32_t r = 0; r < rows; r++)
+        for (uint32_t t = 0; t < top_k; t++)
+            groups[ridx[(uint64_t)r * top_k + t]].push_back({r, rwts[(uint64_t)r * top_k + t] * weight_scale});
     const uint32_t P = rows * top_k;
     std::vector<int32_t> pair_row(P), comb_idx((uint64_t)rows * top_k, -1);
     std::vector<float> comb_w((uint64_t)rows * top_k, 0.0f);
