@@ -44,6 +44,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only replay the fused GEMV plan and a calibration copy (for rocprofv3 --pmc runs)")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run the 8B gate GEMM (14336x4096 Q4_K, M=512) 5 times (for rocprofv3 --pmc runs)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, WRITE_SIZE) of a "
                          "--traffic-probe run into profiles/gemv_decode06b_traffic.json")
@@ -65,6 +67,17 @@ def main() -> int:
     torch.cuda.set_device(0)
     rq.init(0)
     stream = torch.cuda.current_stream()
+
+    if args.prefill_probe:
+        name, ty, n, k = synth.QWEN3_8B_LAYER[4]
+        w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(4, 0, 4)), k, n, device=dev)
+        x = torch.from_numpy(synth.activations(512 * k, synth.seed_for(4, 0, 99))).to(dev)
+        y = torch.empty(512 * n, device=dev)
+        ws = torch.empty(rq.gemm_workspace_size(w, 512), dtype=torch.uint8, device=dev)
+        for _ in range(5):
+            rq.gemm(x, w, 512, workspace=ws, out=y)
+        torch.cuda.synchronize()
+        return 0
 
     # ------------------------------------------------------------ data (config 2)
     t0 = time.time()

@@ -677,6 +677,7 @@ struct GemmGroup {
         const float* x;
         uint32_t k;
         uint64_t off_xq, off_xds, off_xh, off_xsc;  // off_xh, off_xsc: f16 mode
+        bool need_i8 = false, need_h = false;      // layouts its GEMMs read
     };
     bool f16 = false;
     std::vector<Act> acts;
@@ -701,7 +702,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
-            GemmGroup::Act act{it.x, k, 0, 0, 0, 0};
+            GemmGroup::Act act{it.x, k, 0, 0, 0, 0, false, false};
             act.off_xq = g->ws_bytes;
             act.off_xds = act.off_xq + align256((uint64_t)rows * k);
             act.off_xh = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
@@ -711,6 +712,8 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
         }
+        if (g->f16 && it.w->ggml_type == RFXQ_TYPE_Q4_K) g->acts[ai].need_h = true;
+        else g->acts[ai].need_i8 = true;
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         const bool f16 = g->f16 && it.w->ggml_type == RFXQ_TYPE_Q4_K;
@@ -748,10 +751,11 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
 
 int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
     for (const auto& a : g.acts)
-        if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k, reinterpret_cast<int8_t*>(ws + a.off_xq),
-                                  reinterpret_cast<uint32_t*>(ws + a.off_xds), stream,
-                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr,
-                                  g.f16 ? reinterpret_cast<uint16_t*>(ws + a.off_xsc) : nullptr))
+        if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k,
+                                  a.need_i8 ? reinterpret_cast<int8_t*>(ws + a.off_xq) : nullptr,
+                                  a.need_i8 ? reinterpret_cast<uint32_t*>(ws + a.off_xds) : nullptr, stream,
+                                  a.need_h ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr,
+                                  a.need_h ? reinterpret_cast<uint16_t*>(ws + a.off_xsc) : nullptr))
             return rc;
     return RFXQ_OK;
 }
@@ -1102,10 +1106,10 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
         std::vector<QuantDesc> q;
         for (const auto& a : plan->g.acts) {
             const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
-            q.push_back(QuantDesc{a.x, reinterpret_cast<int8_t*>(base + a.off_xq),
-                                  reinterpret_cast<uint32_t*>(base + a.off_xds),
-                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr,
-                                  plan->g.f16 ? reinterpret_cast<uint16_t*>(base + a.off_xsc) : nullptr, rows, a.k,
+            q.push_back(QuantDesc{a.x, a.need_i8 ? reinterpret_cast<int8_t*>(base + a.off_xq) : nullptr,
+                                  a.need_i8 ? reinterpret_cast<uint32_t*>(base + a.off_xds) : nullptr,
+                                  a.need_h ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr,
+                                  a.need_h ? reinterpret_cast<uint16_t*>(base + a.off_xsc) : nullptr, rows, a.k,
                                   plan->qgrid, wgs});
             plan->qgrid += wgs;
         }
