@@ -298,7 +298,7 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
         ms = timed(lambda i: plan.run(), steps, 2)
         tops = ops / (ms * 1e-3) / 1e12
         out[tag] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                    "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1), "dtype": "f16-exact int8 dots (Q4_K), int8 (Q6_K)" if os.environ.get("REFLEX_MMQ_F16", "1") != "0" else "int8",
+                    "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1), "dtype": "f16-exact int8 dots (Q4_K, Q6_K)" if os.environ.get("REFLEX_MMQ_F16", "1") != "0" else "int8",
                     "gemms_per_step": len(items)}
         print(f"prefill {tag}: {ms:.3f} ms/step  {tops:.0f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)",
               file=sys.stderr, flush=True)

@@ -19,10 +19,12 @@
 
 // Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
 // wave_global); 8 lanes per 32-block.
-// Optional layouts for the f16-MFMA Q4_K kernel (mmq2.hpp):
+// Optional layouts for the f16-MFMA kernels (mmq2.hpp):
 //   xh  [rows][k] f16: the int8 values, each group of four stored (q0, q2), (q1, q3)
-//   xsc [rows][k/256][24] u16: per super-block d[8], then Sx' = d*s*2^-6
-//       split exactly into f16 hi[8] and lo[8] (hi = f16(Sx'), lo = f16(Sx' - hi))
+//   xsc [rows][k/256][32] u16: per super-block d[8], then Sx' = d*s*2^-6
+//       split exactly into f16 hi[8] and lo[8] (hi = f16(Sx'), lo = f16(Sx' - hi)),
+//       then d again in the order 0, 2, 1, 3, 4, 6, 5, 7 (dword j of that
+//       copy holds the scales of the two blocks one Q6_K 64-k stage reads)
 RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
                               uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
                               uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint16_t* __restrict__ xsc,
@@ -73,10 +75,12 @@ RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const i
                     const float sx = f16_bits_to_f32(dbits) * f16_bits_to_f32(sbits) * 0.015625f;
                     const half_t hi = (half_t)sx;
                     const half_t lo = (half_t)(sx - (float)hi);
-                    uint16_t* rec = xsc + ((uint64_t)row * (nblk / 8u) + blk / 8u) * 24u + (blk & 7u);
-                    rec[0] = (uint16_t)dbits;
-                    rec[8] = __builtin_bit_cast(uint16_t, hi);
-                    rec[16] = __builtin_bit_cast(uint16_t, lo);
+                    const uint32_t b8 = blk & 7u;
+                    uint16_t* rec = xsc + ((uint64_t)row * (nblk / 8u) + blk / 8u) * 32u;
+                    rec[b8] = (uint16_t)dbits;
+                    rec[8u + b8] = __builtin_bit_cast(uint16_t, hi);
+                    rec[16u + b8] = __builtin_bit_cast(uint16_t, lo);
+                    rec[24u + ((b8 & 4u) | ((b8 & 1u) << 1) | ((b8 >> 1) & 1u))] = (uint16_t)dbits;
                 }
             }
         }

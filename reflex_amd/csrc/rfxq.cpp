@@ -112,7 +112,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmq2_q4k = nullptr;
+    hipFunction_t mmq2_q4k = nullptr, mmq2_q6k = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     void* ws = nullptr;
@@ -172,6 +172,7 @@ int load_ctx(int device, Ctx** out) {
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
         {&c->mmq2_q4k, "rfxq_mmq2_q4k"},
+        {&c->mmq2_q6k, "rfxq_mmq2_q6k"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
         {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
         {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
@@ -524,24 +525,31 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 // ------------------------------------------------------------------ MMQ planning
 
 
-// Q4_K prefill GEMMs run on the f16-MFMA kernel (rfxq_mmq2_q4k: exact integer
-// block dots, one FMA per element and block) unless REFLEX_MMQ_F16=0 selects
-// the int8-MFMA kernel. Gathered rows (MoE) always take the int8 kernel.
-constexpr uint32_t kMmq2Threads = 256;  // rfxq_mmq2_q4k workgroup
+// Q4_K and Q6_K prefill GEMMs run on the f16-MFMA kernels (rfxq_mmq2_q4k,
+// rfxq_mmq2_q6k: exact integer block dots, one FMA per element and block)
+// unless REFLEX_MMQ_F16=0 selects the int8-MFMA kernels. Gathered rows (MoE)
+// always take the int8 kernels.
+constexpr uint32_t kMmq2Threads = 256;  // rfxq_mmq2_* workgroup
 bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 1) != 0; }
 
-// rfxq_mmq2_q4k for this GEMM: f16 mode, Q4_K, and every buffer offset of the
-// kernel's copies (rows and columns rounded up to the 128 tile) fits in 32 bits
+// an f16 kernel for this GEMM: f16 mode, Q4_K or Q6_K (the Q6_K kernel needs
+// an even number of super-blocks per row, so that rows start 4-byte
+// aligned), and every buffer offset of the kernel's copies (rows and columns
+// rounded up to the 128 tile) fits in 32 bits
 bool use_mmq2(const rfxq_weight* w, uint32_t rows) {
-    if (!mmq_f16() || w->ggml_type != RFXQ_TYPE_Q4_K) return false;
+    if (!mmq_f16()) return false;
+    const uint64_t k = w->in_features, n = w->out_features, nsb = k / 256u;
+    uint64_t bb;
+    if (w->ggml_type == RFXQ_TYPE_Q4_K) bb = 144u;
+    else if (w->ggml_type == RFXQ_TYPE_Q6_K && nsb % 2u == 0u) bb = 210u;
+    else return false;
     const uint64_t lim = 0xF0000000ull;
-    const uint64_t k = w->in_features, n = w->out_features;
-    return (n + 128u) * (k / 256u) * 144u < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
+    return (n + 128u) * nsb * bb < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
 }
 
 // bytes of the f16 activation copy and of the super-block scale records
 uint64_t xh_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * k * 2u); }
-uint64_t xsc_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * (k / 256u) * 48u); }
+uint64_t xsc_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * (k / 256u) * 64u); }
 
 struct GemmPlan {
     uint32_t splits, sb_per_split, tiles_m, tiles_n;
@@ -592,8 +600,8 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
                   "rfxq_quantize_q8_1 launch");
 }
 
-// f16: Q4_K descriptors carry the f16 activations (xq, ldq = 2k bytes) and
-// the scale records (xds) and run on rfxq_mmq2_q4k
+// f16: Q4_K / Q6_K descriptors carry the f16 activations (xq, ldq = 2k
+// bytes) and the scale records (xds) and run on rfxq_mmq2_q4k / _q6k
 // m64: the descriptors are tiled by 64 rows (rfxq_mmq_*_m64)
 int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
                bool dots, hipStream_t stream, bool f16 = false, bool m64 = false) {
@@ -603,8 +611,9 @@ int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDes
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && ty == RFXQ_TYPE_Q4_K && !dots && !m64)
-        return launch(c->mmq2_q4k, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq2 launch", kMmq2Threads);
+    if (f16 && !dots && !m64 && ty != RFXQ_TYPE_Q8_0)
+        return launch(ty == RFXQ_TYPE_Q4_K ? c->mmq2_q4k : c->mmq2_q6k, total_wgs, 0, stream, &a, sizeof a,
+                      "rfxq_mmq2 launch", kMmq2Threads);
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
 }
 
@@ -679,7 +688,7 @@ struct GemmGroup {
         uint64_t off_xq, off_xds, off_xh, off_xsc;  // off_xh, off_xsc: f16 mode
         bool need_i8 = false, need_h = false;      // layouts its GEMMs read
     };
-    bool f16 = false;
+    bool f16[3] = {false, false, false};  // per type_index: the f16 kernel
     std::vector<Act> acts;
     std::vector<MmqDesc> descs[3];  // per type_index
     uint32_t wgs[3] = {0, 0, 0};
@@ -688,10 +697,12 @@ struct GemmGroup {
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
-    // f16 kernel for the group's Q4_K GEMMs only if every one of them can take it
-    g->f16 = mmq_f16();
+    // the f16 kernel for the group's GEMMs of one type only if every one of them can take it
+    g->f16[0] = g->f16[1] = mmq_f16();
     for (uint32_t i = 0; i < count; i++)
-        if (items[i].w && items[i].w->ggml_type == RFXQ_TYPE_Q4_K && !use_mmq2(items[i].w, rows)) g->f16 = false;
+        if (items[i].w && items[i].w->ggml_type != RFXQ_TYPE_Q8_0 && !use_mmq2(items[i].w, rows))
+            g->f16[type_index(items[i].w->ggml_type)] = false;
+    const bool any_f16 = g->f16[0] || g->f16[1];
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
@@ -706,17 +717,17 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             act.off_xq = g->ws_bytes;
             act.off_xds = act.off_xq + align256((uint64_t)rows * k);
             act.off_xh = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
-            act.off_xsc = act.off_xh + (g->f16 ? xh_bytes(rows, k) : 0u);
-            g->ws_bytes = act.off_xsc + (g->f16 ? xsc_bytes(rows, k) : 0u);
+            act.off_xsc = act.off_xh + (any_f16 ? xh_bytes(rows, k) : 0u);
+            g->ws_bytes = act.off_xsc + (any_f16 ? xsc_bytes(rows, k) : 0u);
             g->acts.push_back(act);
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
         }
-        if (g->f16 && it.w->ggml_type == RFXQ_TYPE_Q4_K) g->acts[ai].need_h = true;
+        const bool f16 = g->f16[type_index(it.w->ggml_type)];
+        if (f16) g->acts[ai].need_h = true;
         else g->acts[ai].need_i8 = true;
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
-        const bool f16 = g->f16 && it.w->ggml_type == RFXQ_TYPE_Q4_K;
         d.w = it.w->data;
         // offsets until the workspace is known
         d.xq = reinterpret_cast<const int8_t*>(f16 ? g->acts[ai].off_xh : g->acts[ai].off_xq);
@@ -1063,7 +1074,7 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16)) return rc;
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16[t])) return rc;
         }
     }
     return ok();
@@ -1145,7 +1156,7 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
         const uint32_t n = (uint32_t)v.size();
         if (n <= kMmqInline) std::copy(v.begin(), v.end(), tmp);
         if (int rc = launch_mmq(c, v[0].type, tmp, n, n <= kMmqInline ? nullptr : plan->table[t], plan->g.wgs[t],
-                                false, stream, plan->g.f16))
+                                false, stream, plan->g.f16[t]))
             return rc;
     }
     return ok();

@@ -228,37 +228,41 @@ def test_gemm_batch_errors(rq):
         rq.gemm_batch([(x, w1, y), (x, w2, y)], 64)   # one x with two in_features
 
 
-# ------------------------------------------------------------------ f16-MFMA Q4_K kernel
+# ------------------------------------------------------------------ f16-MFMA kernels
 
 @pytest.fixture
 def f16_mode(monkeypatch):
-    """Q4_K GEMMs on rfxq_mmq2_q4k (REFLEX_MMQ_F16=1)."""
+    """Q4_K / Q6_K GEMMs on rfxq_mmq2_q4k / rfxq_mmq2_q6k (REFLEX_MMQ_F16=1)."""
     monkeypatch.setenv("REFLEX_MMQ_F16", "1")
     yield
 
 
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
 @pytest.mark.parametrize("m,n,k", [(2, 200, 1024), (33, 200, 256), (129, 1000, 2048), (512, 1024, 1024),
-                                   (513, 3072, 1024), (300, 136, 4096)])
-def test_gemm_f16_kernel(rq, orc, monkeypatch, m, n, k):
+                                   (513, 3072, 1024), (300, 136, 4096), (64, 130, 768)])
+def test_gemm_f16_kernel(rq, orc, monkeypatch, ty, m, n, k):
     """Same block dots as the int8 kernel (exact), other f32 rounding: the two
-    kernels agree to f32 accumulation noise and both meet the model bound."""
-    w_np = synth.weights(Q4K, n, k, 90 + m)
+    kernels agree to f32 accumulation noise and both meet the model bound.
+    (Q6_K rows with an odd super-block count, k = 256 and 768, stay on the
+    int8 kernel.)"""
+    w_np = synth.weights(ty, n, k, 90 + m)
     x = synth.activations(m * k, 91 + m).reshape(m, k)
-    w = _weight(rq, Q4K, w_np, n, k)
+    w = _weight(rq, ty, w_np, n, k)
     monkeypatch.setenv("REFLEX_MMQ_F16", "0")
     y8 = rq.gemm(_dev(x), w, m).cpu().numpy().reshape(m, n)
     monkeypatch.setenv("REFLEX_MMQ_F16", "1")
-    yh, _ = _check_gemm(rq, orc, Q4K, m, n, k, w_np, x)
+    yh, _ = _check_gemm(rq, orc, ty, m, n, k, w_np, x)
     d = orc.rel_err_row_l2(yh, y8.astype(np.float64))
     print(f"f16 vs int8 kernel: {d:.2e}")
     assert d < 1e-5
 
 
-def test_gemm_f16_kernel_split_k_and_repeat(rq, orc, f16_mode, monkeypatch):
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
+def test_gemm_f16_kernel_split_k_and_repeat(rq, orc, f16_mode, monkeypatch, ty):
     n, k, m = 512, 4096, 64
-    w_np = synth.weights(Q4K, n, k, 7)
+    w_np = synth.weights(ty, n, k, 7)
     x = _dev(synth.activations(m * k, 8))
-    w = _weight(rq, Q4K, w_np, n, k)
+    w = _weight(rq, ty, w_np, n, k)
     ys = []
     for s in ("1", "4", "16"):
         monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", s)
@@ -294,12 +298,34 @@ def test_gemm_f16_plan_matches_single_gemms(rq, f16_mode):
             assert np.array_equal(y.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
 @pytest.mark.parametrize("f16", ["1", "0"])
-def test_gemm_large_activations(rq, orc, monkeypatch, f16):
+def test_gemm_large_activations(rq, orc, monkeypatch, f16, ty):
     """Activations of ~3e3 (32-block sums near 1e5, beyond f16's range as
-    plain values): both Q4_K kernels stay within the model bound."""
+    plain values): the f16 and int8 kernels stay within the model bound."""
     monkeypatch.setenv("REFLEX_MMQ_F16", f16)
     m, n, k = 64, 256, 1024
-    w_np = synth.weights(Q4K, n, k, 33)
+    w_np = synth.weights(ty, n, k, 33)
     x = synth.activations(m * k, 34).reshape(m, k) * np.float32(3000.0) + np.float32(2500.0)
-    _check_gemm(rq, orc, Q4K, m, n, k, w_np, x)
+    _check_gemm(rq, orc, ty, m, n, k, w_np, x)
+
+
+def test_gemm_q6k_f16_extreme_codes(rq, orc, f16_mode, monkeypatch):
+    """Q6_K blocks at the limits of the f16 operand split: scales -128 and
+    127 with codes 0 and 63 (|sc*(q - 32)| = 4096 and 3937), so every block
+    dot sits near 2^24; full-scale activations. The f16 kernel's dots are
+    exact, so it agrees with the int8 kernel to f32 rounding."""
+    m, n, k = 96, 256, 1024
+    rng = np.random.default_rng(5)
+    nb = n * k // 256
+    blk = np.zeros((nb, 210), np.uint8)
+    blk[:, 0:192] = rng.choice(np.array([0x00, 0xFF], np.uint8), size=(nb, 192))
+    blk[:, 192:208] = rng.choice(np.array([0x80, 0x7F], np.uint8), size=(nb, 16))
+    blk[:, 208:210] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+    w_np = blk.reshape(-1)
+    x = np.where(rng.random((m, k)) < 0.5, np.float32(-1.0), np.float32(1.0)).astype(np.float32)
+    w = _weight(rq, Q6K, w_np, n, k)
+    yh, _ = _check_gemm(rq, orc, Q6K, m, n, k, w_np, x)
+    monkeypatch.setenv("REFLEX_MMQ_F16", "0")
+    y8 = rq.gemm(_dev(x), w, m).cpu().numpy().reshape(m, n)
+    assert orc.rel_err_row_l2(yh, y8.astype(np.float64)) < 1e-5
