@@ -125,6 +125,13 @@ RFXQ_DEV void dma16(rsrc_t r, void* lds_base, uint32_t off) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RFXQ_LDSP(lds_base), 16, off, 0, 0, 0);
 }
 
+// the same copy marked non-temporal (cache policy nt): for data read once,
+// such as decode weights streamed from HBM
+RFXQ_DEV void dma16_stream(rsrc_t r, void* lds_base, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RFXQ_LDSP(lds_base), 16, off, 0, 0, 2);
+}
+
+
 RFXQ_DEV uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t shift_bytes) {
     return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }

@@ -100,6 +100,10 @@ RFXQ_DEV void gemv_x_sums(const uint32_t* lds_x, float* lds_s, uint32_t k, uint3
 // lds_p (the row results, free while staging) carries the waves' maxima.
 RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
                             uint32_t* lds_x, float* lds_s, float* lds_p, uint32_t tid) {
+#ifdef RFXQ_NOSTAGE
+    lds_barrier();
+    return 1.0f;
+#endif
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -518,7 +522,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             if (!T::ALIGNED) g &= ~3u;
             g += pc[j];
 #ifndef RFXQ_NOLOAD
-            dma16(wr, ring[t] + 1024 * j, valid && pv[j] ? g : kPastEnd);
+            dma16_stream(wr, ring[t] + 1024 * j, valid && pv[j] ? g : kPastEnd);
 #else
             asm volatile("" ::"v"(g));
 #endif

@@ -100,7 +100,7 @@ static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
 
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
-constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 48 KB weight ring)
+constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 32 KB weight ring)
 constexpr uint32_t kMaxGemvK = 16384;
 constexpr uint32_t kMoeGemvRows = 4;  // moe_ffn_grouped: up to this many tokens run as GEMVs  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 
