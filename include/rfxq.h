@@ -99,6 +99,16 @@ int rfxq_gemv_to(const float* x, uint64_t x_len, const rfxq_weight* w, float* y,
 int rfxq_gemv_rows(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y,
                    hipStream_t stream);
 
+/* Model::gemv_gather (src/model/kernels.rs:2816-2851): y[j] = (W . x)[row_indices[j]]
+ * for j < count, computing only the named rows of W (the System1 candidate
+ * LM-head scoring; the reference runs the full-vocab GEMV for a quantized
+ * weight and picks rows on the host). row_indices is host memory; y is
+ * device memory (count floats); the results equal the full GEMV's at those
+ * rows bit for bit. Empty or out-of-range indices fail with the reference's
+ * messages. */
+int rfxq_gemv_gather(const float* x, uint64_t x_len, const rfxq_weight* w, const uint32_t* row_indices,
+                     uint32_t count, float* y, hipStream_t stream);
+
 /* Fused GEMVs of independent weights in one launch (Model::gemv_qkv_to /
  * gemv_gate_up_to, kernels.rs:1761-1823, generalised to any count and mix of
  * Q4_K / Q6_K / Q8_0). */

@@ -45,6 +45,7 @@ SIGNATURES = {
     "rfxq_dequantize": (_I, [_U32, _P, _U64, _P, _I, _P]),
     "rfxq_gemv_to": (_I, [_P, _U64, _WP, _P, _P]),
     "rfxq_gemv_rows": (_I, [_P, _U64, _WP, _U32, _P, _P]),
+    "rfxq_gemv_gather": (_I, [_P, _U64, _WP, _P, _U32, _P, _P]),
     "rfxq_gemv_batch": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _P]),
     "rfxq_gemv_plan_create": (_I, [ctypes.POINTER(RfxqGemvItem), _U32, _I, ctypes.POINTER(_P)]),
     "rfxq_gemv_plan_run": (_I, [_P, _P]),

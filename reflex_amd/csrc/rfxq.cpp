@@ -930,6 +930,39 @@ int rfxq_gemv_rows(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_
     return ok();
 }
 
+int rfxq_gemv_gather(const float* x, uint64_t x_len, const rfxq_weight* w, const uint32_t* row_indices,
+                     uint32_t count, float* y, hipStream_t stream) {
+    if (int rc = check_weight(w, "gemv_gather")) return rc;
+    if (x_len != w->in_features)
+        return fail(RFXQ_ERR_OTHER, "gemv_gather: x.len()=%llu != in_features=%u", (unsigned long long)x_len,
+                    w->in_features);
+    if (count == 0 || !row_indices) return fail(RFXQ_ERR_OTHER, "gemv_gather: row_indices must not be empty");
+    for (uint32_t j = 0; j < count; j++)
+        if (row_indices[j] >= w->out_features)
+            return fail(RFXQ_ERR_OTHER, "gemv_gather: row index %u out of range (out_features=%u)", row_indices[j],
+                        w->out_features);
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    // each run of consecutive indices is one GEMV over that row slice of W
+    // (rows are whole blocks, so a slice keeps the format's alignment)
+    const uint64_t rb = row_bytes(w->ggml_type, w->in_features);
+    std::vector<GemvItem> v;
+    for (uint32_t i = 0; i < count;) {
+        uint32_t j = i + 1u;
+        while (j < count && row_indices[j] == row_indices[j - 1u] + 1u) j++;
+        rfxq_weight slice = *w;
+        slice.out_features = j - i;
+        slice.data = static_cast<const uint8_t*>(w->data) + (uint64_t)row_indices[i] * rb;
+        slice.len = (uint64_t)(j - i) * rb;
+        GemvItem it;
+        if (int rc = make_gemv_item(x, &slice, y + i, &it)) return rc;
+        v.push_back(it);
+        i = j;
+    }
+    int rc = v.size() <= kGemvInline ? gemv_launch_inline(c, v, stream) : gemv_launch_table(c, v, 0, stream);
+    return rc ? rc : ok();
+}
+
 int rfxq_gemv_batch(const rfxq_gemv_item* items, uint32_t count, hipStream_t stream) {
     if (count == 0) return ok();
     if (!items) return fail(RFXQ_ERR_INVALID_INPUT, "gemv_batch: items is NULL");

@@ -21,6 +21,7 @@ __all__ = [
     "ReflexError", "GgmlError", "GpuError", "OutOfMemoryError", "InvalidInputError",
     "GgmlType", "ggml_type_block_dims", "Weight", "QuantArena",
     "dequantize", "gemv", "gemv_to", "gemv_q4k", "gemv_q6k", "gemv_q8_0", "gemv_batch", "GemvPlan",
+    "gemv_gather",
     "gemm", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
     "route_top_k", "route_top_k_with_norm", "quant_expert_weight", "expert_gemv", "expert_gemm",
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
@@ -217,6 +218,17 @@ def gemv_q6k(x: torch.Tensor, w: Weight) -> torch.Tensor:
 def gemv_q8_0(x: torch.Tensor, w: Weight, rows: int) -> torch.Tensor:
     """``Model::gemv_q8_0`` (kernels.rs:1874)."""
     return _gemv_rows(x, w, rows)
+
+
+def gemv_gather(x: torch.Tensor, w: Weight, row_indices) -> torch.Tensor:
+    """``Model::gemv_gather`` (kernels.rs:2816-2851): the logits of the named
+    rows only, as a device tensor (the reference returns host floats)."""
+    idx = (ctypes.c_uint32 * len(row_indices))(*[int(r) for r in row_indices])
+    y = torch.empty(max(len(row_indices), 1), dtype=torch.float32, device=x.device)
+    with _dev(x):
+        _check(lib().rfxq_gemv_gather(x.data_ptr(), x.numel(), w.cref(), idx, len(row_indices), y.data_ptr(),
+                                      _stream()))
+    return y[:len(row_indices)]
 
 
 def _items(items):

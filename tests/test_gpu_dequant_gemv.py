@@ -207,3 +207,34 @@ def test_gemv_batch_table_launch(rq, orc):
     rq.gemv_batch(items)
     for (_, _, y), ref in zip(items, singles):
         assert np.array_equal(y.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------------ gathered rows
+
+@pytest.mark.parametrize("ty,n,k", [(Q6K, 151936, 1024), (Q4K, 3072, 1024), (Q8_0, 1024, 1024)])
+def test_gemv_gather_matches_full_gemv(rq, ty, n, k):
+    """Model::gemv_gather (system1_tests.rs:16-84 pattern): gathered logits
+    equal the full GEMV's at the same rows, bit for bit; first, middle and
+    last rows, the argmax, duplicates, and runs of consecutive rows (one
+    GEMV per run)."""
+    w = _weight(rq, ty, synth.weights(ty, n, k, 44), n, k)
+    x = _dev(synth.activations(k, 45))
+    full = rq.gemv(x, w).cpu().numpy()
+    am = int(np.argmax(full))
+    rows = [0, n // 2, n - 1, am, am, 5, 6, 7, 8, 3, n - 2, n - 1]
+    got = rq.gemv_gather(x, w, rows).cpu().numpy()
+    assert np.array_equal(got, full[rows])
+    many = np.random.default_rng(46).integers(0, n, 300).tolist()  # table launch
+    assert np.array_equal(rq.gemv_gather(x, w, many).cpu().numpy(), full[many])
+
+
+def test_gemv_gather_errors(rq):
+    n, k = 256, 512
+    w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 47), n, k)
+    x = _dev(synth.activations(k, 48))
+    with pytest.raises(rq.ReflexError, match="row_indices must not be empty"):
+        rq.gemv_gather(x, w, [])
+    with pytest.raises(rq.ReflexError, match=r"row index 256 out of range \(out_features=256\)"):
+        rq.gemv_gather(x, w, [3, 256])
+    with pytest.raises(rq.ReflexError, match="x.len"):
+        rq.gemv_gather(x[:256], w, [1])
