@@ -17,6 +17,7 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -326,6 +327,33 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
         print(f"prefill {tag}: {ms:.3f} ms/step  {tops:.0f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)",
               file=sys.stderr, flush=True)
         del plan, items, keep
+    # fused activation producers at the 8B shapes (rmsnorm before q/k/v and
+    # gate/up, SiLU·up before down): one launch writes the quantized layouts
+    rows, hid, ffn = 512, 4096, 14336
+    x = torch.randn(rows * hid, device=dev, generator=gen)
+    g = torch.ones(hid, device=dev)
+    gate = torch.randn(rows * ffn, device=dev, generator=gen)
+    up = torch.randn(rows * ffn, device=dev, generator=gen)
+    act_h = torch.empty(rq.act_q8_1_size(rows, hid), dtype=torch.uint8, device=dev)
+    act_f = torch.empty(rq.act_q8_1_size(rows, ffn), dtype=torch.uint8, device=dev)
+    lib, st = rq.lib(), lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ms_rms = timed(lambda i: lib.rfxq_rmsnorm_q8_1(x.data_ptr(), g.data_ptr(), rows, hid, 1e-6,
+                                                    act_h.data_ptr(), None, st()), 50, 5)
+    ms_silu = timed(lambda i: lib.rfxq_silu_and_mul_q8_1(gate.data_ptr(), up.data_ptr(), rows, ffn,
+                                                         act_f.data_ptr(), None, st()), 50, 5)
+    tmp = torch.empty(rows * ffn, device=dev)
+    ms_unfused = timed(lambda i: (lib.rfxq_silu_and_mul(gate.data_ptr(), up.data_ptr(), tmp.data_ptr(),
+                                                        rows * ffn, st()),
+                                  lib.rfxq_quantize_act_q8_1(tmp.data_ptr(), rows, ffn, act_f.data_ptr(), st())), 50, 5)
+    act_bytes = lambda k: rows * k * 3 + rows * (k // 32) * 4 + rows * (k // 256) * 64
+    out["producers_8b_m512"] = {
+        "rmsnorm_q8_1_us": round(ms_rms * 1e3, 1),
+        "rmsnorm_q8_1_gbs": round((rows * hid * 4 + act_bytes(hid)) / (ms_rms * 1e-3) / 1e9, 1),
+        "silu_and_mul_q8_1_us": round(ms_silu * 1e3, 1),
+        "silu_and_mul_q8_1_gbs": round((rows * ffn * 8 + act_bytes(ffn)) / (ms_silu * 1e-3) / 1e9, 1),
+        "silu_and_mul_then_quantize_us": round(ms_unfused * 1e3, 1)}
+    print(f"producers 8B M=512: rmsnorm_q8_1 {ms_rms * 1e3:.1f} us, silu_and_mul_q8_1 {ms_silu * 1e3:.1f} us "
+          f"(unfused {ms_unfused * 1e3:.1f} us)", file=sys.stderr, flush=True)
     return out
 
 

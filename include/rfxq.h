@@ -169,6 +169,47 @@ void rfxq_gemm_plan_destroy(rfxq_gemm_plan* plan);
 int rfxq_mmq_block_dots(const int8_t* xq, const uint32_t* xds, uint32_t rows, const rfxq_weight* w, int32_t* dots,
                         hipStream_t stream);
 
+/* ---- fused activation producers (prefill) -------------------------------- */
+
+/* An activation quantized per 32 (Q8_1: int8 values, f16 d and block sum) in
+ * every layout the MMQ kernels read, in one caller-owned buffer of
+ * rfxq_act_q8_1_size(rows, k) bytes (256-byte aligned; k a multiple of 256).
+ * Written by the producers below so that the GEMMs that follow read it
+ * directly (no f32 round trip and no separate quantize launch). No reference
+ * counterpart: the reference feeds the f32 outputs of its rmsnorm and
+ * silu_and_mul into the GEMMs (src/model/dense.rs:1468-1478). */
+uint64_t rfxq_act_q8_1_size(uint32_t rows, uint32_t k);
+
+/* Quantize a plain f32 activation [rows][k] into an activation buffer. */
+int rfxq_quantize_act_q8_1(const float* x, uint32_t rows, uint32_t k, void* act, hipStream_t stream);
+
+/* Model::rmsnorm (src/kernels_cuda/rmsnorm.cu:18-55, rmsnorm.cuh:17-41) fused
+ * with the quantization of its output: y = x / sqrt(mean(x^2) + eps) * weight
+ * with the reference's sum order (one thread per row, index order, fused
+ * multiply-adds), so the optional f32 output y is bit-identical to the
+ * reference kernel's and the buffer equals rfxq_quantize_act_q8_1(y). */
+int rfxq_rmsnorm_q8_1(const float* x, const float* weight, uint32_t rows, uint32_t k, float eps, void* act,
+                      float* y, hipStream_t stream);
+
+/* Model::silu_and_mul (src/kernels_cuda/silu_and_mul.cu:7-23) fused with the
+ * quantization of its output (y optional, equal to rfxq_silu_and_mul's). */
+int rfxq_silu_and_mul_q8_1(const float* gate, const float* up, uint32_t rows, uint32_t k, void* act, float* y,
+                           hipStream_t stream);
+
+/* rfxq_gemm / rfxq_gemm_batch from an activation buffer (rows as written).
+ * The workspace holds split-K partials only (rfxq_gemm_workspace_size
+ * bytes always suffice; NULL uses the library's). */
+int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* y, void* workspace,
+                   uint64_t workspace_bytes, hipStream_t stream);
+
+typedef struct rfxq_gemm_q8_1_item {
+    const void* act;
+    const rfxq_weight* w;
+    float* y;
+} rfxq_gemm_q8_1_item;
+
+int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, hipStream_t stream);
+
 /* ---- MoE ----------------------------------------------------------------- */
 
 /* src/moe.rs:47-98 route_top_k_with_norm on the host: softmax, top-k by

@@ -56,6 +56,7 @@ def lib():
         L.oracle_route_top_k.argtypes = [P, i64, i64, i32, P, P]
         L.oracle_route_top_k.restype = i32
         L.oracle_silu_and_mul.argtypes = [P, P, P, i64]
+        L.oracle_rmsnorm.argtypes = [P, P, P, i64, i64, ctypes.c_float]
         L.oracle_cpu_dequant_matmul.argtypes = [i32, P, i64, i64, P, i64, P, i32]
         L.oracle_cpu_dequant_matmul.restype = i32
         _lib = L
@@ -179,6 +180,15 @@ def silu_and_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     out = np.zeros_like(g)
     lib().oracle_silu_and_mul(_p(g), _p(u), _p(out), g.size)
     return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, rows: int, k: int, eps: float) -> np.ndarray:
+    """rmsnorm.cu:18-55 / rmsnorm.cuh:17-41 (sequential fused sum of squares)."""
+    xx = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    ww = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    out = np.zeros(rows * k, dtype=np.float32)
+    lib().oracle_rmsnorm(_p(xx), _p(ww), _p(out), rows, k, ctypes.c_float(eps))
+    return out.reshape(rows, k)
 
 
 def moe_ffn_grouped_reference(x, routes, gate_w, up_w, down_w, ty, hidden, ffn, n_experts):

@@ -15,6 +15,7 @@
  *     quant_resident_tests.rs:669-692, quant_resident_tests.rs:40-52
  *   - route_top_k_with_norm: src/moe.rs:47-98
  *   - silu_and_mul: src/kernels_cuda/silu_and_mul.cu:7-23
+ *   - rmsnorm: src/kernels_cuda/rmsnorm.cu:18-55, rmsnorm.cuh:17-41
  *   - moe_gather / moe_scatter_add: src/kernels_cuda/elementwise.cu:175-222
  *   - quantize_q8_1: the Q8_1 activation block (layout dequant.rs:228-240:
  *     d f16, s f16, qs[32]) filled by ggml's published quantize_row_q8_1_ref
@@ -429,6 +430,22 @@ void oracle_silu_and_mul(const float* gate, const float* up, float* out, long n)
     for (long i = 0; i < n; i++) {
         float g = gate[i];
         out[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+}
+
+/*
+ * rmsnorm.cu:18-55 with rmsnorm.cuh:17-41: per row, sum_sq accumulated in
+ * index order as fused multiply-adds (nvcc contracts `sum_sq += v * v`, as
+ * rmsnorm.cuh:4-5 states), r = 1 / sqrtf(sum_sq / hidden + eps), and
+ * y = (x * r) * w (two roundings).
+ */
+void oracle_rmsnorm(const float* x, const float* w, float* y, long rows, long k, float eps) {
+    for (long r = 0; r < rows; r++) {
+        const float* xr = x + r * k;
+        float sum_sq = 0.0f;
+        for (long i = 0; i < k; i++) sum_sq = fmaf(xr[i], xr[i], sum_sq);
+        const float inv = 1.0f / sqrtf(sum_sq / (float)k + eps);
+        for (long i = 0; i < k; i++) y[r * k + i] = (xr[i] * inv) * w[i];
     }
 }
 

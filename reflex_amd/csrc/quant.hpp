@@ -17,18 +17,31 @@
 #pragma once
 #include "common.hpp"
 
+// Sources of the values to quantize: a lane loads four consecutive values
+// of a row (row r, elements [c, c + 4)).
+struct QuantSrcPlain {  // x[src_rows[r] or r][c], row stride ldx
+    const float* x;
+    uint32_t ldx;
+    const int32_t* src_rows;
+    __device__ __forceinline__ float4 load(uint32_t r, uint32_t c) const {
+        const uint32_t sr = src_rows ? (uint32_t)src_rows[r] : r;
+        return *reinterpret_cast<const float4*>(x + (uint64_t)sr * ldx + c);
+    }
+};
+
 // Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
-// wave_global); 8 lanes per 32-block.
+// wave_global); 8 lanes per 32-block. `yout` (optional) receives the values
+// quantized, f32 [rows][k] (the producer's own output).
 // Optional layouts for the f16-MFMA kernels (mmq2.hpp):
 //   xh  [rows][k] f16: the int8 values, each group of four stored (q0, q2), (q1, q3)
 //   xsc [rows][k/256][32] u16: per super-block d[8], then Sx' = d*s*2^-6
 //       split exactly into f16 hi[8] and lo[8] (hi = f16(Sx'), lo = f16(Sx' - hi)),
 //       then d again in the order 0, 2, 1, 3, 4, 6, 5, 7 (dword j of that
 //       copy holds the scales of the two blocks one Q6_K 64-k stage reads)
-RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const int32_t* __restrict__ src_rows,
-                              uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
+template <class Src>
+RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
                               uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint16_t* __restrict__ xsc,
-                              uint64_t wave_global, uint64_t nwaves) {
+                              float* __restrict__ yout, uint64_t wave_global, uint64_t nwaves) {
     const uint32_t nblk = k / 32u;
     const uint64_t total = (uint64_t)rows * nblk;
     const uint32_t lane = threadIdx.x & 63u;
@@ -38,8 +51,8 @@ RFXQ_DEV void quant_q8_1_rows(const float* __restrict__ x, uint32_t ldx, const i
         const uint64_t bb = valid ? bi : total - 1u;
         const uint32_t row = (uint32_t)(bb / nblk), blk = (uint32_t)(bb % nblk);
         const uint32_t part = lane & 7u;
-        const uint32_t srow = src_rows ? (uint32_t)src_rows[row] : row;
-        const float4 v = *reinterpret_cast<const float4*>(x + (uint64_t)srow * ldx + 32u * blk + 4u * part);
+        const float4 v = src.load(row, 32u * blk + 4u * part);
+        if (yout && valid) *reinterpret_cast<float4*>(yout + (uint64_t)row * k + 32u * blk + 4u * part) = v;
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
         amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
@@ -94,7 +107,7 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float
                                                                     uint32_t* __restrict__ xds,
                                                                     uint16_t* __restrict__ xh,
                                                                     uint16_t* __restrict__ xsc) {
-    quant_q8_1_rows(x, ldx, src_rows, rows, k, xq, ldq, xds, xh, xsc,
+    quant_q8_1_rows(QuantSrcPlain{x, ldx, src_rows}, rows, k, xq, ldq, xds, xh, xsc, nullptr,
                     ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
 }
 
@@ -119,6 +132,96 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1_multi(const
     }
     const QuantDesc d = table[lo];
     const uint32_t wg = blockIdx.x - d.wg_begin;
-    quant_q8_1_rows(d.x, d.k, nullptr, d.rows, d.k, d.xq, d.k, d.xds, d.xh, d.xsc,
+    quant_q8_1_rows(QuantSrcPlain{d.x, d.k, nullptr}, d.rows, d.k, d.xq, d.k, d.xds, d.xh, d.xsc, nullptr,
                     ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6, ((uint64_t)d.wgs * blockDim.x) >> 6);
+}
+
+// ---------------------------------------------------------------- fused producers
+//
+// The activation producers of the prefill GEMMs write the quantized layouts
+// directly (and, optionally, their own f32 output), so the activation is not
+// written in f32 and read back by a separate quantize launch.
+
+// RMSNorm (src/kernels_cuda/rmsnorm.cu:18-55 with rmsnorm.cuh:17-41):
+// y = (x * r) * g, r = 1 / sqrtf(sum_sq / k + eps), sum_sq accumulated by one
+// thread per row in index order as fused multiply-adds (the reference's
+// order and contraction, so y is bit-identical to its output).
+constexpr uint32_t kNormRowsPerWg = 4;
+
+struct QuantSrcRms {
+    const float* x;
+    const float* g;
+    const float* rinv;  // per row of the workgroup (LDS)
+    uint32_t k;
+    __device__ __forceinline__ float4 load(uint32_t r, uint32_t c) const {
+        const float4 v = *reinterpret_cast<const float4*>(x + (uint64_t)r * k + c);
+        const float4 w = *reinterpret_cast<const float4*>(g + c);
+        const float s = rinv[r];
+        return make_float4((v.x * s) * w.x, (v.y * s) * w.y, (v.z * s) * w.z, (v.w * s) * w.w);
+    }
+};
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_rmsnorm_q8_1(const float* __restrict__ x,
+                                                                   const float* __restrict__ g, uint32_t rows,
+                                                                   uint32_t k, float eps, int8_t* __restrict__ xq,
+                                                                   uint32_t* __restrict__ xds,
+                                                                   uint16_t* __restrict__ xh,
+                                                                   uint16_t* __restrict__ xsc,
+                                                                   float* __restrict__ y) {
+    __shared__ float rinv[kNormRowsPerWg];
+    const uint32_t r0 = blockIdx.x * kNormRowsPerWg;
+    const uint32_t nr = min(kNormRowsPerWg, rows - r0);
+    if (threadIdx.x < nr) {
+        // one lane per row: the chain of fused multiply-adds is sequential,
+        // the row's loads run kAhead float4s ahead of it
+        constexpr uint32_t kAhead = 8;
+        const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)(r0 + threadIdx.x) * k);
+        const uint32_t n4 = k / 4u;  // a multiple of 64
+        float4 buf[kAhead];
+#pragma unroll
+        for (uint32_t j = 0; j < kAhead; j++) buf[j] = xr[j];
+        float sum_sq = 0.0f;
+        for (uint32_t j0 = 0; j0 < n4; j0 += kAhead) {
+#pragma unroll
+            for (uint32_t j = 0; j < kAhead; j++) {
+                const float4 v = buf[j];
+                buf[j] = xr[j0 + j + kAhead < n4 ? j0 + j + kAhead : 0u];
+                sum_sq = __builtin_fmaf(v.x, v.x, sum_sq);
+                sum_sq = __builtin_fmaf(v.y, v.y, sum_sq);
+                sum_sq = __builtin_fmaf(v.z, v.z, sum_sq);
+                sum_sq = __builtin_fmaf(v.w, v.w, sum_sq);
+            }
+        }
+        rinv[threadIdx.x] = 1.0f / sqrtf(sum_sq / (float)k + eps);
+    }
+    __syncthreads();
+    const uint64_t o = (uint64_t)r0 * k, nblk = k / 32u;
+    quant_q8_1_rows(QuantSrcRms{x + o, g, rinv, k}, nr, k, xq + o, k, xds + r0 * nblk, xh + o,
+                    xsc + r0 * (nblk / 8u) * 32u, y ? y + o : nullptr, threadIdx.x >> 6, 4u);
+}
+
+// SiLU(gate) * up (src/kernels_cuda/silu_and_mul.cu:7-23: g / (1 + expf(-g)) * u)
+struct QuantSrcSilu {
+    const float* gate;
+    const float* up;
+    uint32_t k;
+    __device__ __forceinline__ float4 load(uint32_t r, uint32_t c) const {
+        const uint64_t i = (uint64_t)r * k + c;
+        const float4 g = *reinterpret_cast<const float4*>(gate + i);
+        const float4 u = *reinterpret_cast<const float4*>(up + i);
+        return make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                           (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
+    }
+};
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_silu_and_mul_q8_1(const float* __restrict__ gate,
+                                                                        const float* __restrict__ up,
+                                                                        uint32_t rows, uint32_t k,
+                                                                        int8_t* __restrict__ xq,
+                                                                        uint32_t* __restrict__ xds,
+                                                                        uint16_t* __restrict__ xh,
+                                                                        uint16_t* __restrict__ xsc,
+                                                                        float* __restrict__ y) {
+    quant_q8_1_rows(QuantSrcSilu{gate, up, k}, rows, k, xq, k, xds, xh, xsc, y,
+                    ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
 }

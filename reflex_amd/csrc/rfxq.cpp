@@ -101,8 +101,9 @@ static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
 constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 32 KB weight ring)
-constexpr uint32_t kMaxGemvK = 16384;
-constexpr uint32_t kMoeGemvRows = 4;  // moe_ffn_grouped: up to this many tokens run as GEMVs  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
+constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
+constexpr uint32_t kMoeGemvRows = 4;   // moe_ffn_grouped: up to this many tokens run as GEMVs
+constexpr uint32_t kNormRowsPerWg = 4;  // rows per rfxq_rmsnorm_q8_1 workgroup (the kernel's constant)
 
 // ------------------------------------------------------------------ per-device module
 
@@ -115,6 +116,7 @@ struct Ctx {
     hipFunction_t mmq2_q4k = nullptr, mmq2_q6k = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
+    hipFunction_t rms_q = nullptr, silu_q = nullptr;
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
     // device area for per-call descriptor tables (grow-only, separate from ws)
@@ -182,6 +184,8 @@ int load_ctx(int device, Ctx** out) {
         {&c->gather, "rfxq_moe_gather"},
         {&c->scatter, "rfxq_moe_scatter_add"},
         {&c->silu, "rfxq_silu_and_mul"},
+        {&c->rms_q, "rfxq_rmsnorm_q8_1"},
+        {&c->silu_q, "rfxq_silu_and_mul_q8_1"},
         {&c->combine, "rfxq_moe_combine"},
     };
     for (auto& f : fns) {
@@ -625,25 +629,13 @@ int check_mmq_weight(const rfxq_weight* w, const char* what) {
     return RFXQ_OK;
 }
 
-int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
-              hipStream_t stream) {
+// One GEMM's MMQ launch from quantized activations (xh / xsc for the f16
+// kernels, xq / xds otherwise), then the split-K reduce when p splits K
+// (partials in `part`).
+int gemm_run(Ctx* c, const GemmPlan& p, const int8_t* xq, const uint32_t* xds, const uint16_t* xh,
+             const uint16_t* xsc, bool f16, const rfxq_weight* w, uint32_t rows, float* y, float* part,
+             hipStream_t stream) {
     const uint32_t k = w->in_features, n = w->out_features;
-    const GemmPlan p = plan_gemm(c, rows, k, n);
-    if (!ws) {
-        if (int rc = ctx_workspace(c, p.total, &ws)) return rc;
-    } else if (ws_bytes < p.total) {
-        return fail(RFXQ_ERR_INVALID_INPUT, "gemm: workspace of %llu bytes, needs %llu",
-                    (unsigned long long)ws_bytes, (unsigned long long)p.total);
-    }
-    uint8_t* base = static_cast<uint8_t*>(ws);
-    int8_t* xq = reinterpret_cast<int8_t*>(base);
-    uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
-    float* part = reinterpret_cast<float*>(base + p.off_part);
-    const bool f16 = use_mmq2(w, rows);
-    uint16_t* xh = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xh) : nullptr;
-    uint16_t* xsc = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xsc) : nullptr;
-    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, f16 ? nullptr : xds, stream, xh, xsc))
-        return rc;
     MmqDesc d;
     std::memset(&d, 0, sizeof d);
     d.w = w->data;
@@ -674,6 +666,61 @@ int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float
             return rc;
     }
     return RFXQ_OK;
+}
+
+int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
+              hipStream_t stream) {
+    const uint32_t k = w->in_features, n = w->out_features;
+    const GemmPlan p = plan_gemm(c, rows, k, n);
+    if (!ws) {
+        if (int rc = ctx_workspace(c, p.total, &ws)) return rc;
+    } else if (ws_bytes < p.total) {
+        return fail(RFXQ_ERR_INVALID_INPUT, "gemm: workspace of %llu bytes, needs %llu",
+                    (unsigned long long)ws_bytes, (unsigned long long)p.total);
+    }
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    int8_t* xq = reinterpret_cast<int8_t*>(base);
+    uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
+    float* part = reinterpret_cast<float*>(base + p.off_part);
+    const bool f16 = use_mmq2(w, rows);
+    uint16_t* xh = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xh) : nullptr;
+    uint16_t* xsc = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xsc) : nullptr;
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, f16 ? nullptr : xds, stream, xh, xsc))
+        return rc;
+    return gemm_run(c, p, xq, xds, xh, xsc, f16, w, rows, y, part, stream);
+}
+
+// ------------------------------------------------------------------ quantized activation buffers
+
+// One activation quantized in every layout the MMQ kernels read: xq, xds,
+// then (f16 kernels) xh and xsc, each 256-byte aligned.
+struct ActLayout {
+    uint64_t xds, xh, xsc, total;
+};
+
+ActLayout act_layout(uint32_t rows, uint32_t k) {
+    ActLayout L;
+    L.xds = align256((uint64_t)rows * k);
+    L.xh = L.xds + align256((uint64_t)rows * (k / 32u) * 4u);
+    L.xsc = L.xh + xh_bytes(rows, k);
+    L.total = L.xsc + xsc_bytes(rows, k);
+    return L;
+}
+
+int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
+    if (!act) return fail(RFXQ_ERR_INVALID_INPUT, "%s: act is NULL", what);
+    if (reinterpret_cast<uintptr_t>(act) % 256u) return fail(RFXQ_ERR_OTHER, "%s: act is not 256-byte aligned", what);
+    if (rows == 0 || k == 0 || k % 256u)
+        return fail(RFXQ_ERR_OTHER, "%s: rows=%u k=%u (k must be a non-zero multiple of 256)", what, rows, k);
+    return RFXQ_OK;
+}
+
+// the descriptor fields of a GEMM reading activation buffer `act`
+void act_desc(MmqDesc* d, const void* act, const ActLayout& L, bool f16, uint32_t k) {
+    const uint8_t* a = static_cast<const uint8_t*>(act);
+    d->xq = reinterpret_cast<const int8_t*>(f16 ? a + L.xh : a);
+    d->xds = reinterpret_cast<const uint32_t*>(f16 ? a + L.xsc : a + L.xds);
+    d->ldq = f16 ? 2u * k : k;
 }
 
 // ------------------------------------------------------------------ grouped GEMMs
@@ -1108,6 +1155,160 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
                 wg += d[j].tiles_m * d[j].tiles_n;
             }
             if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16[t])) return rc;
+        }
+    }
+    return ok();
+}
+
+uint64_t rfxq_act_q8_1_size(uint32_t rows, uint32_t k) {
+    return rows && k && k % 256u == 0 ? act_layout(rows, k).total : 0;
+}
+
+int rfxq_quantize_act_q8_1(const float* x, uint32_t rows, uint32_t k, void* act, hipStream_t stream) {
+    if (int rc = check_act(act, rows, k, "quantize_act_q8_1")) return rc;
+    if (!x || reinterpret_cast<uintptr_t>(x) % 16u)
+        return fail(RFXQ_ERR_OTHER, "quantize_act_q8_1: x is NULL or not 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    const ActLayout L = act_layout(rows, k);
+    uint8_t* b = static_cast<uint8_t*>(act);
+    if (int rc = launch_quant(c, x, k, nullptr, rows, k, reinterpret_cast<int8_t*>(b),
+                              reinterpret_cast<uint32_t*>(b + L.xds), stream, reinterpret_cast<uint16_t*>(b + L.xh),
+                              reinterpret_cast<uint16_t*>(b + L.xsc)))
+        return rc;
+    return ok();
+}
+
+int rfxq_rmsnorm_q8_1(const float* x, const float* weight, uint32_t rows, uint32_t k, float eps, void* act, float* y,
+                      hipStream_t stream) {
+    if (int rc = check_act(act, rows, k, "rmsnorm_q8_1")) return rc;
+    if (!x || !weight || reinterpret_cast<uintptr_t>(x) % 16u || reinterpret_cast<uintptr_t>(weight) % 16u ||
+        reinterpret_cast<uintptr_t>(y) % 16u)
+        return fail(RFXQ_ERR_OTHER, "rmsnorm_q8_1: x and weight must be non-NULL, x, weight and y 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    const ActLayout L = act_layout(rows, k);
+    uint8_t* b = static_cast<uint8_t*>(act);
+    struct {
+        const float* x;
+        const float* g;
+        uint32_t rows, k;
+        float eps;
+        uint32_t pad;
+        int8_t* xq;
+        uint32_t* xds;
+        uint16_t* xh;
+        uint16_t* xsc;
+        float* y;
+    } a = {x, weight, rows, k, eps, 0, reinterpret_cast<int8_t*>(b), reinterpret_cast<uint32_t*>(b + L.xds),
+           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsc), y};
+    const uint32_t grid = (rows + kNormRowsPerWg - 1u) / kNormRowsPerWg;
+    if (int rc = launch(c->rms_q, grid, 0, stream, &a, sizeof a, "rfxq_rmsnorm_q8_1 launch")) return rc;
+    return ok();
+}
+
+int rfxq_silu_and_mul_q8_1(const float* gate, const float* up, uint32_t rows, uint32_t k, void* act, float* y,
+                           hipStream_t stream) {
+    if (int rc = check_act(act, rows, k, "silu_and_mul_q8_1")) return rc;
+    if (!gate || !up || reinterpret_cast<uintptr_t>(gate) % 16u || reinterpret_cast<uintptr_t>(up) % 16u ||
+        reinterpret_cast<uintptr_t>(y) % 16u)
+        return fail(RFXQ_ERR_OTHER, "silu_and_mul_q8_1: gate and up must be non-NULL, gate, up and y 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    const ActLayout L = act_layout(rows, k);
+    uint8_t* b = static_cast<uint8_t*>(act);
+    struct {
+        const float* gate;
+        const float* up;
+        uint32_t rows, k;
+        int8_t* xq;
+        uint32_t* xds;
+        uint16_t* xh;
+        uint16_t* xsc;
+        float* y;
+    } a = {gate, up, rows, k, reinterpret_cast<int8_t*>(b), reinterpret_cast<uint32_t*>(b + L.xds),
+           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsc), y};
+    if (int rc = launch(c->silu_q, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
+                        "rfxq_silu_and_mul_q8_1 launch"))
+        return rc;
+    return ok();
+}
+
+int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* y, void* workspace,
+                   uint64_t workspace_bytes, hipStream_t stream) {
+    if (int rc = check_mmq_weight(w, "gemm_q8_1")) return rc;
+    const uint32_t k = w->in_features, n = w->out_features;
+    if (int rc = check_act(act, rows, k, "gemm_q8_1")) return rc;
+    if (!y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1: y is NULL");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    const GemmPlan p = plan_gemm(c, rows, k, n);
+    float* part = nullptr;
+    if (p.splits > 1) {
+        const uint64_t need = (uint64_t)p.splits * rows * n * 4u;
+        void* ws = workspace;
+        if (!ws) {
+            if (int rc = ctx_workspace(c, need, &ws)) return rc;
+        } else if (workspace_bytes < need) {
+            return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1: workspace of %llu bytes, needs %llu",
+                        (unsigned long long)workspace_bytes, (unsigned long long)need);
+        }
+        part = static_cast<float*>(ws);
+    }
+    const ActLayout L = act_layout(rows, k);
+    const uint8_t* b = static_cast<const uint8_t*>(act);
+    if (int rc = gemm_run(c, p, reinterpret_cast<const int8_t*>(b), reinterpret_cast<const uint32_t*>(b + L.xds),
+                          reinterpret_cast<const uint16_t*>(b + L.xh), reinterpret_cast<const uint16_t*>(b + L.xsc),
+                          use_mmq2(w, rows), w, rows, y, part, stream))
+        return rc;
+    return ok();
+}
+
+int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, hipStream_t stream) {
+    if (count == 0) return ok();
+    if (!items) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: items is NULL");
+    bool f16[3] = {mmq_f16(), mmq_f16(), false};
+    for (uint32_t i = 0; i < count; i++) {
+        const rfxq_gemm_q8_1_item& it = items[i];
+        if (int rc = check_mmq_weight(it.w, "gemm_q8_1_batch")) return rc;
+        if (int rc = check_act(it.act, rows, it.w->in_features, "gemm_q8_1_batch")) return rc;
+        if (!it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: item %u has a NULL y", i);
+        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !use_mmq2(it.w, rows)) f16[type_index(it.w->ggml_type)] = false;
+    }
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    std::vector<MmqDesc> descs[3];
+    for (uint32_t i = 0; i < count; i++) {
+        const rfxq_gemm_q8_1_item& it = items[i];
+        const uint32_t k = it.w->in_features, t = type_index(it.w->ggml_type);
+        MmqDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.w = it.w->data;
+        act_desc(&d, it.act, act_layout(rows, k), f16[t], k);
+        d.y = it.y;
+        d.m = rows;
+        d.n = it.w->out_features;
+        d.k = k;
+        d.type = it.w->ggml_type;
+        d.ldy = d.n;
+        d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
+        d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
+        d.splits = 1;
+        d.sb_per_split = k / 256u;
+        descs[t].push_back(d);
+    }
+    for (uint32_t t = 0; t < 3; t++) {
+        auto& v = descs[t];
+        for (size_t i0 = 0; i0 < v.size(); i0 += kMmqInline) {
+            const uint32_t cnt = (uint32_t)std::min<size_t>(kMmqInline, v.size() - i0);
+            MmqDesc d[kMmqInline];
+            uint32_t wg = 0;
+            for (uint32_t j = 0; j < cnt; j++) {
+                d[j] = v[i0 + j];
+                d[j].wg_begin = wg;
+                wg += d[j].tiles_m * d[j].tiles_n;
+            }
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, f16[t])) return rc;
         }
     }
     return ok();

@@ -25,6 +25,7 @@ __all__ = [
     "gemm", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
     "route_top_k", "route_top_k_with_norm", "quant_expert_weight", "expert_gemv", "expert_gemm",
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
+    "act_q8_1_size", "quantize_act_q8_1", "rmsnorm_q8_1", "silu_and_mul_q8_1", "gemm_q8_1", "gemm_q8_1_batch",
 ]
 
 
@@ -306,6 +307,65 @@ def gemm_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int
     arr, _keep = _items(items)
     with _dev(items[0][0]):
         _check(lib().rfxq_gemm_batch(arr, len(items), rows, _stream()))
+
+
+# ------------------------------------------------------------------ fused activation producers
+
+def act_q8_1_size(rows: int, k: int) -> int:
+    """Bytes of a quantized activation buffer (every MMQ layout) for [rows][k]."""
+    return int(lib().rfxq_act_q8_1_size(rows, k))
+
+
+def _act(rows: int, k: int, device) -> torch.Tensor:
+    n = act_q8_1_size(rows, k)
+    if n == 0:
+        raise InvalidInputError(11, f"activation buffer: rows={rows} k={k} (k must be a multiple of 256)")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def quantize_act_q8_1(x: torch.Tensor, rows: int, k: int) -> torch.Tensor:
+    """A plain f32 activation [rows][k] quantized into an activation buffer."""
+    act = _act(rows, k, x.device)
+    with _dev(x):
+        _check(lib().rfxq_quantize_act_q8_1(x.data_ptr(), rows, k, act.data_ptr(), _stream()))
+    return act
+
+
+def rmsnorm_q8_1(x: torch.Tensor, weight: torch.Tensor, rows: int, k: int, eps: float, want_y: bool = False):
+    """``Model::rmsnorm`` (rmsnorm.cu) fused with quantization: (act, y or None)."""
+    act = _act(rows, k, x.device)
+    y = torch.empty(rows * k, dtype=torch.float32, device=x.device) if want_y else None
+    with _dev(x):
+        _check(lib().rfxq_rmsnorm_q8_1(x.data_ptr(), weight.data_ptr(), rows, k, eps, act.data_ptr(),
+                                       y.data_ptr() if y is not None else None, _stream()))
+    return act, y
+
+
+def silu_and_mul_q8_1(gate: torch.Tensor, up: torch.Tensor, rows: int, k: int, want_y: bool = False):
+    """``Model::silu_and_mul`` (silu_and_mul.cu) fused with quantization: (act, y or None)."""
+    act = _act(rows, k, gate.device)
+    y = torch.empty(rows * k, dtype=torch.float32, device=gate.device) if want_y else None
+    with _dev(gate):
+        _check(lib().rfxq_silu_and_mul_q8_1(gate.data_ptr(), up.data_ptr(), rows, k, act.data_ptr(),
+                                            y.data_ptr() if y is not None else None, _stream()))
+    return act, y
+
+
+def gemm_q8_1(act: torch.Tensor, w: Weight, rows: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``Model::gemm`` from a quantized activation buffer."""
+    y = out if out is not None else torch.empty(rows * w.out_features, dtype=torch.float32, device=act.device)
+    with _dev(act):
+        _check(lib().rfxq_gemm_q8_1(act.data_ptr(), rows, w.cref(), y.data_ptr(), None, 0, _stream()))
+    return y
+
+
+def gemm_q8_1_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int) -> None:
+    """Grouped GEMMs from activation buffers: items are (act, w, y)."""
+    if not items:
+        return
+    arr, _keep = _items(items)
+    with _dev(items[0][0]):
+        _check(lib().rfxq_gemm_q8_1_batch(arr, len(items), rows, _stream()))
 
 
 class GemmPlan:

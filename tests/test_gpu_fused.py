@@ -1,0 +1,106 @@
+"""Fused activation producers of the prefill GEMMs: RMSNorm and SiLU·up
+that write the quantized activation layouts directly, and GEMMs that read
+them. Parity: the producers' f32 outputs are bit-identical to the reference
+kernels' (rmsnorm.cu through the oracle restatement; silu_and_mul.cu through
+rfxq_silu_and_mul), their activation buffers equal the quantizer's on those
+outputs byte for byte, and GEMMs from the buffers equal rfxq_gemm on the f32
+activations bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from reflex_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4K, Q6K = 8, 12, 14
+DEV = "cuda:0"
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _a256(n):
+    return (n + 255) // 256 * 256
+
+
+def _layouts(act, rows, k):
+    """The written regions of an activation buffer: xq, xds, xh, xsc."""
+    b = act.cpu().numpy()
+    xds = _a256(rows * k)
+    xh = xds + _a256(rows * k // 32 * 4)
+    xsc = xh + _a256(rows * k * 2)
+    return (b[:rows * k], b[xds:xds + rows * k // 32 * 4], b[xh:xh + rows * k * 2],
+            b[xsc:xsc + rows * (k // 256) * 64])
+
+
+def _same_act(a, b, rows, k):
+    for i, (u, v) in enumerate(zip(_layouts(a, rows, k), _layouts(b, rows, k))):
+        assert np.array_equal(u, v), f"layout {i}"
+
+
+@pytest.mark.parametrize("rows,k", [(1, 1024), (7, 4096), (512, 1024), (33, 2048)])
+def test_rmsnorm_q8_1(rq, orc, rows, k):
+    rng = np.random.default_rng(rows + k)
+    x = (rng.standard_normal((rows, k)) * 3.0).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    eps = 1e-6
+    act, y = rq.rmsnorm_q8_1(_dev(x), _dev(g), rows, k, eps, want_y=True)
+    want = orc.rmsnorm(x, g, rows, k, eps)
+    assert np.array_equal(y.cpu().numpy().reshape(rows, k), want)
+    _same_act(act, rq.quantize_act_q8_1(_dev(want), rows, k), rows, k)
+    act2, none = rq.rmsnorm_q8_1(_dev(x), _dev(g), rows, k, eps)   # without the f32 output
+    assert none is None
+    _same_act(act2, act, rows, k)
+
+
+@pytest.mark.parametrize("rows,k", [(1, 3072), (64, 768 * 4), (512, 1024)])
+def test_silu_and_mul_q8_1(rq, rows, k):
+    rng = np.random.default_rng(rows * 3 + k)
+    gate = _dev((rng.standard_normal(rows * k) * 4).astype(np.float32))
+    up = _dev(rng.standard_normal(rows * k).astype(np.float32))
+    act, y = rq.silu_and_mul_q8_1(gate, up, rows, k, want_y=True)
+    ref = rq.silu_and_mul(gate, up)
+    assert torch.equal(y, ref)
+    _same_act(act, rq.quantize_act_q8_1(ref, rows, k), rows, k)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("rows,n,k", [(512, 1024, 1024), (64, 512, 4096), (300, 136, 2048)])
+def test_gemm_from_activation_buffer(rq, ty, rows, n, k):
+    x = _dev(synth.activations(rows * k, 5 + rows))
+    w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, 6 + n), k, n, device=DEV)
+    want = rq.gemm(x, w, rows)
+    act = rq.quantize_act_q8_1(x, rows, k)
+    assert torch.equal(rq.gemm_q8_1(act, w, rows), want)
+
+
+def test_gemm_q8_1_batch(rq):
+    rows = 200
+    shapes = [(Q4K, 768, 1024), (Q6K, 256, 1024), (Q4K, 640, 2048), (Q8_0, 128, 1024)]
+    xa, xb = _dev(synth.activations(rows * 1024, 1)), _dev(synth.activations(rows * 2048, 2))
+    aa, ab = rq.quantize_act_q8_1(xa, rows, 1024), rq.quantize_act_q8_1(xb, rows, 2048)
+    items = []
+    for i, (ty, n, k) in enumerate(shapes):
+        w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, 20 + i), k, n, device=DEV)
+        y = torch.full((rows * n,), float("nan"), device=DEV)
+        items.append((aa if k == 1024 else ab, w, y))
+    refs = []
+    for (act, w, _), (ty, n, k) in zip(items, shapes):
+        r = torch.empty(rows * n, device=DEV)
+        rq.gemm_batch([(xa if k == 1024 else xb, w, r)], rows)
+        refs.append(r)
+    rq.gemm_q8_1_batch(items, rows)
+    for (_, _, y), r in zip(items, refs):
+        assert torch.equal(y, r)
+
+
+def test_fused_producer_errors(rq):
+    x = _dev(np.ones((4, 1000), np.float32))
+    with pytest.raises(rq.ReflexError, match="multiple of 256"):
+        rq.quantize_act_q8_1(x, 4, 1000)
+    w = rq.Weight.from_blocks(Q4K, synth.weights(Q4K, 64, 1024, 3), 1024, 64, device=DEV)
+    act = torch.empty(rq.act_q8_1_size(4, 1024) + 256, dtype=torch.uint8, device=DEV)
+    with pytest.raises(rq.ReflexError, match="256-byte aligned"):
+        rq.gemm_q8_1(act[16:], w, 4)

@@ -324,3 +324,76 @@ def test_committed_fixtures_reproduce(orc):
         assert np.array_equal(orc.reference_gemm(ty, w, n, k, f["x"][:, :k]), f[f"{name}_y"])
     qs, ds = orc.quantize_q8_1(f["x"])
     assert np.array_equal(qs, f["xq"]) and np.array_equal(ds, f["xds"])
+
+
+# ------------------------------------------------------------------ rmsnorm
+
+def _round_f32(q):
+    """A Fraction rounded to the nearest float32 (ties to even), exactly."""
+    from fractions import Fraction
+    if q == 0:
+        return np.float32(0.0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)                       # subnormal spacing below 2^-126
+    ulp = Fraction(2) ** (e - 23)
+    m = a / ulp
+    n = m.numerator // m.denominator
+    rem = m - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return np.float32(sign * float(n * ulp))
+
+
+def _rmsnorm_exact(x, w, eps):
+    """Independent restatement: the sum of squares as a chain of exactly
+    rounded fused multiply-adds (rational arithmetic), then numpy float32
+    division, sqrt and products (IEEE, correctly rounded)."""
+    from fractions import Fraction
+    rows, k = x.shape
+    out = np.zeros_like(x)
+    for r in range(rows):
+        s = np.float32(0.0)
+        for v in x[r]:
+            s = _round_f32(Fraction(float(v)) * Fraction(float(v)) + Fraction(float(s)))
+        inv = np.float32(1.0) / np.sqrt(s / np.float32(k) + np.float32(eps))
+        out[r] = (x[r] * inv) * w
+    return out
+
+
+def test_rmsnorm_matches_exact_fma_chain(orc):
+    """rmsnorm.cuh:17-41's fused sum order, pinned by exact rational FMAs; a
+    plain (separately rounded) sum of squares differs on these inputs."""
+    rng = np.random.default_rng(12)
+    rows, k, eps = 5, 64, 1e-6
+    x = (rng.standard_normal((rows, k)) * np.exp(rng.uniform(-3, 3, (rows, k)))).astype(np.float32)
+    w = rng.standard_normal(k).astype(np.float32)
+    got = orc.rmsnorm(x, w, rows, k, eps)
+    want = _rmsnorm_exact(x, w, eps)
+    assert np.array_equal(got, want)
+    # the same with a separately rounded v*v: different outputs on some rows
+    rows2 = 64
+    x2 = (rng.standard_normal((rows2, k)) * np.exp(rng.uniform(-3, 3, (rows2, k)))).astype(np.float32)
+    plain = np.zeros(rows2, np.float32)
+    for r in range(rows2):
+        for v in x2[r]:
+            plain[r] = np.float32(plain[r] + np.float32(v * v))
+    inv_plain = np.float32(1.0) / np.sqrt(plain / np.float32(k) + np.float32(eps))
+    assert not np.array_equal((x2 * inv_plain[:, None]) * w, orc.rmsnorm(x2, w, rows2, k, eps))
+
+
+def test_rmsnorm_closed_form(orc):
+    """Rows of one repeated power of two: the sum of squares is exact, so
+    y = w * c / sqrt(c^2 + eps) exactly as numpy computes it in f32."""
+    k = 256
+    for c, eps in [(1.0, 1e-6), (0.5, 1e-5), (2.0, 0.0)]:
+        x = np.full((2, k), c, np.float32)
+        w = np.linspace(-2, 2, k, dtype=np.float32)
+        got = orc.rmsnorm(x, w, 2, k, eps)
+        inv = np.float32(1.0) / np.sqrt(np.float32(c * c) + np.float32(eps))
+        assert np.array_equal(got, np.stack([(x[0] * inv) * w] * 2))
