@@ -286,6 +286,15 @@ def moe_leg(rq, synth, torch, np, dev, timed):
                     "tops": round(ops / (ms * 1e-3) / 1e12, 2)}
         print(f"moe {tag}: {ms * 1e3:.1f} us/step  {gbs:.0f} GB/s of routed expert weights "
               f"({gbs / HBM_PEAK_GBS:.1%} of HBM), {used} experts", file=sys.stderr, flush=True)
+        # the same step with routing on the device (logits in device memory)
+        lg = torch.from_numpy(logits).to(dev)
+        ms_d = timed(lambda i: rq.moe_ffn_grouped_device(x, tokens, H, lg, E, K, True, 1.0, gate, up, down, y),
+                     steps, 3)
+        gbs_d = wbytes / (ms_d * 1e-3) / 1e9
+        out[tag + "_device_routing"] = {"ms_per_step": round(ms_d, 4), "gbs": round(gbs_d, 1),
+                                        "frac_hbm_peak": round(gbs_d / HBM_PEAK_GBS, 4)}
+        print(f"moe {tag} (device routing): {ms_d * 1e3:.1f} us/step  {gbs_d:.0f} GB/s", file=sys.stderr,
+              flush=True)
     del gate, up, down
     return out
 

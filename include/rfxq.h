@@ -245,6 +245,30 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
                          const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
                          hipStream_t stream);
 
+/* ---- MoE with device-side routing --------------------------------------- */
+
+/* route_top_k_with_norm (src/moe.rs:47-98) for `tokens` rows of device
+ * logits [tokens][expert_count]: expert ids and weights (times
+ * weight_scale) [tokens][top_k] in selection order, in device memory. The
+ * softmax sum is taken in a different order than the host's, so weights can
+ * differ from route_top_k's in the last bit. expert_count <= 1024, top_k <= 64. */
+int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_count, uint32_t top_k,
+                          int normalize, float weight_scale, int32_t* idx, float* weights, hipStream_t stream);
+
+/* rfxq_moe_ffn_grouped with the router logits in device memory: routing,
+ * grouping by expert and the MMQ descriptor tables are built on the device
+ * (the reference copies the logits to the host and uploads per-expert row
+ * lists, src/model/dense.rs:1539-1546, 1602-1605), so the call adds no host
+ * synchronisation and no host-to-device copy. Every token count takes the
+ * grouped MMQ path (64-row tiles for short expert groups). Requires
+ * 4 <= expert_count <= 1024, top_k <= 64 and rows * top_k <= 16384.
+ * Routing errors of the host path (non-finite softmax sums) are not
+ * reported: such tokens get non-finite outputs. */
+int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
+                                uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
+                                const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
+                                hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,9 @@ SIGNATURES = {
     "rfxq_silu_and_mul": (_I, [_P, _P, _P, _U64, _P]),
     "rfxq_moe_ffn_grouped": (_I, [_P, _U32, _U32, _P, _U32, _U32, _I, ctypes.c_float, _WP, _WP, _WP, _P, _P]),
     "rfxq_act_q8_1_size": (_U64, [_U32, _U32]),
+    "rfxq_moe_route_device": (_I, [_P, _U32, _U32, _U32, _I, ctypes.c_float, _P, _P, _P]),
+    "rfxq_moe_ffn_grouped_device": (_I, [_P, _U32, _U32, _P, _U32, _U32, _I, ctypes.c_float, _WP, _WP, _WP, _P,
+                                         _P]),
     "rfxq_quantize_act_q8_1": (_I, [_P, _U32, _U32, _P, _P]),
     "rfxq_rmsnorm_q8_1": (_I, [_P, _P, _U32, _U32, ctypes.c_float, _P, _P, _P]),
     "rfxq_silu_and_mul_q8_1": (_I, [_P, _P, _U32, _U32, _P, _P, _P]),

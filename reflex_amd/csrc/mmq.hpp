@@ -486,6 +486,10 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
         }
 }
 
+// The descriptor of workgroup `wg`: the last one whose wg_begin is at or
+// below it (descriptors with no tiles share the next one's wg_begin and are
+// skipped). A workgroup past the last descriptor's tiles (launch grids that
+// are upper bounds, for tables built on the device) returns at once.
 RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
     if (a.ndesc <= MMQ_INLINE) {
         MmqDesc d = a.inl[0];
@@ -511,6 +515,7 @@ RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
         __shared__ float lds_sx[64 * MI * 8];                                 \
         __shared__ u4_t lds_masks[64];                                        \
         const MmqDesc d = mmq_pick(args, blockIdx.x);                         \
+        if (blockIdx.x - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return; \
         mmq_tile<TY, DOTS, MI>(d, blockIdx.x - d.wg_begin, lds_da, lds_sx, lds_masks); \
     }
 RFXQ_MMQ_ENTRY(rfxq_mmq_q4k, TY_Q4K, false, 2, 2)

@@ -334,6 +334,7 @@ RFXQ_DEV void mmq2_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmq2_q4k(MmqArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[mmq2::kLds];
     const MmqDesc d = mmq_pick(args, blockIdx.x);
+    if (blockIdx.x - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
     mmq2_q4k_tile(d, blockIdx.x - d.wg_begin, lds);
 }
 
@@ -633,5 +634,6 @@ RFXQ_DEV void mmq2_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmq2_q6k(MmqArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[mmq2::kLds6];
     const MmqDesc d = mmq_pick(args, blockIdx.x);
+    if (blockIdx.x - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
     mmq2_q6k_tile(d, blockIdx.x - d.wg_begin, lds);
 }

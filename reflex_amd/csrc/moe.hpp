@@ -65,3 +65,214 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_moe_combine(const float* 
         out[i] = acc;
     }
 }
+
+// ---------------------------------------------------------------- device routing
+//
+// The grouped MoE pipeline with routing on the device: router logits stay in
+// device memory (the reference copies them to the host, dense.rs:1602-1605,
+// and uploads per-expert row lists, :1539-1546). rfxq_moe_route does the
+// routing, rfxq_moe_plan the grouping and the MMQ descriptor tables; the
+// MMQ, SiLU, quantize and combine launches that follow read those tables.
+
+constexpr uint32_t kRouteMaxE = 1024;    // experts per lane: up to 16
+constexpr uint32_t kPlanMaxPairs = 16384;  // sort keys in LDS
+
+// route_top_k_with_norm (src/moe.rs:47-98), one wave per token: softmax of
+// the logits (max subtracted; the sum over lanes then a butterfly, so it can
+// differ from a sequential sum in the last bit), the k best by probability
+// descending then expert index ascending, renormalised by their sum (in
+// selection order) when `normalize`; weights multiplied by `scale`.
+extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __restrict__ logits, uint32_t tokens,
+                                                                uint32_t E, uint32_t k, uint32_t normalize,
+                                                                float scale, int32_t* __restrict__ idx,
+                                                                float* __restrict__ wts) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const float* l = logits + (uint64_t)t * E;
+    constexpr uint32_t J = kRouteMaxE / 64u;
+    float p[J];
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane + 64u * j;
+        p[j] = e < E ? l[e] : -INFINITY;
+        mx = fmaxf(mx, p[j]);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane + 64u * j;
+        p[j] = e < E ? expf(p[j] - mx) : 0.0f;
+        sum += p[j];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) p[j] = lane + 64u * j < E ? p[j] / sum : -1.0f;
+    float top_sum = 0.0f;
+    float sel_p = 0.0f;
+    int32_t sel_e = 0;
+    for (uint32_t s = 0; s < k; s++) {
+        // the lane's best, then the wave's: larger p, on ties the lower index
+        float bp = -2.0f;
+        int32_t be = 0x7FFFFFFF;
+#pragma unroll
+        for (uint32_t j = 0; j < J; j++) {
+            const int32_t e = (int32_t)(lane + 64u * j);
+            if (p[j] > bp) {
+                bp = p[j];
+                be = e;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float op = __shfl_xor(bp, m, 64);
+            const int32_t oe = __shfl_xor(be, m, 64);
+            if (op > bp || (op == bp && oe < be)) {
+                bp = op;
+                be = oe;
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < J; j++)
+            if ((int32_t)(lane + 64u * j) == be) p[j] = -1.0f;
+        top_sum += bp;
+        if (lane == s) {
+            sel_p = bp;
+            sel_e = be;
+        }
+    }
+    if (lane < k) {
+        const float wv = normalize ? sel_p / top_sum : sel_p;
+        idx[(uint64_t)t * k + lane] = sel_e;
+        wts[(uint64_t)t * k + lane] = wv * scale;
+    }
+}
+
+// Grouping and descriptor tables, one workgroup of 1024 threads: the pairs
+// (token t, slot j) sorted by (expert, t*k + j) with a bitonic sort of the
+// keys expert*P2 + pair in LDS; then
+//   pair_row[q]       token of the pair at sorted position q (MMQ row gather)
+//   comb_idx/comb_w   per token, its pairs' positions and weights in
+//                     increasing expert order (the combine's order)
+//   descs_gu[2e], [2e+1], descs_dn[e]  the gate, up and down MMQ descriptors
+//                     of expert e, from templates whose per-expert fields
+//                     (weights, rows, outputs, tile counts, workgroup
+//                     offsets) are filled here.
+struct MoePlanArgs {
+    const int32_t* idx;
+    const float* wts;
+    int32_t* pair_row;
+    int32_t* comb_idx;
+    float* comb_w;
+    MmqDesc* descs_gu;
+    MmqDesc* descs_dn;
+    MmqDesc tg, tu, td;         // templates (m, rows, wg_begin filled per expert)
+    uint64_t w_stride_gu;       // bytes between experts in gate / up
+    uint64_t w_stride_dn;       // ... in down
+    uint32_t tokens, k, E, P2;  // P2: power of two >= tokens * k
+    uint32_t bm, ffn, hidden, pad;
+};
+
+extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) {
+    __shared__ uint32_t key[kPlanMaxPairs];
+    __shared__ uint32_t start[kRouteMaxE + 1], cnt[kRouteMaxE];
+    const uint32_t tid = threadIdx.x, P = a.tokens * a.k, P2 = a.P2;
+    for (uint32_t i = tid; i < P2; i += 1024u)
+        key[i] = i < P ? (uint32_t)a.idx[i] * P2 + i : 0xFFFFFFFFu;
+    for (uint32_t e = tid; e < a.E; e += 1024u) cnt[e] = 0u;
+    __syncthreads();
+    for (uint32_t size = 2; size <= P2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = tid; i < P2 / 2u; i += 1024u) {
+                const uint32_t lo = 2u * i - (i & (stride - 1u));
+                const uint32_t hi = lo + stride;
+                const bool up = (lo & size) == 0u;
+                const uint32_t x = key[lo], y = key[hi];
+                if ((x > y) == up) {
+                    key[lo] = y;
+                    key[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // per sorted position: gather row, combine slot, expert bounds
+    for (uint32_t q = tid; q < P; q += 1024u) {
+        const uint32_t pair = key[q] % P2, e = key[q] / P2;
+        const uint32_t t = pair / a.k;
+        a.pair_row[q] = (int32_t)t;
+        uint32_t slot = 0;
+        for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)a.idx[(uint64_t)t * a.k + j] < e;
+        a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
+        a.comb_w[(uint64_t)t * a.k + slot] = a.wts[pair];
+        if (q == 0u || key[q - 1u] / P2 != e) start[e] = q;
+        if (q + 1u == P || key[q + 1u] / P2 != e) cnt[e] = q + 1u;  // end, made a count below
+    }
+    __syncthreads();
+    // per expert (one thread each): rows, tiles; workgroup offsets by an
+    // inclusive scan over the experts (Hillis-Steele in LDS)
+    __shared__ uint32_t scan_gu[kRouteMaxE], scan_dn[kRouteMaxE];
+    const uint32_t tn_f = (a.ffn + 127u) / 128u, tn_h = (a.hidden + 127u) / 128u;
+    uint32_t m = 0, tm = 0;
+    if (tid < a.E) {
+        m = cnt[tid] ? cnt[tid] - start[tid] : 0u;
+        tm = (m + a.bm - 1u) / a.bm;
+        scan_gu[tid] = 2u * tm * tn_f;
+        scan_dn[tid] = tm * tn_h;
+    }
+    __syncthreads();
+    for (uint32_t off = 1; off < a.E; off <<= 1) {
+        uint32_t vg = 0, vd = 0;
+        if (tid < a.E && tid >= off) {
+            vg = scan_gu[tid - off];
+            vd = scan_dn[tid - off];
+        }
+        __syncthreads();
+        if (tid < a.E) {
+            scan_gu[tid] += vg;
+            scan_dn[tid] += vd;
+        }
+        __syncthreads();
+    }
+    if (tid < a.E) {
+        const uint32_t e = tid;
+        const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
+        const uint32_t wg_gu = scan_gu[e] - 2u * tm * tn_f, wg_dn = scan_dn[e] - tm * tn_h;
+        // descriptors from the templates, filled in place in global memory
+        MmqDesc* g = a.descs_gu + 2u * e;
+        MmqDesc* u = g + 1;
+        MmqDesc* d = a.descs_dn + e;
+        {
+            const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.tg);
+            const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.tu);
+            const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.td);
+            uint32_t* pg = reinterpret_cast<uint32_t*>(g);
+            uint32_t* pu = reinterpret_cast<uint32_t*>(u);
+            uint32_t* pd = reinterpret_cast<uint32_t*>(d);
+#pragma unroll
+            for (uint32_t i = 0; i < sizeof(MmqDesc) / 4u; i++) {
+                pg[i] = tg[i];
+                pu[i] = tu[i];
+                pd[i] = td[i];
+            }
+        }
+        g->w = a.tg.w + (uint64_t)e * a.w_stride_gu;
+        u->w = a.tu.w + (uint64_t)e * a.w_stride_gu;
+        d->w = a.td.w + (uint64_t)e * a.w_stride_dn;
+        g->rows = u->rows = a.pair_row + st;
+        g->m = u->m = d->m = m;
+        g->tiles_m = u->tiles_m = d->tiles_m = tm;
+        g->y = a.tg.y + (uint64_t)st * a.ffn;
+        u->y = a.tu.y + (uint64_t)st * a.ffn;
+        d->xq = a.td.xq + (uint64_t)st * a.ffn;
+        d->xds = a.td.xds + (uint64_t)st * (a.ffn / 32u);
+        d->y = a.td.y + (uint64_t)st * a.hidden;
+        g->wg_begin = wg_gu;
+        u->wg_begin = wg_gu + tm * tn_f;
+        d->wg_begin = wg_dn;
+    }
+}

@@ -103,6 +103,8 @@ constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus its 32 KB weight ring)
 constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 constexpr uint32_t kMoeGemvRows = 4;   // moe_ffn_grouped: up to this many tokens run as GEMVs
+constexpr uint32_t kRouteMaxE = 1024;     // rfxq_moe_route: experts per token
+constexpr uint32_t kPlanMaxPairs = 16384;  // rfxq_moe_plan: routed pairs sorted in LDS
 constexpr uint32_t kNormRowsPerWg = 4;  // rows per rfxq_rmsnorm_q8_1 workgroup (the kernel's constant)
 
 // ------------------------------------------------------------------ per-device module
@@ -116,7 +118,7 @@ struct Ctx {
     hipFunction_t mmq2_q4k = nullptr, mmq2_q6k = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
-    hipFunction_t rms_q = nullptr, silu_q = nullptr;
+    hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
     // device area for per-call descriptor tables (grow-only, separate from ws)
@@ -186,6 +188,8 @@ int load_ctx(int device, Ctx** out) {
         {&c->silu, "rfxq_silu_and_mul"},
         {&c->rms_q, "rfxq_rmsnorm_q8_1"},
         {&c->silu_q, "rfxq_silu_and_mul_q8_1"},
+        {&c->moe_route, "rfxq_moe_route"},
+        {&c->moe_plan, "rfxq_moe_plan"},
         {&c->combine, "rfxq_moe_combine"},
     };
     for (auto& f : fns) {
@@ -1736,6 +1740,184 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
         if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
     }
+    return ok();
+}
+
+int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_count, uint32_t top_k,
+                          int normalize, float weight_scale, int32_t* idx, float* weights, hipStream_t stream) {
+    if (tokens == 0) return ok();
+    if (!logits || !idx || !weights) return fail(RFXQ_ERR_INVALID_INPUT, "moe_route_device: NULL pointer");
+    if (expert_count == 0 || expert_count > kRouteMaxE)
+        return fail(RFXQ_ERR_OTHER, "moe_route_device: expert_count=%u (1..=%u)", expert_count, kRouteMaxE);
+    if (top_k == 0 || top_k > expert_count || top_k > 64u)
+        return fail(RFXQ_ERR_OTHER, "route_top_k: k (%u) must be in 1..=%u (logits.len())", top_k,
+                    std::min(expert_count, 64u));
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    struct {
+        const float* l;
+        uint32_t tokens, E, k, normalize;
+        float scale;
+        uint32_t pad;
+        int32_t* idx;
+        float* w;
+    } a = {logits, tokens, expert_count, top_k, normalize ? 1u : 0u, weight_scale, 0, idx, weights};
+    if (int rc = launch(c->moe_route, (tokens + 3u) / 4u, 0, stream, &a, sizeof a, "rfxq_moe_route launch"))
+        return rc;
+    return ok();
+}
+
+struct MoePlanArgs {
+    const int32_t* idx;
+    const float* wts;
+    int32_t* pair_row;
+    int32_t* comb_idx;
+    float* comb_w;
+    MmqDesc* descs_gu;
+    MmqDesc* descs_dn;
+    MmqDesc tg, tu, td;
+    uint64_t w_stride_gu, w_stride_dn;
+    uint32_t tokens, k, E, P2;
+    uint32_t bm, ffn, hidden, pad;
+};
+static_assert(sizeof(MoePlanArgs) == 392, "MoePlanArgs layout");
+
+int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
+                                uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
+                                const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
+                                hipStream_t stream) {
+    if (!x || !out || !router_logits || !gate || !up || !down)
+        return fail(RFXQ_ERR_INVALID_INPUT, "moe_ffn_grouped_device: NULL argument");
+    if (rows == 0) return ok();
+    if (gate->expert_count != expert_count || up->expert_count != expert_count || down->expert_count != expert_count)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: expert tensors must have expert_count=%u", expert_count);
+    if (gate->in_features != hidden || up->in_features != hidden || down->out_features != hidden ||
+        gate->out_features != up->out_features || down->in_features != gate->out_features)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: shapes gate [%u,%u] up [%u,%u] down [%u,%u] hidden %u",
+                    gate->in_features, gate->out_features, up->in_features, up->out_features, down->in_features,
+                    down->out_features, hidden);
+    if (expert_count < 4 || expert_count > kRouteMaxE)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped_device: expert_count=%u (4..=%u)", expert_count, kRouteMaxE);
+    if (top_k == 0 || top_k > expert_count || top_k > 64u)
+        return fail(RFXQ_ERR_OTHER, "route_top_k: k (%u) must be in 1..=%u (logits.len())", top_k,
+                    std::min(expert_count, 64u));
+    const uint64_t P64 = (uint64_t)rows * top_k;
+    if (P64 > kPlanMaxPairs)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped_device: %llu routed pairs (at most %u)",
+                    (unsigned long long)P64, kPlanMaxPairs);
+    const uint32_t P = (uint32_t)P64, ffn = gate->out_features;
+    rfxq_weight g0, u0, d0;
+    if (int rc = expert_slice(gate, 0, &g0, "moe_ffn_grouped gate")) return rc;
+    if (int rc = expert_slice(up, 0, &u0, "moe_ffn_grouped up")) return rc;
+    if (int rc = expert_slice(down, 0, &d0, "moe_ffn_grouped down")) return rc;
+    if (int rc = check_mmq_weight(&g0, "moe_ffn_grouped gate")) return rc;
+    if (int rc = check_mmq_weight(&u0, "moe_ffn_grouped up")) return rc;
+    if (int rc = check_mmq_weight(&d0, "moe_ffn_grouped down")) return rc;
+    if (gate->ggml_type != up->ggml_type || gate->len != up->len)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: gate and up must share a type and shape");
+    if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped: x not 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+
+    // workspace: quantized tokens, gate/up outputs, quantized SiLU·up, down
+    // outputs, routing, grouping and descriptor tables
+    const uint64_t o_xq = 0;
+    const uint64_t o_xds = o_xq + align256((uint64_t)rows * hidden);
+    const uint64_t o_gate = o_xds + align256((uint64_t)rows * (hidden / 32u) * 4u);
+    const uint64_t o_up = o_gate + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_xq2 = o_up + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_xds2 = o_xq2 + align256((uint64_t)P * ffn);
+    const uint64_t o_down = o_xds2 + align256((uint64_t)P * (ffn / 32u) * 4u);
+    const uint64_t o_idx = o_down + align256((uint64_t)P * hidden * 4u);
+    const uint64_t o_w = o_idx + align256((uint64_t)P * 4u);
+    const uint64_t o_pr = o_w + align256((uint64_t)P * 4u);
+    const uint64_t o_ci = o_pr + align256((uint64_t)P * 4u);
+    const uint64_t o_cw = o_ci + align256((uint64_t)P * 4u);
+    const uint64_t o_dgu = o_cw + align256((uint64_t)P * 4u);
+    const uint64_t o_ddn = o_dgu + align256((uint64_t)2u * expert_count * sizeof(MmqDesc));
+    const uint64_t total = o_ddn + align256((uint64_t)expert_count * sizeof(MmqDesc));
+    void* ws;
+    if (int rc = ctx_workspace(c, total, &ws)) return rc;
+    uint8_t* B = static_cast<uint8_t*>(ws);
+    int8_t* xq = reinterpret_cast<int8_t*>(B + o_xq);
+    uint32_t* xds = reinterpret_cast<uint32_t*>(B + o_xds);
+    float* gout = reinterpret_cast<float*>(B + o_gate);
+    float* uout = reinterpret_cast<float*>(B + o_up);
+    int8_t* xq2 = reinterpret_cast<int8_t*>(B + o_xq2);
+    uint32_t* xds2 = reinterpret_cast<uint32_t*>(B + o_xds2);
+    float* dout = reinterpret_cast<float*>(B + o_down);
+    int32_t* d_idx = reinterpret_cast<int32_t*>(B + o_idx);
+    float* d_w = reinterpret_cast<float*>(B + o_w);
+    MmqDesc* d_gu = reinterpret_cast<MmqDesc*>(B + o_dgu);
+    MmqDesc* d_dn = reinterpret_cast<MmqDesc*>(B + o_ddn);
+
+    // 64-row tiles when the experts would average at most 48 rows
+    const bool m64 = P <= 48u * std::min(expert_count, P);
+    const uint32_t bm = m64 ? 64u : kMmqBM;
+    MoePlanArgs pa;
+    std::memset(&pa, 0, sizeof pa);
+    pa.idx = d_idx;
+    pa.wts = d_w;
+    pa.pair_row = reinterpret_cast<int32_t*>(B + o_pr);
+    pa.comb_idx = reinterpret_cast<int32_t*>(B + o_ci);
+    pa.comb_w = reinterpret_cast<float*>(B + o_cw);
+    pa.descs_gu = d_gu;
+    pa.descs_dn = d_dn;
+    auto tmpl = [&](MmqDesc* d, const rfxq_weight* w0, const int8_t* q, const uint32_t* s, float* y, uint32_t n,
+                    uint32_t k) {
+        d->w = static_cast<const uint8_t*>(w0->data);
+        d->xq = q;
+        d->xds = s;
+        d->y = y;
+        d->n = n;
+        d->k = k;
+        d->type = w0->ggml_type;
+        d->ldq = k;
+        d->ldy = n;
+        d->tiles_n = (n + kMmqBN - 1u) / kMmqBN;
+        d->splits = 1;
+        d->sb_per_split = k / 256u;
+    };
+    tmpl(&pa.tg, &g0, xq, xds, gout, ffn, hidden);
+    tmpl(&pa.tu, &u0, xq, xds, uout, ffn, hidden);
+    tmpl(&pa.td, &d0, xq2, xds2, dout, hidden, ffn);
+    pa.w_stride_gu = gate->len / expert_count;
+    pa.w_stride_dn = down->len / expert_count;
+    pa.tokens = rows;
+    pa.k = top_k;
+    pa.E = expert_count;
+    uint32_t p2 = 2;
+    while (p2 < P) p2 <<= 1;
+    pa.P2 = p2;
+    pa.bm = bm;
+    pa.ffn = ffn;
+    pa.hidden = hidden;
+
+    if (int rc = rfxq_moe_route_device(router_logits, rows, expert_count, top_k, normalize, weight_scale, d_idx, d_w,
+                                       stream))
+        return rc;
+    if (int rc = launch(c->moe_plan, 1, 0, stream, &pa, sizeof pa, "rfxq_moe_plan launch", 1024)) return rc;
+    if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
+    // launch grids: upper bounds on the tiles (sum over experts of
+    // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
+    const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
+    if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
+                            2u * tiles_bound * pa.tg.tiles_n, false, stream, false, m64))
+        return rc;
+    if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
+    if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
+    if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
+                            stream, false, m64))
+        return rc;
+    struct {
+        const float* po;
+        const int32_t* idx;
+        const float* w;
+        float* out;
+        uint32_t tokens, k, hidden, pad;
+    } a = {dout, pa.comb_idx, pa.comb_w, out, rows, top_k, hidden, 0};
+    const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
+    if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
     return ok();
 }
 

@@ -25,6 +25,7 @@ __all__ = [
     "gemm", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
     "route_top_k", "route_top_k_with_norm", "quant_expert_weight", "expert_gemv", "expert_gemm",
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
+    "moe_route_device", "moe_ffn_grouped_device",
     "act_q8_1_size", "quantize_act_q8_1", "rmsnorm_q8_1", "silu_and_mul_q8_1", "gemm_q8_1", "gemm_q8_1_batch",
 ]
 
@@ -472,3 +473,24 @@ def moe_ffn_grouped(x: torch.Tensor, rows: int, hidden: int, router_logits: np.n
         _check(lib().rfxq_moe_ffn_grouped(x.data_ptr(), rows, hidden, lg.ctypes.data, expert_count, top_k,
                                           int(normalize), float(weight_scale), gate.cref(), up.cref(), down.cref(),
                                           out.data_ptr(), _stream()))
+
+
+def moe_route_device(logits: torch.Tensor, tokens: int, expert_count: int, top_k: int, normalize: bool,
+                     weight_scale: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """``route_top_k_with_norm`` (moe.rs:47-98) on device logits: (expert ids, weights), [tokens, top_k]."""
+    idx = torch.empty((tokens, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device=logits.device)
+    with _dev(logits):
+        _check(lib().rfxq_moe_route_device(logits.data_ptr(), tokens, expert_count, top_k, int(normalize),
+                                           float(weight_scale), idx.data_ptr(), w.data_ptr(), _stream()))
+    return idx, w
+
+
+def moe_ffn_grouped_device(x: torch.Tensor, rows: int, hidden: int, router_logits: torch.Tensor, expert_count: int,
+                           top_k: int, normalize: bool, weight_scale: float, gate: Weight, up: Weight, down: Weight,
+                           out: torch.Tensor) -> None:
+    """``moe_ffn_grouped`` with routing on the device (logits stay in device memory)."""
+    with _dev(x):
+        _check(lib().rfxq_moe_ffn_grouped_device(x.data_ptr(), rows, hidden, router_logits.data_ptr(), expert_count,
+                                                 top_k, int(normalize), float(weight_scale), gate.cref(), up.cref(),
+                                                 down.cref(), out.data_ptr(), _stream()))

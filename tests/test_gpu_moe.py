@@ -127,3 +127,95 @@ def test_moe_ffn_grouped_back_to_back(rq, orc):
         rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, top_k, True, 1.0, wg, wu, wd, alone)
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), alone.cpu().numpy())
+
+
+# ------------------------------------------------------------------ routing on the device
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_moe_route_device_matches_host(rq, normalize):
+    """route_top_k_with_norm on the device: the same experts in the same
+    order as the host router (moe.rs:47-98) for every token, weights within
+    a few ulp (the softmax sum is reduced in another order); ties go to the
+    lower index."""
+    tokens, experts, k = 512, 128, 8
+    logits = synth.normals(700, tokens * experts).reshape(tokens, experts)
+    logits[0, :] = 0.25                    # all tied: experts 0..k-1
+    logits[1, 5] = logits[1, 9] = 40.0     # a tie at the top
+    idx, w = rq.moe_route_device(_dev(logits), tokens, experts, k, normalize, 0.5)
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(tokens):
+        host = rq.route_top_k_with_norm(logits[t], k, normalize)
+        assert [e for e, _ in host] == idx[t].tolist(), t
+        np.testing.assert_allclose(w[t], np.array([v for _, v in host], np.float32) * 0.5, rtol=1e-6, atol=0)
+    assert idx[0].tolist() == list(range(k)) and idx[1][:2].tolist() == [5, 9]
+
+
+def _moe_device_case(rq, orc, tokens, experts, hidden, ffn, top_k, seed):
+    gate = synth.weights(Q4K, experts * ffn, hidden, seed)
+    up = synth.weights(Q4K, experts * ffn, hidden, seed + 1)
+    down = synth.weights(Q4K, experts * hidden, ffn, seed + 2)
+    x = _dev(synth.activations(tokens * hidden, seed + 3))
+    logits = synth.normals(seed + 4, tokens * experts).reshape(tokens, experts)
+    W = lambda a, i, o: rq.Weight(rq.GgmlType.Q4K, _dev(a), [i, o, experts])  # noqa: E731
+    ws = (W(gate, hidden, ffn), W(up, hidden, ffn), W(down, ffn, hidden))
+    out_d = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped_device(x, tokens, hidden, _dev(logits), experts, top_k, True, 1.0, *ws, out_d)
+    out_h = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, top_k, True, 1.0, *ws, out_h)
+    routes = [orc.route_top_k(logits[t], top_k) for t in range(tokens)]
+    ref = orc.moe_ffn_grouped_reference(x.cpu().numpy().reshape(tokens, hidden), routes, gate, up, down, Q4K,
+                                        hidden, ffn, experts)
+    return (out_d.cpu().numpy().reshape(tokens, hidden), out_h.cpu().numpy().reshape(tokens, hidden), ref, ws, x,
+            logits)
+
+
+@pytest.mark.parametrize("tokens,experts,hidden,ffn,k", [(64, 16, 512, 256, 4), (48, 128, 2048, 768, 8),
+                                                         (300, 8, 512, 512, 2)])
+def test_moe_ffn_grouped_device(rq, orc, tokens, experts, hidden, ffn, k):
+    """Device routing and grouping give the host-routed pipeline's result
+    (same kernels; only last-bit weight differences) and meet its bound
+    against the host reference."""
+    y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, experts, hidden, ffn, k, 800 + tokens)
+    assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
+    assert orc.rel_err_row_l2(y_d, ref) < 3e-3
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_moe_ffn_grouped_device_decode(rq, orc, tokens):
+    """Few tokens take the grouped MMQ path too (64-row tiles)."""
+    y_d, _, ref, _, _, _ = _moe_device_case(rq, orc, tokens, 128, 2048, 768, 8, 900 + tokens)
+    assert orc.rel_err_row_l2(y_d, ref) < 3e-3
+
+
+def test_moe_ffn_grouped_device_in_graph(rq, orc):
+    """No host work per call: the whole device-routed MoE layer replays from
+    a HIP graph, each replay equal to the eager call."""
+    tokens, experts, hidden, ffn, k = 40, 16, 512, 256, 4
+    y_d, _, _, ws, x, logits = _moe_device_case(rq, orc, tokens, experts, hidden, ffn, k, 950)
+    lg = _dev(logits)
+    out = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)  # workspace sized
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(tokens, hidden), y_d)
+        torch.randn(1024, device=DEV).sum().item()
+
+
+def test_moe_ffn_grouped_device_errors(rq):
+    experts, hidden, ffn = 2, 256, 256
+    W = lambda n, i, o: rq.Weight(rq.GgmlType.Q4K, torch.zeros(n, dtype=torch.uint8, device=DEV), [i, o, experts])  # noqa: E731
+    g = W(experts * ffn * hidden // 256 * 144, hidden, ffn)
+    d = W(experts * ffn * hidden // 256 * 144, ffn, hidden)
+    x = torch.zeros(hidden, device=DEV)
+    lg = torch.zeros(experts, device=DEV)
+    with pytest.raises(rq.ReflexError, match="expert_count=2"):
+        rq.moe_ffn_grouped_device(x, 1, hidden, lg, experts, 1, True, 1.0, g, g, d, torch.empty(hidden, device=DEV))
