@@ -743,10 +743,21 @@ struct GemmGroup {
     std::vector<Act> acts;
     std::vector<MmqDesc> descs[3];  // per type_index
     uint32_t wgs[3] = {0, 0, 0};
+    // GEMMs split along K (a type with fewer tiles than two per CU):
+    // partials at workspace offset `off`, reduced into y after the type's launch
+    struct Reduce {
+        uint32_t t, i;
+        uint64_t off;
+        float* y;
+        float* part;  // bound
+        uint64_t n;
+        uint32_t splits;
+    };
+    std::vector<Reduce> reduces;
     uint64_t ws_bytes = 0;
 };
 
-int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g) {
+int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
     // the f16 kernel for the group's GEMMs of one type only if every one of them can take it
     g->f16[0] = g->f16[1] = mmq_f16();
@@ -799,6 +810,49 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         g->wgs[t] += d.tiles_m * d.tiles_n;
         g->descs[t].push_back(d);
     }
+    // a type whose tiles would leave CUs idle splits K (fixed-order reduce)
+    // (REFLEX_QUANT_MMA_SPLITS sets the split count, as for single GEMMs)
+    const uint32_t forced = env_u32("REFLEX_QUANT_MMA_SPLITS", 0);
+    for (uint32_t t = 0; t < 3; t++) {
+        auto& v = g->descs[t];
+        if (v.empty() || (!forced && g->wgs[t] >= 2u * cus)) continue;
+        const uint32_t want = forced ? forced : (2u * cus + g->wgs[t] - 1u) / g->wgs[t];
+        uint32_t wg = 0;
+        for (uint32_t i = 0; i < v.size(); i++) {
+            MmqDesc& d = v[i];
+            const uint32_t nsb = d.k / 256u;
+            const uint32_t s = std::min(want, nsb);
+            d.sb_per_split = (nsb + s - 1u) / s;
+            d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
+            if (d.splits > 1u) {
+                const uint64_t n = (uint64_t)rows * d.n;
+                g->reduces.push_back({t, i, g->ws_bytes, d.y, nullptr, n, d.splits});
+                g->ws_bytes += align256((uint64_t)d.splits * n * 4u);
+            }
+            d.wg_begin = wg;
+            wg += d.tiles_m * d.tiles_n * d.splits;
+        }
+        g->wgs[t] = wg;
+    }
+    return RFXQ_OK;
+}
+
+int launch_reduce(Ctx* c, const float* part, float* y, uint64_t n, uint32_t splits, hipStream_t stream) {
+    struct {
+        const float* ws;
+        float* y;
+        uint64_t n;
+        uint32_t splits, pad;
+    } a = {part, y, n, splits, 0};
+    const uint64_t blocks = std::min<uint64_t>((n + 255u) / 256u, 8192u);
+    return launch(c->reduce, (uint32_t)blocks, 0, stream, &a, sizeof a, "rfxq_splitk_reduce launch");
+}
+
+// the split-K reduces of type t
+int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream) {
+    for (const auto& r : g.reduces)
+        if (r.t == t)
+            if (int rc = launch_reduce(c, r.part, r.y, r.n, r.splits, stream)) return rc;
     return RFXQ_OK;
 }
 
@@ -809,6 +863,10 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
             d.xq = reinterpret_cast<const int8_t*>(ws + reinterpret_cast<uintptr_t>(d.xq));
             d.xds = reinterpret_cast<const uint32_t*>(ws + reinterpret_cast<uintptr_t>(d.xds));
         }
+    for (auto& r : g->reduces) {
+        r.part = reinterpret_cast<float*>(ws + r.off);
+        g->descs[r.t][r.i].y = r.part;
+    }
 }
 
 int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
@@ -1141,7 +1199,7 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
     GemmGroup g;
-    if (int rc = build_gemm_group(items, count, rows, &g)) return rc;
+    if (int rc = build_gemm_group(items, count, rows, &g, (uint32_t)c->cus)) return rc;
     void* ws = nullptr;
     if (int rc = ctx_workspace(c, g.ws_bytes, &ws)) return rc;
     bind_gemm_group(&g, static_cast<uint8_t*>(ws));
@@ -1156,10 +1214,11 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
             for (uint32_t j = 0; j < cnt; j++) {
                 d[j] = v[i0 + j];
                 d[j].wg_begin = wg;
-                wg += d[j].tiles_m * d[j].tiles_n;
+                wg += d[j].tiles_m * d[j].tiles_n * d[j].splits;
             }
             if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16[t])) return rc;
         }
+        if (int rc = run_group_reduces(c, g, t, stream)) return rc;
     }
     return ok();
 }
@@ -1330,7 +1389,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
     auto plan = std::make_unique<rfxq_gemm_plan>();
     plan->device = device;
     plan->rows = rows;
-    if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g);
+    if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g, (uint32_t)c->cus);
     uint64_t tables = 0;
     if (rc == RFXQ_OK) {
         tables = align256(plan->g.acts.size() * sizeof(QuantDesc));
@@ -1396,6 +1455,7 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
         if (int rc = launch_mmq(c, v[0].type, tmp, n, n <= kMmqInline ? nullptr : plan->table[t], plan->g.wgs[t],
                                 false, stream, plan->g.f16[t]))
             return rc;
+        if (int rc = run_group_reduces(c, plan->g, t, stream)) return rc;
     }
     return ok();
 }

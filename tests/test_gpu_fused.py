@@ -76,7 +76,8 @@ def test_gemm_from_activation_buffer(rq, ty, rows, n, k):
     assert torch.equal(rq.gemm_q8_1(act, w, rows), want)
 
 
-def test_gemm_q8_1_batch(rq):
+def test_gemm_q8_1_batch(rq, monkeypatch):
+    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")  # the reference groups unsplit, as the batch
     rows = 200
     shapes = [(Q4K, 768, 1024), (Q6K, 256, 1024), (Q4K, 640, 2048), (Q8_0, 128, 1024)]
     xa, xb = _dev(synth.activations(rows * 1024, 1)), _dev(synth.activations(rows * 2048, 2))
