@@ -28,6 +28,7 @@ extern "C" {
 #define RFXQ_ERR_GGUF 1           /* type without a kernel here (ReflexError::Gguf) */
 #define RFXQ_ERR_GPU 3            /* a HIP call failed (ReflexError::Cuda) */
 #define RFXQ_ERR_OUT_OF_MEMORY 5  /* device allocation failed */
+#define RFXQ_ERR_IO 10            /* file open / map failed (ReflexError::Io) */
 #define RFXQ_ERR_INVALID_INPUT 11 /* bad argument (null pointer, k out of range, ...) */
 #define RFXQ_ERR_OTHER 12         /* shape / alignment precondition (ReflexError::Other) */
 
@@ -268,6 +269,37 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
                                 uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
                                 const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
                                 hipStream_t stream);
+
+/* ---- GGUF files (the on-disk path) ---------------------------------------- */
+
+/* GgufFile (src/gguf.rs:183-334): the file memory-mapped and parsed (magic,
+ * version, metadata with nested arrays, tensor infos, data section at the
+ * `general.alignment` boundary, default 32). Errors: RFXQ_ERR_IO (open /
+ * map), RFXQ_ERR_GGUF (format, with the reference's messages). Tensor data
+ * pointers point into the mapping and live until rfxq_gguf_close. */
+typedef struct rfxq_gguf rfxq_gguf;
+int rfxq_gguf_open(const char* path, rfxq_gguf** out);
+void rfxq_gguf_close(rfxq_gguf* file);
+uint32_t rfxq_gguf_version(const rfxq_gguf* file);
+uint64_t rfxq_gguf_tensor_count(const rfxq_gguf* file);
+/* tensor_info (gguf.rs:281): the first tensor of that name */
+int rfxq_gguf_find_tensor(const rfxq_gguf* file, const char* name, uint64_t* index);
+/* dims: 4 entries, unused ones 1 */
+int rfxq_gguf_tensor_info(const rfxq_gguf* file, uint64_t index, const char** name, uint32_t* n_dims,
+                          uint64_t* dims, uint32_t* ggml_type, uint64_t* offset);
+/* tensor_bytes (gguf.rs:310-334): the tensor's bytes in the mapping */
+int rfxq_gguf_tensor_data(const rfxq_gguf* file, uint64_t index, const void** data, uint64_t* bytes);
+int rfxq_gguf_meta_u64(const rfxq_gguf* file, const char* key, uint64_t* out);
+int rfxq_gguf_meta_f64(const rfxq_gguf* file, const char* key, double* out);
+int rfxq_gguf_meta_str(const rfxq_gguf* file, const char* key, const char** out);
+int rfxq_gguf_meta_array_len(const rfxq_gguf* file, const char* key, uint64_t* out);
+/* QuantArena (src/model/loading.rs:266-317): bytes of one device allocation
+ * holding the listed tensors at 256-byte aligned offsets (0 on a bad index
+ * or range), and the upload into it; weights[j] describes tensor j as the
+ * kernels take it (GGUF shape [in, out(, experts)], raw blocks). */
+uint64_t rfxq_gguf_arena_size(const rfxq_gguf* file, const uint64_t* indices, uint32_t count);
+int rfxq_gguf_upload(const rfxq_gguf* file, const uint64_t* indices, uint32_t count, void* arena,
+                     uint64_t arena_bytes, rfxq_weight* weights, hipStream_t stream);
 
 #ifdef __cplusplus
 }

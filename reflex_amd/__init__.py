@@ -67,6 +67,19 @@ SIGNATURES = {
     "rfxq_silu_and_mul": (_I, [_P, _P, _P, _U64, _P]),
     "rfxq_moe_ffn_grouped": (_I, [_P, _U32, _U32, _P, _U32, _U32, _I, ctypes.c_float, _WP, _WP, _WP, _P, _P]),
     "rfxq_act_q8_1_size": (_U64, [_U32, _U32]),
+    "rfxq_gguf_open": (_I, [ctypes.c_char_p, _P]),
+    "rfxq_gguf_close": (None, [_P]),
+    "rfxq_gguf_version": (_U32, [_P]),
+    "rfxq_gguf_tensor_count": (_U64, [_P]),
+    "rfxq_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, _P]),
+    "rfxq_gguf_tensor_info": (_I, [_P, _U64, _P, _P, _P, _P, _P]),
+    "rfxq_gguf_tensor_data": (_I, [_P, _U64, _P, _P]),
+    "rfxq_gguf_meta_u64": (_I, [_P, ctypes.c_char_p, _P]),
+    "rfxq_gguf_meta_f64": (_I, [_P, ctypes.c_char_p, _P]),
+    "rfxq_gguf_meta_str": (_I, [_P, ctypes.c_char_p, _P]),
+    "rfxq_gguf_meta_array_len": (_I, [_P, ctypes.c_char_p, _P]),
+    "rfxq_gguf_arena_size": (_U64, [_P, _P, _U32]),
+    "rfxq_gguf_upload": (_I, [_P, _P, _U32, _P, _U64, _P, _P]),
     "rfxq_moe_route_device": (_I, [_P, _U32, _U32, _U32, _I, ctypes.c_float, _P, _P, _P]),
     "rfxq_moe_ffn_grouped_device": (_I, [_P, _U32, _U32, _P, _U32, _U32, _I, ctypes.c_float, _WP, _WP, _WP, _P,
                                          _P]),

@@ -24,6 +24,15 @@
 #include <string>
 #include <vector>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <cerrno>
+
+#include "gguf.hpp"
+
+
 extern "C" const unsigned char rfxq_code_object[];
 extern "C" const unsigned char rfxq_code_object_end[];
 
@@ -294,7 +303,13 @@ bool block_dims(uint32_t ty, uint32_t* qk, uint32_t* bb) {
         case RFXQ_TYPE_Q8_1: *qk = 32; *bb = 36; return true;
         case RFXQ_TYPE_Q4_K: *qk = 256; *bb = 144; return true;
         case RFXQ_TYPE_Q6_K: *qk = 256; *bb = 210; return true;
-        default: return false;
+        default: {
+            uint64_t q, b;  // every other type of the GGUF block table
+            if (!gguf::block_dims(ty, &q, &b)) return false;
+            *qk = (uint32_t)q;
+            *bb = (uint32_t)b;
+            return true;
+        }
     }
 }
 
@@ -1978,6 +1993,177 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     } a = {dout, pa.comb_idx, pa.comb_w, out, rows, top_k, hidden, 0};
     const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * hidden + 255u) / 256u, 16384u);
     if (int rc = launch(c->combine, (uint32_t)blocks, 0, stream, &a, sizeof a, "moe_combine launch")) return rc;
+    return ok();
+}
+
+// ---------------------------------------------------------------- GGUF files
+
+struct rfxq_gguf {
+    int fd = -1;
+    void* map = nullptr;
+    size_t len = 0;
+    gguf::File f;
+};
+
+int rfxq_gguf_open(const char* path, rfxq_gguf** out) {
+    if (!path || !out) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_open: NULL argument");
+    *out = nullptr;
+    const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(RFXQ_ERR_IO, "opening GGUF file: %s", std::strerror(errno));
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+        const int e = errno;
+        ::close(fd);
+        return fail(RFXQ_ERR_IO, "stat GGUF file: %s", std::strerror(e));
+    }
+    auto g = std::make_unique<rfxq_gguf>();
+    g->fd = fd;
+    g->len = (size_t)st.st_size;
+    if (g->len) {
+        g->map = mmap(nullptr, g->len, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (g->map == MAP_FAILED) {
+            const int e = errno;
+            ::close(fd);
+            return fail(RFXQ_ERR_IO, "mmap GGUF file: %s", std::strerror(e));
+        }
+    }
+    g->f.data = static_cast<const uint8_t*>(g->map);
+    g->f.len = g->len;
+    std::string err;
+    if (!g->f.parse(&err)) {
+        if (g->map) munmap(g->map, g->len);
+        ::close(fd);
+        return fail(RFXQ_ERR_GGUF, "%s", err.c_str());
+    }
+    *out = g.release();
+    return ok();
+}
+
+void rfxq_gguf_close(rfxq_gguf* g) {
+    if (!g) return;
+    if (g->map) munmap(g->map, g->len);
+    if (g->fd >= 0) ::close(g->fd);
+    delete g;
+}
+
+uint32_t rfxq_gguf_version(const rfxq_gguf* g) { return g ? g->f.version : 0u; }
+
+uint64_t rfxq_gguf_tensor_count(const rfxq_gguf* g) { return g ? g->f.tensors.size() : 0u; }
+
+int rfxq_gguf_find_tensor(const rfxq_gguf* g, const char* name, uint64_t* index) {
+    if (!g || !name || !index) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_find_tensor: NULL argument");
+    auto it = g->f.by_name.find(name);
+    if (it == g->f.by_name.end()) return fail(RFXQ_ERR_GGUF, "tensor '%s' not found in GGUF file", name);
+    *index = it->second;
+    return ok();
+}
+
+int rfxq_gguf_tensor_info(const rfxq_gguf* g, uint64_t index, const char** name, uint32_t* n_dims, uint64_t* dims,
+                          uint32_t* ggml_type, uint64_t* offset) {
+    if (!g) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_tensor_info: NULL file");
+    if (index >= g->f.tensors.size())
+        return fail(RFXQ_ERR_INVALID_INPUT, "gguf_tensor_info: index %llu of %zu", (unsigned long long)index,
+                    g->f.tensors.size());
+    const gguf::Tensor& t = g->f.tensors[index];
+    if (name) *name = t.name.c_str();
+    if (n_dims) *n_dims = (uint32_t)t.dims.size();
+    if (dims)
+        for (size_t j = 0; j < 4; j++) dims[j] = j < t.dims.size() ? t.dims[j] : 1u;
+    if (ggml_type) *ggml_type = t.type;
+    if (offset) *offset = t.offset;
+    return ok();
+}
+
+int rfxq_gguf_tensor_data(const rfxq_gguf* g, uint64_t index, const void** data, uint64_t* bytes) {
+    if (!g || !data || !bytes) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_tensor_data: NULL argument");
+    if (index >= g->f.tensors.size()) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_tensor_data: bad index");
+    uint64_t start, nb;
+    std::string err;
+    if (!g->f.range(g->f.tensors[index], &start, &nb, &err)) return fail(RFXQ_ERR_GGUF, "%s", err.c_str());
+    *data = g->f.data + start;
+    *bytes = nb;
+    return ok();
+}
+
+const gguf::Value* gguf_meta(const rfxq_gguf* g, const char* key) {
+    if (!g || !key) return nullptr;
+    auto it = g->f.meta.find(key);
+    return it == g->f.meta.end() ? nullptr : &it->second;
+}
+
+int rfxq_gguf_meta_u64(const rfxq_gguf* g, const char* key, uint64_t* out) {
+    const gguf::Value* v = gguf_meta(g, key);
+    if (!v || !out || !v->as_u64(out))
+        return fail(RFXQ_ERR_GGUF, "GGUF metadata '%s' missing or not an unsigned integer", key ? key : "");
+    return ok();
+}
+
+int rfxq_gguf_meta_f64(const rfxq_gguf* g, const char* key, double* out) {
+    const gguf::Value* v = gguf_meta(g, key);
+    if (!v || !out || v->kind != gguf::Value::FLOAT)
+        return fail(RFXQ_ERR_GGUF, "GGUF metadata '%s' missing or not a float", key ? key : "");
+    *out = v->f;
+    return ok();
+}
+
+int rfxq_gguf_meta_str(const rfxq_gguf* g, const char* key, const char** out) {
+    const gguf::Value* v = gguf_meta(g, key);
+    if (!v || !out || v->kind != gguf::Value::STR)
+        return fail(RFXQ_ERR_GGUF, "GGUF metadata '%s' missing or not a string", key ? key : "");
+    *out = v->s.c_str();
+    return ok();
+}
+
+int rfxq_gguf_meta_array_len(const rfxq_gguf* g, const char* key, uint64_t* out) {
+    const gguf::Value* v = gguf_meta(g, key);
+    if (!v || !out || v->kind != gguf::Value::ARRAY)
+        return fail(RFXQ_ERR_GGUF, "GGUF metadata '%s' missing or not an array", key ? key : "");
+    *out = v->arr.size();
+    return ok();
+}
+
+// QuantArena::for_tensors (src/model/loading.rs:266-296): every tensor at a
+// 256-byte aligned offset of one allocation
+uint64_t rfxq_gguf_arena_size(const rfxq_gguf* g, const uint64_t* indices, uint32_t count) {
+    if (!g || (!indices && count)) return 0;
+    uint64_t total = 0;
+    for (uint32_t j = 0; j < count; j++) {
+        uint64_t start, nb;
+        std::string err;
+        if (indices[j] >= g->f.tensors.size() || !g->f.range(g->f.tensors[indices[j]], &start, &nb, &err)) return 0;
+        total += align256(nb);
+    }
+    return total;
+}
+
+int rfxq_gguf_upload(const rfxq_gguf* g, const uint64_t* indices, uint32_t count, void* arena, uint64_t arena_bytes,
+                     rfxq_weight* weights, hipStream_t stream) {
+    if (!g || !arena || !weights || (!indices && count))
+        return fail(RFXQ_ERR_INVALID_INPUT, "gguf_upload: NULL argument");
+    if (reinterpret_cast<uintptr_t>(arena) % 256u)
+        return fail(RFXQ_ERR_OTHER, "gguf_upload: arena is not 256-byte aligned");
+    uint64_t used = 0;
+    for (uint32_t j = 0; j < count; j++) {
+        if (indices[j] >= g->f.tensors.size()) return fail(RFXQ_ERR_INVALID_INPUT, "gguf_upload: bad index");
+        const gguf::Tensor& t = g->f.tensors[indices[j]];
+        uint64_t start, nb;
+        std::string err;
+        if (!g->f.range(t, &start, &nb, &err)) return fail(RFXQ_ERR_GGUF, "%s", err.c_str());
+        const uint64_t end = used + align256(nb);
+        if (end > arena_bytes)
+            return fail(RFXQ_ERR_OTHER, "quantized weight arena overflow: need %llu bytes, have %llu",
+                        (unsigned long long)end, (unsigned long long)arena_bytes);
+        uint8_t* dst = static_cast<uint8_t*>(arena) + used;
+        HIPCHK(hipMemcpyAsync(dst, g->f.data + start, nb, hipMemcpyHostToDevice, stream), "gguf_upload copy");
+        rfxq_weight& w = weights[j];
+        w.ggml_type = t.type;
+        w.in_features = t.dims.empty() ? 1u : (uint32_t)t.dims[0];
+        w.out_features = t.dims.size() > 1 ? (uint32_t)t.dims[1] : 1u;
+        w.expert_count = t.dims.size() > 2 ? (uint32_t)t.dims[2] : 0u;
+        w.data = dst;
+        w.len = nb;
+        used = end;
+    }
     return ok();
 }
 

@@ -18,7 +18,7 @@ import torch
 from . import RfxqGemvItem, RfxqWeight, lib
 
 __all__ = [
-    "ReflexError", "GgmlError", "GpuError", "OutOfMemoryError", "InvalidInputError",
+    "ReflexError", "GgmlError", "GpuError", "OutOfMemoryError", "InvalidInputError", "IoError", "GgufFile",
     "GgmlType", "ggml_type_block_dims", "Weight", "QuantArena",
     "dequantize", "gemv", "gemv_to", "gemv_q4k", "gemv_q6k", "gemv_q8_0", "gemv_batch", "GemvPlan",
     "gemv_gather",
@@ -56,7 +56,11 @@ class InvalidInputError(ReflexError):  # ReflexError::InvalidInput
     pass
 
 
-_ERR = {1: GgmlError, 3: GpuError, 5: OutOfMemoryError, 11: InvalidInputError}
+class IoError(ReflexError):           # ReflexError::Io
+    pass
+
+
+_ERR = {1: GgmlError, 3: GpuError, 5: OutOfMemoryError, 10: IoError, 11: InvalidInputError}
 
 
 def _check(rc: int) -> None:
@@ -494,3 +498,92 @@ def moe_ffn_grouped_device(x: torch.Tensor, rows: int, hidden: int, router_logit
         _check(lib().rfxq_moe_ffn_grouped_device(x.data_ptr(), rows, hidden, router_logits.data_ptr(), expert_count,
                                                  top_k, int(normalize), float(weight_scale), gate.cref(), up.cref(),
                                                  down.cref(), out.data_ptr(), _stream()))
+
+
+# ------------------------------------------------------------------ GGUF files
+
+class GgufFile:
+    """``GgufFile`` (src/gguf.rs:183-334): a memory-mapped, parsed GGUF file."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        self._lib = lib()
+        _check(self._lib.rfxq_gguf_open(str(path).encode(), ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.rfxq_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return int(lib().rfxq_gguf_version(self._h))
+
+    @property
+    def tensor_count(self) -> int:
+        return int(lib().rfxq_gguf_tensor_count(self._h))
+
+    def find(self, name: str) -> int:
+        i = ctypes.c_uint64()
+        _check(lib().rfxq_gguf_find_tensor(self._h, name.encode(), ctypes.byref(i)))
+        return i.value
+
+    def tensor_info(self, index: int) -> dict:
+        name, nd, ty, off = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+        dims = (ctypes.c_uint64 * 4)()
+        _check(lib().rfxq_gguf_tensor_info(self._h, index, ctypes.byref(name), ctypes.byref(nd), dims,
+                                           ctypes.byref(ty), ctypes.byref(off)))
+        return {"name": name.value.decode(), "shape": list(dims[:nd.value]), "ggml_type": ty.value,
+                "offset": off.value}
+
+    def tensor_bytes(self, name_or_index) -> np.ndarray:
+        """The tensor's raw bytes (a copy out of the mapping)."""
+        i = self.find(name_or_index) if isinstance(name_or_index, str) else int(name_or_index)
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _check(lib().rfxq_gguf_tensor_data(self._h, i, ctypes.byref(p), ctypes.byref(n)))
+        return np.frombuffer(ctypes.string_at(p.value, n.value), dtype=np.uint8).copy()
+
+    def meta_u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _check(lib().rfxq_gguf_meta_u64(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def meta_f64(self, key: str) -> float:
+        v = ctypes.c_double()
+        _check(lib().rfxq_gguf_meta_f64(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def meta_str(self, key: str) -> str:
+        v = ctypes.c_char_p()
+        _check(lib().rfxq_gguf_meta_str(self._h, key.encode(), ctypes.byref(v)))
+        return v.value.decode()
+
+    def meta_array_len(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _check(lib().rfxq_gguf_meta_array_len(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def upload(self, names: list[str], device="cuda") -> dict:
+        """QuantArena (loading.rs:266-317): the named tensors in one device
+        allocation at 256-byte aligned offsets; returns name -> Weight."""
+        idx = (ctypes.c_uint64 * len(names))(*[self.find(n) for n in names])
+        size = int(lib().rfxq_gguf_arena_size(self._h, idx, len(names)))
+        if size == 0 and names:
+            raise GgmlError(1, "gguf upload: a tensor's byte range is invalid")
+        arena = torch.empty(max(size, 256), dtype=torch.uint8, device=device)
+        ws = (RfxqWeight * max(len(names), 1))()
+        with _dev(arena):
+            _check(lib().rfxq_gguf_upload(self._h, idx, len(names), arena.data_ptr(), arena.numel(), ws, _stream()))
+        torch.cuda.synchronize(arena.device)  # the copies read the mapping
+        out = {}
+        for j, n in enumerate(names):
+            w = ws[j]
+            shape = [w.in_features, w.out_features] + ([w.expert_count] if w.expert_count else [])
+            ty = GgmlType(w.ggml_type) if w.ggml_type in GgmlType._value2member_map_ else w.ggml_type
+            out[n] = Weight(ty, arena, shape,
+                            offset=w.data - arena.data_ptr(), len=w.len)
+        return out

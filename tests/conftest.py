@@ -31,3 +31,11 @@ def rq():
     assert torch.cuda.is_available(), "GPU test without a GPU"
     reflex_amd.init(0)
     return reflex_amd
+
+
+@pytest.fixture(scope="session")
+def rqh():
+    """The product package for host-only calls (GGUF parsing, routing): no device needed."""
+    import reflex_amd
+
+    return reflex_amd
