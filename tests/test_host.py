@@ -35,8 +35,13 @@ def test_exports_every_header_symbol():
     assert declared == set(rq.SIGNATURES), declared ^ set(rq.SIGNATURES)
 
 
-def test_no_error_initially():
+def test_error_state_resets_on_success():
+    """The thread's last error is cleared by the next successful call."""
     rq = _lib()
+    with pytest.raises(rq.ReflexError):
+        rq.ggml_type_block_dims(99)
+    assert rq.lib().rfxq_last_error_code() == 1
+    assert rq.ggml_type_block_dims(rq.GgmlType.Q8_0) == (32, 34)
     assert rq.lib().rfxq_last_error_code() == 0
 
 
