@@ -100,10 +100,6 @@ RFXQ_DEV void gemv_x_sums(const uint32_t* lds_x, float* lds_s, uint32_t k, uint3
 // lds_p (the row results, free while staging) carries the waves' maxima.
 RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
                             uint32_t* lds_x, float* lds_s, float* lds_p, uint32_t tid) {
-#ifdef RFXQ_NOSTAGE
-    lds_barrier();
-    return 1.0f;
-#endif
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -118,20 +114,14 @@ RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool presca
         gemv_x_put(lds_x, e, v, prescale_hi, 1.0f);
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-#ifndef RFXQ_GEMV_NORANGE
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
     if ((tid & 63u) == 0u) lds_st32(lds_addr(lds_p) + 4u * (tid >> 6), __builtin_bit_cast(uint32_t, amax));
-#endif
     lds_barrier();
-#ifndef RFXQ_GEMV_NORANGE
     {
         const u4_t m4 = lds_ld128(lds_addr(lds_p));
         amax = fmaxf(fmaxf(as_f32(m4.x), as_f32(m4.y)), fmaxf(as_f32(m4.z), as_f32(m4.w)));
     }
-#else
-    amax = 0.0f;
-#endif
     gemv_x_sums(lds_x, lds_s, k, tid);
     lds_barrier();
     float inv = 1.0f;
@@ -431,15 +421,9 @@ struct Q80 {
 // slot is its own array, so the compiler's wait counting knows which copy a
 // read depends on and waits for exactly that one.
 constexpr uint32_t kSlotBytes = 4096;
-#ifndef RFXQ_KRING
-#define RFXQ_KRING 2
-#endif
-constexpr int kRing = RFXQ_KRING;
+constexpr int kRing = 2;
 __shared__ __attribute__((aligned(16))) uint8_t gemv_ring0[4][kSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t gemv_ring1[4][kSlotBytes];
-#if RFXQ_KRING > 2
-__shared__ __attribute__((aligned(16))) uint8_t gemv_ring2[4][kSlotBytes];
-#endif
 
 // Offset for copies past a wave's last item: beyond any weight buffer's range
 // (the host keeps weights below it), so the copy writes zeros and fetches
@@ -502,11 +486,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
         pc[j] = 16u * (p - r * ppr);
     }
     const uint32_t uo = sub * ppr * 16u + T::unit_off(li);  // this lane's unit in a slot
-#if RFXQ_KRING > 2
-    uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave], gemv_ring2[wave]};
-#else
     uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave]};
-#endif
 
     // next item to copy: pass lu, row iteration lit; S = buffer offset of the
     // item's first row chunk (scalar)
@@ -521,11 +501,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             uint32_t g = lS + prb[j];
             if (!T::ALIGNED) g &= ~3u;
             g += pc[j];
-#ifndef RFXQ_NOLOAD
             dma16_stream(wr, ring[t] + 1024 * j, valid && pv[j] ? g : kPastEnd);
-#else
-            asm volatile("" ::"v"(g));
-#endif
         }
         lS += row_step;
         if (++lit == n_it) {
@@ -566,12 +542,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * NJ) : "memory");
                 const typename T::Raw rr = T::fetch(ring[t], uo + sh, unit);
                 issue(t);  // the slot's reads are done (fetch waits for them): refill it during the math
-#ifndef RFXQ_NOMATH
                 float acc = T::dot(rr, unit, xv, magic);
-#else
-                float acc = 0.f;
-                for (uint32_t i = 0; i < sizeof(rr) / 4; i++) acc += as_f32(reinterpret_cast<const uint32_t*>(&rr)[i] & 0x3FFFFFFFu);
-#endif
                 acc = group_sum<LPR>(acc);
                 const uint32_t row = base0 + sub + cit * stride;
                 if (li == 0u && row < row_end) {
