@@ -1627,25 +1627,22 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     if (bad >= 0)
         return route_top_k(router_logits_host + (uint64_t)bad * expert_count, expert_count, top_k, normalize != 0,
                            ridx.data() + (uint64_t)bad * top_k, rwts.data() + (uint64_t)bad * top_k);
-    // grouping by expert, tokens in order
-    std::vector<std::vector<std::pair<uint32_t, float>>> groups(expert_count);
-    for (uint32_t r = 0; r < rows; r++)
-        for (uint32_t t = 0; t < top_k; t++)
-            groups[ridx[(uint64_t)r * top_k + t]].push_back({r, rwts[(uint64_t)r * top_k + t] * weight_scale});
+    // grouping by expert, tokens in order (a counting sort)
     const uint32_t P = rows * top_k;
+    std::vector<uint32_t> off(expert_count + 1, 0), fill(rows, 0);
+    for (uint32_t q = 0; q < P; q++) off[ridx[q] + 1]++;
+    for (uint32_t e = 0; e < expert_count; e++) off[e + 1] += off[e];
+    std::vector<uint32_t> order(P), cur(off.begin(), off.end() - 1);
+    for (uint32_t q = 0; q < P; q++) order[cur[ridx[q]]++] = q;  // pairs by expert, then token
     std::vector<int32_t> pair_row(P), comb_idx((uint64_t)rows * top_k, -1);
     std::vector<float> comb_w((uint64_t)rows * top_k, 0.0f);
-    std::vector<uint32_t> fill(rows, 0), off(expert_count + 1, 0);
     uint32_t p = 0;
-    for (uint32_t e = 0; e < expert_count; e++) {
-        off[e] = p;
-        for (auto& rw : groups[e]) {
-            pair_row[p] = (int32_t)rw.first;
-            const uint32_t slot = fill[rw.first]++;
-            comb_idx[(uint64_t)rw.first * top_k + slot] = (int32_t)p;
-            comb_w[(uint64_t)rw.first * top_k + slot] = rw.second;
-            p++;
-        }
+    for (; p < P; p++) {
+        const uint32_t q = order[p], r = q / top_k;
+        pair_row[p] = (int32_t)r;
+        const uint32_t slot = fill[r]++;  // the token's pairs in increasing expert order
+        comb_idx[(uint64_t)r * top_k + slot] = (int32_t)p;
+        comb_w[(uint64_t)r * top_k + slot] = rwts[q] * weight_scale;
     }
     off[expert_count] = p;
 
