@@ -234,10 +234,11 @@ def main() -> int:
     if os.path.exists(traffic_file):
         result["roofline"]["traffic"] = json.load(open(traffic_file)).get("bytes_per_launch")
 
+    del plans, copies
     if not args.quick:
+        result["decode_8b"] = decode_8b_leg(rq, synth, torch, np, dev, timed)
         result["prefill"] = prefill_leg(rq, synth, torch, np, dev, timed)
         result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
-    del plans, copies
     torch.cuda.empty_cache()
     if not args.quick and not args.no_cpu:
         result["cpu_baseline"] = cpu_leg(host_w, layer, L, np)
@@ -282,6 +283,33 @@ def traffic_summary(fetch_csv: str, write_csv: str) -> int:
         json.dump(out, fh, indent=1)
     print(json.dumps(out))
     return 0
+
+
+def decode_8b_leg(rq, synth, torch, np, dev, timed):
+    """Config 4 at M=1: one Qwen3-8B layer's seven GEMVs as one fused launch
+    (q/o 4096x4096, k 1024x4096, gate/up 14336x4096 Q4_K; v 1024x4096 and down
+    4096x14336 Q6_K; 138 MB), and the tied LM head 151936x1024 Q6_K (128 MB),
+    each with three rotated weight copies (beyond the 256 MB Infinity Cache)."""
+    out = {}
+    for tag, layer in (("layer", synth.QWEN3_8B_LAYER), ("lm_head", [synth.LM_HEAD])):
+        xs = {k: torch.randn(k, device=dev) for k in {k for *_, k in layer}}
+        plans, keep = [], []
+        for c in range(3):
+            items = []
+            for pi, (_, ty, n, k) in enumerate(layer):
+                w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(4, c, pi)), k, n, device=dev)
+                keep.append(w)
+                items.append((xs[k], w, torch.empty(n, device=dev)))
+            plans.append(rq.GemvPlan(items))
+        nbytes = sum(synth.weight_bytes(ty, n, k) + 4 * (n + k) for _, ty, n, k in layer)
+        ms = timed(lambda i: plans[i % 3].run(), 300, 300)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[tag] = {"us_per_step": round(ms * 1e3, 1), "mb_per_step": round(nbytes / 1e6, 1), "gbs": round(gbs, 1),
+                    "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"decode 8B {tag}: {ms * 1e3:.1f} us/step  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)",
+              file=sys.stderr, flush=True)
+        del plans, keep
+    return out
 
 
 def moe_leg(rq, synth, torch, np, dev, timed):

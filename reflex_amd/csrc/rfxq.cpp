@@ -371,6 +371,8 @@ struct GemvItem {
     bool passes;  // several units per lane: row partials in LDS
 };
 
+void gemv_shape(GemvItem* it, uint32_t k);
+
 int make_gemv_item(const float* x, const rfxq_weight* w, float* y, GemvItem* it) {
     if (int rc = check_weight(w, "gemv")) return rc;
     const uint32_t k = w->in_features, n = w->out_features;
@@ -382,39 +384,65 @@ int make_gemv_item(const float* x, const rfxq_weight* w, float* y, GemvItem* it)
     if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemv: x or y is NULL");
     if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemv: x is not 16-byte aligned");
     if (reinterpret_cast<uintptr_t>(y) % 4u) return fail(RFXQ_ERR_OTHER, "gemv: y is not 4-byte aligned");
-    const uint32_t units = w->ggml_type == RFXQ_TYPE_Q8_0 ? k / 32u : k / 64u;
-    uint32_t lpr_log2 = 0;
-    const uint32_t lpr_max = std::min<uint32_t>(6u, env_u32("RFXQ_GEMV_LPR_LOG2_MAX", 6));
-    while (lpr_log2 < lpr_max && (units % (2u << lpr_log2)) == 0) lpr_log2++;
-    if (lpr_log2 < 2) lpr_log2 = 2;  // >= 4 lanes per row (units is always a multiple of 4 here)
-    if (units % (1u << lpr_log2)) {
+    if (w->ggml_type == RFXQ_TYPE_Q8_0 && (k / 32u) % 4u)
         // Q8_0 with k/32 not a multiple of 4: not supported by the lane mapping
         return fail(RFXQ_ERR_OTHER, "gemv: %s in_features=%u needs k/32 %% 4 == 0", type_name(w->ggml_type), k);
-    }
     std::memset(it, 0, sizeof *it);
     GemvDesc* d = &it->d;
     d->w = w->data;
     d->x = x;
     d->y = y;
-    d->k = k;
     d->n = n;
     d->type = w->ggml_type;
+    gemv_shape(it, k);
+    return RFXQ_OK;
+}
+
+// K, lanes per row (the most units per lane group up to 64 lanes that divide
+// the row's units; at least 4) and the iteration sizes of an item.
+void gemv_shape(GemvItem* it, uint32_t k) {
+    GemvDesc* d = &it->d;
+    const uint32_t units = d->type == RFXQ_TYPE_Q8_0 ? k / 32u : k / 64u;
+    uint32_t lpr_log2 = 0;
+    const uint32_t lpr_max = std::min<uint32_t>(6u, env_u32("RFXQ_GEMV_LPR_LOG2_MAX", 6));
+    while (lpr_log2 < lpr_max && (units % (2u << lpr_log2)) == 0) lpr_log2++;
+    if (lpr_log2 < 2) lpr_log2 = 2;  // >= 4 lanes per row (units is always a multiple of 4 here)
+    d->k = k;
     d->lpr_log2 = lpr_log2;
     it->rows_iter = 256u >> lpr_log2;
-    it->iters = (n + it->rows_iter - 1u) / it->rows_iter;
-    it->iter_bytes = row_bytes(w->ggml_type, k) * it->rows_iter;
+    it->iters = (d->n + it->rows_iter - 1u) / it->rows_iter;
+    it->iter_bytes = row_bytes(d->type, k) * it->rows_iter;
     it->passes = (units >> lpr_log2) > 1u;
-    return RFXQ_OK;
 }
 
 // Workgroups of a launch: about RFXQ_GEMV_WG_KB (default 128) KB of weights
 // each, so the x staging is amortised and each wave's load ring reaches a
 // steady state; launches too small for 2 workgroups per CU at that size use
-// smaller ranges (down to one iteration).
-uint32_t gemv_grid(const Ctx* c, uint64_t total_iters, uint64_t total_bytes) {
+// smaller ranges (down to one iteration). A launch with more workgroups than
+// the chip holds at once (CUs x workgroups per CU, set by the LDS of the
+// widest x) runs as exactly one wave of resident workgroups with larger
+// ranges: ranges are byte-balanced, so any further wave would be partial and
+// leave most CUs idle while it runs (measured on a 139 MB launch: 34.6 us
+// against 44.0 us with 1062 workgroups). Only launches of more than 512 KB
+// per resident workgroup take whole waves of workgroups instead.
+uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) {
+    uint64_t total_iters = 0, total_bytes = 0;
+    uint32_t kmax = 0;
+    for (const auto& it : v) {
+        total_iters += it.iters;
+        total_bytes += it.iters * it.iter_bytes;
+        kmax = std::max(kmax, it.d.k);
+    }
     const uint64_t kb = std::max<uint32_t>(1u, env_u32("RFXQ_GEMV_WG_KB", 128));
     uint64_t g = (total_bytes + kb * 1024u - 1u) / (kb * 1024u);
     g = std::max<uint64_t>(g, 2u * (uint32_t)c->cus);
+    // LDS per workgroup: the 32 KB weight ring, x and its sums, and up to 4 KB of row results
+    const uint32_t occ = std::min<uint32_t>(4u, (160u * 1024u) / (32768u + kmax * 2u + kmax / 4u + 4096u));
+    const uint64_t slots = (uint64_t)std::max(1, c->cus) * std::max(1u, occ);
+    if (g > slots) {
+        const uint64_t waves = (total_bytes + slots * 512u * 1024u - 1u) / (slots * 512u * 1024u);
+        g = slots * std::max<uint64_t>(1u, waves);
+    }
     return (uint32_t)std::max<uint64_t>(1u, std::min<uint64_t>(g, total_iters));
 }
 
@@ -438,12 +466,9 @@ int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_it
 // Up to kGemvInline GEMVs in one launch, descriptors inline; the kernel splits
 // the iterations evenly by count over the grid.
 int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t stream) {
-    uint64_t total = 0, bytes = 0;
-    for (const auto& it : v) {
-        total += it.iters;
-        bytes += it.iters * it.iter_bytes;
-    }
-    const uint32_t grid = gemv_grid(c, total, bytes);
+    uint64_t total = 0;
+    for (const auto& it : v) total += it.iters;
+    const uint32_t grid = gemv_grid(c, v);
     const uint32_t per_wg = (uint32_t)((total + grid - 1u) / grid);  // no range holds more iterations
     std::vector<uint32_t> max_iters(v.size());
     for (size_t i = 0; i < v.size(); i++) max_iters[i] = std::min(per_wg, v[i].iters);
@@ -462,12 +487,7 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 // One launch over any number of GEMVs: descriptors and byte-balanced ranges
 // uploaded (stream-ordered) into the context's table area at byte `at`
 int gemv_launch_table(Ctx* c, const std::vector<GemvItem>& v, uint64_t at, hipStream_t stream) {
-    uint64_t total = 0, bytes = 0;
-    for (const auto& it : v) {
-        total += it.iters;
-        bytes += it.iters * it.iter_bytes;
-    }
-    const uint32_t grid = gemv_grid(c, total, bytes);
+    const uint32_t grid = gemv_grid(c, v);
     std::vector<GemvRange> ranges;
     std::vector<uint32_t> max_iters;
     gemv_split_bytes(v, grid, &ranges, &max_iters);
@@ -1116,12 +1136,7 @@ int rfxq_gemv_plan_create(const rfxq_gemv_item* items, uint32_t count, int devic
     std::vector<GemvRange> ranges;
     std::vector<uint32_t> max_iters;
     if (rc == RFXQ_OK) {
-        uint64_t total = 0, bytes = 0;
-        for (const auto& it : v) {
-            total += it.iters;
-            bytes += it.iters * it.iter_bytes;
-        }
-        plan->grid = gemv_grid(c, total, bytes);
+        plan->grid = gemv_grid(c, v);
         gemv_split_bytes(v, plan->grid, &ranges, &max_iters);
         std::memset(&plan->args, 0, sizeof plan->args);
         plan->args.ndesc = count;
