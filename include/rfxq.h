@@ -257,11 +257,12 @@ int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_
                           int normalize, float weight_scale, int32_t* idx, float* weights, hipStream_t stream);
 
 /* rfxq_moe_ffn_grouped with the router logits in device memory: routing,
- * grouping by expert and the MMQ descriptor tables are built on the device
- * (the reference copies the logits to the host and uploads per-expert row
- * lists, src/model/dense.rs:1539-1546, 1602-1605), so the call adds no host
- * synchronisation and no host-to-device copy. Every token count takes the
- * grouped MMQ path (64-row tiles for short expert groups). Requires
+ * grouping by expert and the GEMV or MMQ descriptor tables are built on the
+ * device (the reference copies the logits to the host and uploads
+ * per-expert row lists, src/model/dense.rs:1539-1546, 1602-1605), so the
+ * call adds no host synchronisation and no host-to-device copy. Up to 4
+ * tokens run every routed pair as GEMVs, as the host-routed path does; more
+ * take the grouped MMQ path (64-row tiles for short expert groups). Requires
  * 4 <= expert_count <= 1024, top_k <= 64 and rows * top_k <= 16384.
  * Routing errors of the host path (non-finite softmax sums) are not
  * reported: such tokens get non-finite outputs. */

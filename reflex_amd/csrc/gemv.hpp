@@ -42,7 +42,7 @@ struct GemvDesc {
 
 #define GEMV_INLINE 4
 struct GemvArgs {
-    const GemvDesc* table;  // ndesc > GEMV_INLINE: the descriptors
+    const GemvDesc* table;  // the descriptors (NULL: the first ndesc <= GEMV_INLINE of inl)
     const uint4* ranges;    // optional: per workgroup {d0, it0, d1, it1}
     uint32_t ndesc, part_floats;
     GemvDesc inl[GEMV_INLINE];
@@ -596,8 +596,8 @@ RFXQ_DEV void gemv_dispatch_lpr(const GemvDesc& d, uint32_t rb, uint32_t re, boo
 // contiguous range of the launch's iterations in descriptor order, [first,
 // last) with first = (d0, it0), last = (d1, it1), crossing descriptors where
 // needed (x is restaged in LDS at each crossing). With an iteration table the
-// ranges are balanced by bytes on the host; without one (at most
-// GEMV_INLINE inline descriptors) by iteration count.
+// ranges are balanced by bytes on the host; without one (inline descriptors,
+// or a table written on the device) by iteration count.
 RFXQ_DEV uint32_t gemv_iters(const GemvDesc& d) {
     const uint32_t rows_iter = 256u >> d.lpr_log2;
     return (d.n + rows_iter - 1u) / rows_iter;
@@ -606,7 +606,7 @@ RFXQ_DEV uint32_t gemv_iters(const GemvDesc& d) {
 // (a pointer into the kernel arguments, so a runtime index is a scalar load
 // rather than a register copy of the whole array)
 RFXQ_DEV const GemvDesc* gemv_desc(const GemvArgs& a, uint32_t i) {
-    return a.ndesc > GEMV_INLINE ? a.table + i : &a.inl[0] + i;
+    return a.table ? a.table + i : &a.inl[0] + i;
 }
 
 // A descriptor read into scalar registers: every field is marked wave-uniform,
@@ -634,16 +634,26 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_gemv(GemvArgs args) {
         d1 = __builtin_amdgcn_readfirstlane(r.z);
         it1 = __builtin_amdgcn_readfirstlane(r.w);
     } else {
-        uint32_t total = 0, cnt[GEMV_INLINE];
-        for (uint32_t i = 0; i < args.ndesc; i++) total += cnt[i] = gemv_iters(args.inl[i]);
+        // no range table: iterations split evenly by count, descriptor
+        // counts read from the descriptors (inline or a table)
+        uint32_t total = 0;
+        for (uint32_t i = 0; i < args.ndesc; i++) total += gemv_iters(*gemv_desc(args, i));
         uint32_t g0 = (uint32_t)(((uint64_t)total * blockIdx.x) / gridDim.x);
         uint32_t g1 = (uint32_t)(((uint64_t)total * (blockIdx.x + 1u)) / gridDim.x);
         d0 = 0;
-        while (d0 + 1u < args.ndesc && g0 >= cnt[d0]) g0 -= cnt[d0++];
+        for (uint32_t c; d0 + 1u < args.ndesc && g0 >= (c = gemv_iters(*gemv_desc(args, d0)));) {
+            g0 -= c;
+            d0++;
+        }
         d1 = 0;
-        while (d1 + 1u < args.ndesc && g1 > cnt[d1]) g1 -= cnt[d1++];
-        it0 = g0;
-        it1 = g1;
+        for (uint32_t c; d1 + 1u < args.ndesc && g1 > (c = gemv_iters(*gemv_desc(args, d1)));) {
+            g1 -= c;
+            d1++;
+        }
+        it0 = __builtin_amdgcn_readfirstlane(g0);
+        it1 = __builtin_amdgcn_readfirstlane(g1);
+        d0 = __builtin_amdgcn_readfirstlane(d0);
+        d1 = __builtin_amdgcn_readfirstlane(d1);
     }
     bool restage = false;
     for (uint32_t di = d0; di <= d1; di++) {

@@ -175,6 +175,12 @@ struct MoePlanArgs {
     uint64_t w_stride_dn;       // ... in down
     uint32_t tokens, k, E, P2;  // P2: power of two >= tokens * k
     uint32_t bm, ffn, hidden, pad;
+    // GEMV form (few tokens; gemv_gu NULL: not written): per sorted pair q,
+    // gemv_gu[2q], [2q+1] = gate, up of its token's row, gemv_dn[q] = down of
+    // the pair's SiLU·up row, from templates whose w, x and y are the bases
+    GemvDesc* gemv_gu;
+    GemvDesc* gemv_dn;
+    GemvDesc vg, vu, vd;
 };
 
 extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) {
@@ -209,6 +215,28 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)a.idx[(uint64_t)t * a.k + j] < e;
         a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
         a.comb_w[(uint64_t)t * a.k + slot] = a.wts[pair];
+        if (a.gemv_gu) {
+            GemvDesc* dg = a.gemv_gu + 2u * q;
+            GemvDesc* du = dg + 1;
+            GemvDesc* dd = a.gemv_dn + q;
+            const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.vg);
+            const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.vu);
+            const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.vd);
+#pragma unroll
+            for (uint32_t i = 0; i < sizeof(GemvDesc) / 4u; i++) {
+                reinterpret_cast<uint32_t*>(dg)[i] = tg[i];
+                reinterpret_cast<uint32_t*>(du)[i] = tu[i];
+                reinterpret_cast<uint32_t*>(dd)[i] = td[i];
+            }
+            dg->w = a.vg.w + (uint64_t)e * a.w_stride_gu;
+            du->w = a.vu.w + (uint64_t)e * a.w_stride_gu;
+            dd->w = a.vd.w + (uint64_t)e * a.w_stride_dn;
+            dg->x = du->x = a.vg.x + (uint64_t)t * a.hidden;
+            dg->y = a.vg.y + (uint64_t)q * a.ffn;
+            du->y = a.vu.y + (uint64_t)q * a.ffn;
+            dd->x = a.vd.x + (uint64_t)q * a.ffn;
+            dd->y = a.vd.y + (uint64_t)q * a.hidden;
+        }
         if (q == 0u || key[q - 1u] / P2 != e) start[e] = q;
         if (q + 1u == P || key[q + 1u] / P2 != e) cnt[e] = q + 1u;  // end, made a count below
     }

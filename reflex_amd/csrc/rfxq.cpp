@@ -1866,8 +1866,29 @@ struct MoePlanArgs {
     uint64_t w_stride_gu, w_stride_dn;
     uint32_t tokens, k, E, P2;
     uint32_t bm, ffn, hidden, pad;
+    GemvDesc* gemv_gu;
+    GemvDesc* gemv_dn;
+    GemvDesc vg, vu, vd;
 };
-static_assert(sizeof(MoePlanArgs) == 392, "MoePlanArgs layout");
+static_assert(sizeof(MoePlanArgs) == 576, "MoePlanArgs layout");
+
+// A GEMV launch over descriptors the device writes (`table`, in the order of
+// `v`, whose shapes they share): workgroups split the iterations by count.
+int gemv_launch_device(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* table, hipStream_t stream) {
+    uint64_t total = 0;
+    for (const auto& it : v) total += it.iters;
+    const uint32_t grid = gemv_grid(c, v);
+    const uint32_t per_wg = (uint32_t)((total + grid - 1u) / grid);
+    std::vector<uint32_t> max_iters(v.size());
+    for (size_t i = 0; i < v.size(); i++) max_iters[i] = std::min(per_wg, v[i].iters);
+    GemvArgs a;
+    std::memset(&a, 0, sizeof a);
+    uint32_t lds;
+    if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
+    a.ndesc = (uint32_t)v.size();
+    a.table = table;
+    return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+}
 
 int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
                                 uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
@@ -1922,7 +1943,11 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     const uint64_t o_cw = o_ci + align256((uint64_t)P * 4u);
     const uint64_t o_dgu = o_cw + align256((uint64_t)P * 4u);
     const uint64_t o_ddn = o_dgu + align256((uint64_t)2u * expert_count * sizeof(MmqDesc));
-    const uint64_t total = o_ddn + align256((uint64_t)expert_count * sizeof(MmqDesc));
+    // few tokens: every routed pair runs as GEMVs (as in the host-routed path)
+    const bool gemv_form = rows <= kMoeGemvRows;
+    const uint64_t o_vgu = o_ddn + align256((uint64_t)expert_count * sizeof(MmqDesc));
+    const uint64_t o_vdn = o_vgu + (gemv_form ? align256((uint64_t)2u * P * sizeof(GemvDesc)) : 0u);
+    const uint64_t total = o_vdn + (gemv_form ? align256((uint64_t)P * sizeof(GemvDesc)) : 0u);
     void* ws;
     if (int rc = ctx_workspace(c, total, &ws)) return rc;
     uint8_t* B = static_cast<uint8_t*>(ws);
@@ -1979,23 +2004,45 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     pa.bm = bm;
     pa.ffn = ffn;
     pa.hidden = hidden;
+    GemvItem ig, iu, id;
+    if (gemv_form) {
+        if (int rc = make_gemv_item(x, &g0, gout, &ig)) return rc;
+        if (int rc = make_gemv_item(x, &u0, uout, &iu)) return rc;
+        if (int rc = make_gemv_item(gout, &d0, dout, &id)) return rc;
+        pa.gemv_gu = reinterpret_cast<GemvDesc*>(B + o_vgu);
+        pa.gemv_dn = reinterpret_cast<GemvDesc*>(B + o_vdn);
+        pa.vg = ig.d;
+        pa.vu = iu.d;
+        pa.vd = id.d;
+    }
 
     if (int rc = rfxq_moe_route_device(router_logits, rows, expert_count, top_k, normalize, weight_scale, d_idx, d_w,
                                        stream))
         return rc;
     if (int rc = launch(c->moe_plan, 1, 0, stream, &pa, sizeof pa, "rfxq_moe_plan launch", 1024)) return rc;
-    if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
-    // launch grids: upper bounds on the tiles (sum over experts of
-    // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
-    const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
-    if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
-                            2u * tiles_bound * pa.tg.tiles_n, false, stream, false, m64))
-        return rc;
-    if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-    if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
-    if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
-                            stream, false, m64))
-        return rc;
+    if (gemv_form) {
+        std::vector<GemvItem> gu, dn(P, id);
+        for (uint32_t q = 0; q < P; q++) {
+            gu.push_back(ig);
+            gu.push_back(iu);
+        }
+        if (int rc = gemv_launch_device(c, gu, pa.gemv_gu, stream)) return rc;
+        if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
+        if (int rc = gemv_launch_device(c, dn, pa.gemv_dn, stream)) return rc;
+    } else {
+        if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
+        // launch grids: upper bounds on the tiles (sum over experts of
+        // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
+        const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
+        if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
+                                2u * tiles_bound * pa.tg.tiles_n, false, stream, false, m64))
+            return rc;
+        if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
+        if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
+        if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
+                                stream, false, m64))
+            return rc;
+    }
     struct {
         const float* po;
         const int32_t* idx;

@@ -180,11 +180,37 @@ def test_moe_ffn_grouped_device(rq, orc, tokens, experts, hidden, ffn, k):
     assert orc.rel_err_row_l2(y_d, ref) < 3e-3
 
 
-@pytest.mark.parametrize("tokens", [1, 4])
-def test_moe_ffn_grouped_device_decode(rq, orc, tokens):
-    """Few tokens take the grouped MMQ path too (64-row tiles)."""
-    y_d, _, ref, _, _, _ = _moe_device_case(rq, orc, tokens, 128, 2048, 768, 8, 900 + tokens)
+@pytest.mark.parametrize("tokens,k", [(1, 8), (4, 8), (1, 1), (2, 1), (5, 8)])
+def test_moe_ffn_grouped_device_decode(rq, orc, tokens, k):
+    """Up to 4 tokens run every routed pair as GEMVs whose descriptors the
+    device plan writes (as the host-routed path does with host-built ones;
+    1-2 pairs exercise the table path of launches with few descriptors);
+    5 tokens take the grouped MMQ path (64-row tiles)."""
+    y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, 128, 2048, 768, k, 900 + tokens + k)
+    assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
     assert orc.rel_err_row_l2(y_d, ref) < 3e-3
+
+
+def test_moe_ffn_grouped_device_decode_in_graph(rq, orc):
+    """The GEMV form of the device-routed layer replays from a HIP graph too."""
+    tokens, experts, hidden, ffn, k = 2, 32, 1024, 512, 4
+    y_d, _, _, ws, x, logits = _moe_device_case(rq, orc, tokens, experts, hidden, ffn, k, 960)
+    lg = _dev(logits)
+    out = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(tokens, hidden), y_d)
+        torch.randn(1024, device=DEV).sum().item()
 
 
 def test_moe_ffn_grouped_device_in_graph(rq, orc):
