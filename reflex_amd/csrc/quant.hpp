@@ -168,32 +168,45 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_rmsnorm_q8_1(const float*
                                                                    uint16_t* __restrict__ xh,
                                                                    uint16_t* __restrict__ xsc,
                                                                    float* __restrict__ y) {
+    // The rows pass through LDS in chunks of kNormChunk floats, double
+    // buffered: waves 1-3 copy chunk c + 1 (coalesced) while lanes 0..nr-1
+    // of wave 0 run the chain of fused multiply-adds over chunk c from LDS
+    // (one lane per row; the order is fixed, so the chain is the bound).
+    constexpr uint32_t kNormChunk = 1024;
+    constexpr uint32_t kRowF4 = kNormChunk / 4u + 1u;  // +1 float4: rows start on different banks
+    __shared__ float4 stage[2][kNormRowsPerWg * kRowF4];
     __shared__ float rinv[kNormRowsPerWg];
     const uint32_t r0 = blockIdx.x * kNormRowsPerWg;
     const uint32_t nr = min(kNormRowsPerWg, rows - r0);
-    if (threadIdx.x < nr) {
-        // one lane per row: the chain of fused multiply-adds is sequential,
-        // the row's loads run kAhead float4s ahead of it
-        constexpr uint32_t kAhead = 8;
-        const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)(r0 + threadIdx.x) * k);
-        const uint32_t n4 = k / 4u;  // a multiple of 64
-        float4 buf[kAhead];
-#pragma unroll
-        for (uint32_t j = 0; j < kAhead; j++) buf[j] = xr[j];
-        float sum_sq = 0.0f;
-        for (uint32_t j0 = 0; j0 < n4; j0 += kAhead) {
-#pragma unroll
-            for (uint32_t j = 0; j < kAhead; j++) {
-                const float4 v = buf[j];
-                buf[j] = xr[j0 + j + kAhead < n4 ? j0 + j + kAhead : 0u];
+    const uint32_t tid = threadIdx.x, nchunks = (k + kNormChunk - 1u) / kNormChunk;
+    auto copy = [&](uint32_t c, uint32_t t0, uint32_t nt) {
+        const uint32_t c0 = c * kNormChunk, len4 = min(kNormChunk, k - c0) / 4u;  // k is a multiple of 256
+        for (uint32_t i = t0; i < nr * len4; i += nt) {
+            const uint32_t r = i / len4, j = i - r * len4;
+            stage[c & 1u][r * kRowF4 + j] = *reinterpret_cast<const float4*>(x + (uint64_t)(r0 + r) * k + c0 + 4u * j);
+        }
+    };
+    copy(0, tid, 256u);
+    __syncthreads();
+    float sum_sq = 0.0f;
+    for (uint32_t c = 0; c < nchunks; c++) {
+        if (tid >= 64u) {
+            if (c + 1u < nchunks) copy(c + 1u, tid - 64u, 192u);
+        } else if (tid < nr) {
+            const float4* sr = &stage[c & 1u][tid * kRowF4];
+            const uint32_t len4 = min(kNormChunk, k - c * kNormChunk) / 4u;
+#pragma unroll 8
+            for (uint32_t j = 0; j < len4; j++) {
+                const float4 v = sr[j];
                 sum_sq = __builtin_fmaf(v.x, v.x, sum_sq);
                 sum_sq = __builtin_fmaf(v.y, v.y, sum_sq);
                 sum_sq = __builtin_fmaf(v.z, v.z, sum_sq);
                 sum_sq = __builtin_fmaf(v.w, v.w, sum_sq);
             }
         }
-        rinv[threadIdx.x] = 1.0f / sqrtf(sum_sq / (float)k + eps);
+        __syncthreads();
     }
+    if (tid < nr) rinv[tid] = 1.0f / sqrtf(sum_sq / (float)k + eps);
     __syncthreads();
     const uint64_t o = (uint64_t)r0 * k, nblk = k / 32u;
     quant_q8_1_rows(QuantSrcRms{x + o, g, rinv, k}, nr, k, xq + o, k, xds + r0 * nblk, xh + o,
