@@ -209,6 +209,24 @@ def test_gemv_batch_table_launch(rq, orc):
         assert np.array_equal(y.cpu().numpy(), ref)
 
 
+def test_gemv_plan_several_waves_of_workgroups(rq):
+    """A plan beyond 512 KB per resident workgroup (9 x 33 MB at K = 14336,
+    two workgroups per CU) runs as whole waves of workgroups; every output
+    equals its single call bit for bit."""
+    n, k = 4096, 14336
+    w_np = synth.weights(Q4K, n, k, 41)
+    buf = _dev(w_np)
+    items, singles = [], []
+    for i in range(9):
+        w = rq.Weight(rq.GgmlType(Q4K), buf, [k, n])
+        x = _dev(synth.activations(k, 60 + i))
+        singles.append(rq.gemv(x, w).cpu().numpy())
+        items.append((x, w, torch.full((n,), float("nan"), device=DEV)))
+    rq.GemvPlan(items).run()
+    for (_, _, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)
+
+
 # ------------------------------------------------------------------ gathered rows
 
 @pytest.mark.parametrize("ty,n,k", [(Q6K, 151936, 1024), (Q4K, 3072, 1024), (Q8_0, 1024, 1024)])
