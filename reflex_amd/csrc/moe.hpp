@@ -82,13 +82,11 @@ constexpr uint32_t kPlanMaxPairs = 16384;  // sort keys in LDS
 // differ from a sequential sum in the last bit), the k best by probability
 // descending then expert index ascending, renormalised by their sum (in
 // selection order) when `normalize`; weights multiplied by `scale`.
-extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __restrict__ logits, uint32_t tokens,
-                                                                uint32_t E, uint32_t k, uint32_t normalize,
-                                                                float scale, int32_t* __restrict__ idx,
-                                                                float* __restrict__ wts) {
+// One wave routes token t (all 64 lanes take part).
+__device__ __forceinline__ void moe_route_token(const float* __restrict__ logits, uint32_t t, uint32_t E,
+                                                uint32_t k, uint32_t normalize, float scale,
+                                                int32_t* __restrict__ idx, float* __restrict__ wts) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (t >= tokens) return;
     const float* l = logits + (uint64_t)t * E;
     constexpr uint32_t J = kRouteMaxE / 64u;
     float p[J];
@@ -152,6 +150,15 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __
     }
 }
 
+extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __restrict__ logits, uint32_t tokens,
+                                                                uint32_t E, uint32_t k, uint32_t normalize,
+                                                                float scale, int32_t* __restrict__ idx,
+                                                                float* __restrict__ wts) {
+    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    moe_route_token(logits, t, E, k, normalize, scale, idx, wts);
+}
+
 // Grouping and descriptor tables, one workgroup of 1024 threads: the pairs
 // (token t, slot j) sorted by (expert, t*k + j) with a bitonic sort of the
 // keys expert*P2 + pair in LDS; then
@@ -181,12 +188,23 @@ struct MoePlanArgs {
     GemvDesc* gemv_gu;
     GemvDesc* gemv_dn;
     GemvDesc vg, vu, vd;
+    // routing in this launch (few tokens; NULL: idx / wts come from
+    // rfxq_moe_route): one wave per token writes idx and wts first
+    const float* logits;
+    uint32_t normalize;
+    float scale;
 };
 
 extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) {
     __shared__ uint32_t key[kPlanMaxPairs];
     __shared__ uint32_t start[kRouteMaxE + 1], cnt[kRouteMaxE];
     const uint32_t tid = threadIdx.x, P = a.tokens * a.k, P2 = a.P2;
+    if (a.logits) {
+        for (uint32_t t = tid >> 6; t < a.tokens; t += 16u)
+            moe_route_token(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
+                            const_cast<float*>(a.wts));
+        __syncthreads();  // (a workgroup barrier orders the global writes for the reads below)
+    }
     for (uint32_t i = tid; i < P2; i += 1024u)
         key[i] = i < P ? (uint32_t)a.idx[i] * P2 + i : 0xFFFFFFFFu;
     for (uint32_t e = tid; e < a.E; e += 1024u) cnt[e] = 0u;

@@ -1869,8 +1869,11 @@ struct MoePlanArgs {
     GemvDesc* gemv_gu;
     GemvDesc* gemv_dn;
     GemvDesc vg, vu, vd;
+    const float* logits;
+    uint32_t normalize;
+    float scale;
 };
-static_assert(sizeof(MoePlanArgs) == 576, "MoePlanArgs layout");
+static_assert(sizeof(MoePlanArgs) == 592, "MoePlanArgs layout");
 
 // A GEMV launch over descriptors the device writes (`table`, in the order of
 // `v`, whose shapes they share): workgroups split the iterations by count.
@@ -2016,9 +2019,14 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         pa.vd = id.d;
     }
 
-    if (int rc = rfxq_moe_route_device(router_logits, rows, expert_count, top_k, normalize, weight_scale, d_idx, d_w,
-                                       stream))
+    if (gemv_form) {  // few tokens: the plan launch routes them too
+        pa.logits = router_logits;
+        pa.normalize = normalize ? 1u : 0u;
+        pa.scale = weight_scale;
+    } else if (int rc = rfxq_moe_route_device(router_logits, rows, expert_count, top_k, normalize, weight_scale,
+                                              d_idx, d_w, stream)) {
         return rc;
+    }
     if (int rc = launch(c->moe_plan, 1, 0, stream, &pa, sizeof pa, "rfxq_moe_plan launch", 1024)) return rc;
     if (gemv_form) {
         std::vector<GemvItem> gu, dn(P, id);
