@@ -209,6 +209,18 @@ def test_gemv_batch_table_launch(rq, orc):
         assert np.array_equal(y.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+def test_gemv_maximum_in_features(rq, orc, ty):
+    """K = 16384 (the largest x staged in LDS) meets the bound; one super-block
+    more is rejected with an error, not run."""
+    n, k = 48, 16384
+    _check_gemv(rq, orc, ty, n, k, orc.synthetic(ty, k, n, 5), orc.activations(k, 6), tol=5e-4)
+    k2 = k + 256
+    w = _weight(rq, ty, orc.synthetic(ty, k2, 4, 7), 4, k2)
+    with pytest.raises(rq.ReflexError, match="exceeds"):
+        rq.gemv(torch.zeros(k2, device=DEV), w)
+
+
 def test_gemv_plan_several_waves_of_workgroups(rq):
     """A plan beyond 512 KB per resident workgroup (9 x 33 MB at K = 14336,
     two workgroups per CU) runs as whole waves of workgroups; every output
