@@ -463,9 +463,11 @@ int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_it
     return RFXQ_OK;
 }
 
-// Up to kGemvInline GEMVs in one launch, descriptors inline; the kernel splits
-// the iterations evenly by count over the grid.
-int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t stream) {
+// One launch whose workgroups split the iterations evenly by count (no
+// range table): over up to kGemvInline descriptors passed inline (`table`
+// NULL), or over a table the device writes (in the order of `v`, whose
+// shapes it shares).
+int gemv_launch_counted(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* table, hipStream_t stream) {
     uint64_t total = 0;
     for (const auto& it : v) total += it.iters;
     const uint32_t grid = gemv_grid(c, v);
@@ -477,8 +479,14 @@ int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t strea
     uint32_t lds;
     if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
     a.ndesc = (uint32_t)v.size();
-    for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
+    a.table = table;
+    if (!table)
+        for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
     return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+}
+
+int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t stream) {
+    return gemv_launch_counted(c, v, nullptr, stream);
 }
 
 void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector<GemvRange>* ranges,
@@ -1875,24 +1883,6 @@ struct MoePlanArgs {
 };
 static_assert(sizeof(MoePlanArgs) == 592, "MoePlanArgs layout");
 
-// A GEMV launch over descriptors the device writes (`table`, in the order of
-// `v`, whose shapes they share): workgroups split the iterations by count.
-int gemv_launch_device(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* table, hipStream_t stream) {
-    uint64_t total = 0;
-    for (const auto& it : v) total += it.iters;
-    const uint32_t grid = gemv_grid(c, v);
-    const uint32_t per_wg = (uint32_t)((total + grid - 1u) / grid);
-    std::vector<uint32_t> max_iters(v.size());
-    for (size_t i = 0; i < v.size(); i++) max_iters[i] = std::min(per_wg, v[i].iters);
-    GemvArgs a;
-    std::memset(&a, 0, sizeof a);
-    uint32_t lds;
-    if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
-    a.ndesc = (uint32_t)v.size();
-    a.table = table;
-    return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
-}
-
 int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
                                 uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
                                 const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
@@ -2034,9 +2024,9 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
             gu.push_back(ig);
             gu.push_back(iu);
         }
-        if (int rc = gemv_launch_device(c, gu, pa.gemv_gu, stream)) return rc;
+        if (int rc = gemv_launch_counted(c, gu, pa.gemv_gu, stream)) return rc;
         if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-        if (int rc = gemv_launch_device(c, dn, pa.gemv_dn, stream)) return rc;
+        if (int rc = gemv_launch_counted(c, dn, pa.gemv_dn, stream)) return rc;
     } else {
         if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
         // launch grids: upper bounds on the tiles (sum over experts of
