@@ -82,10 +82,18 @@ constexpr uint32_t kPlanMaxPairs = 16384;  // sort keys in LDS
 // differ from a sequential sum in the last bit), the k best by probability
 // descending then expert index ascending, renormalised by their sum (in
 // selection order) when `normalize`; weights multiplied by `scale`.
-// One wave routes token t (all 64 lanes take part).
+// Selection by rank rather than k rounds of a wave-wide arg-max (each a
+// chain of cross-lane shuffles): the probabilities go to LDS and every
+// expert counts those that precede it (greater, or equal at a lower index);
+// the experts of rank < k are the selection, in rank order. A NaN
+// probability ranks below every number, so the k indices are always valid
+// experts (such a token's weights are NaN).
+constexpr uint32_t kRouteLds = kRouteMaxE + 128u;  // floats per wave: probabilities, then k (p, e) slots
+// One wave routes token t (all 64 lanes take part); `sp` is the wave's
+// kRouteLds floats of LDS.
 __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits, uint32_t t, uint32_t E,
                                                 uint32_t k, uint32_t normalize, float scale,
-                                                int32_t* __restrict__ idx, float* __restrict__ wts) {
+                                                int32_t* __restrict__ idx, float* __restrict__ wts, float* sp) {
     const uint32_t lane = threadIdx.x & 63u;
     const float* l = logits + (uint64_t)t * E;
     constexpr uint32_t J = kRouteMaxE / 64u;
@@ -108,44 +116,47 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    // ranking values: the probability, NaN as -0.5 (below every probability)
 #pragma unroll
-    for (uint32_t j = 0; j < J; j++) p[j] = lane + 64u * j < E ? p[j] / sum : -1.0f;
-    float top_sum = 0.0f;
-    float sel_p = 0.0f;
-    int32_t sel_e = 0;
-    for (uint32_t s = 0; s < k; s++) {
-        // the lane's best, then the wave's: larger p, on ties the lower index
-        float bp = -2.0f;
-        int32_t be = 0x7FFFFFFF;
-#pragma unroll
-        for (uint32_t j = 0; j < J; j++) {
-            const int32_t e = (int32_t)(lane + 64u * j);
-            if (p[j] > bp) {
-                bp = p[j];
-                be = e;
-            }
-        }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float op = __shfl_xor(bp, m, 64);
-            const int32_t oe = __shfl_xor(be, m, 64);
-            if (op > bp || (op == bp && oe < be)) {
-                bp = op;
-                be = oe;
-            }
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < J; j++)
-            if ((int32_t)(lane + 64u * j) == be) p[j] = -1.0f;
-        top_sum += bp;
-        if (lane == s) {
-            sel_p = bp;
-            sel_e = be;
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane + 64u * j;
+        if (e < E) {
+            p[j] = p[j] / sum;
+            sp[e] = p[j] == p[j] ? p[j] : -0.5f;
+        } else if (e < ((E + 3u) & ~3u)) {
+            sp[e] = -1.0f;  // padding to whole float4s: precedes nothing
         }
     }
+    float* slot_p = sp + kRouteMaxE;
+    int32_t* slot_e = reinterpret_cast<int32_t*>(sp + kRouteMaxE + 64u);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane + 64u * j;
+        if (64u * j < E) {  // wave-uniform
+            const float mine = e < E ? sp[e] : 0.0f;
+            uint32_t r = 0;
+#pragma unroll 8
+            for (uint32_t c = 0; c < E; c += 4u) {
+                const float4 q = *reinterpret_cast<const float4*>(sp + c);
+                r += (q.x > mine || (q.x == mine && c < e)) ? 1u : 0u;
+                r += (q.y > mine || (q.y == mine && c + 1u < e)) ? 1u : 0u;
+                r += (q.z > mine || (q.z == mine && c + 2u < e)) ? 1u : 0u;
+                r += (q.w > mine || (q.w == mine && c + 3u < e)) ? 1u : 0u;
+            }
+            if (e < E && r < k) {
+                slot_p[r] = p[j];
+                slot_e[r] = (int32_t)e;
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float top_sum = 0.0f;  // in selection order
+    for (uint32_t s = 0; s < k; s++) top_sum += slot_p[s];
     if (lane < k) {
+        const float sel_p = slot_p[lane];
         const float wv = normalize ? sel_p / top_sum : sel_p;
-        idx[(uint64_t)t * k + lane] = sel_e;
+        idx[(uint64_t)t * k + lane] = slot_e[lane];
         wts[(uint64_t)t * k + lane] = wv * scale;
     }
 }
@@ -154,9 +165,10 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __
                                                                 uint32_t E, uint32_t k, uint32_t normalize,
                                                                 float scale, int32_t* __restrict__ idx,
                                                                 float* __restrict__ wts) {
+    __shared__ __attribute__((aligned(16))) float sp[4][kRouteLds];
     const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (t >= tokens) return;
-    moe_route_token(logits, t, E, k, normalize, scale, idx, wts);
+    moe_route_token(logits, t, E, k, normalize, scale, idx, wts, sp[threadIdx.x >> 6]);
 }
 
 // Grouping and descriptor tables, one workgroup of 1024 threads: the pairs
@@ -200,9 +212,11 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     __shared__ uint32_t start[kRouteMaxE + 1], cnt[kRouteMaxE];
     const uint32_t tid = threadIdx.x, P = a.tokens * a.k, P2 = a.P2;
     if (a.logits) {
-        for (uint32_t t = tid >> 6; t < a.tokens; t += 16u)
-            moe_route_token(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
-                            const_cast<float*>(a.wts));
+        __shared__ __attribute__((aligned(16))) float sp[4][kRouteLds];
+        if (tid < 256u)
+            for (uint32_t t = tid >> 6; t < a.tokens; t += 4u)
+                moe_route_token(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
+                                const_cast<float*>(a.wts), sp[tid >> 6]);
         __syncthreads();  // (a workgroup barrier orders the global writes for the reads below)
     }
     for (uint32_t i = tid; i < P2; i += 1024u)
@@ -230,6 +244,7 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         const uint32_t t = pair / a.k;
         a.pair_row[q] = (int32_t)t;
         uint32_t slot = 0;
+#pragma unroll 8
         for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)a.idx[(uint64_t)t * a.k + j] < e;
         a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
         a.comb_w[(uint64_t)t * a.k + slot] = a.wts[pair];

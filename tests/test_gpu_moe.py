@@ -150,6 +150,34 @@ def test_moe_route_device_matches_host(rq, normalize):
     assert idx[0].tolist() == list(range(k)) and idx[1][:2].tolist() == [5, 9]
 
 
+@pytest.mark.parametrize("experts,k", [(130, 8), (6, 6), (3, 2), (1024, 64)])
+def test_moe_route_device_shapes(rq, experts, k):
+    """Expert counts off the multiple of 4 and at the limits route as the
+    host does (same experts, same order)."""
+    tokens = 37
+    logits = synth.normals(710 + experts, tokens * experts).reshape(tokens, experts)
+    logits[3, :] = -1.5  # all tied
+    idx, w = rq.moe_route_device(_dev(logits), tokens, experts, k, True, 1.0)
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(tokens):
+        host = rq.route_top_k_with_norm(logits[t], k, True)
+        assert [e for e, _ in host] == idx[t].tolist(), t
+        np.testing.assert_allclose(w[t], np.array([v for _, v in host], np.float32), rtol=1e-6, atol=0)
+
+
+def test_moe_route_device_nan_logits_give_valid_experts(rq):
+    """A token with NaN logits still selects k distinct valid experts (its
+    weights are NaN), so nothing downstream indexes past the expert tensors."""
+    tokens, experts, k = 3, 16, 4
+    logits = synth.normals(720, tokens * experts).reshape(tokens, experts)
+    logits[1, 5] = np.nan
+    idx, w = rq.moe_route_device(_dev(logits), tokens, experts, k, True, 1.0)
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    assert ((idx >= 0) & (idx < experts)).all()
+    assert len(set(idx[1].tolist())) == k and np.isnan(w[1]).all()
+    assert np.isfinite(w[[0, 2]]).all()
+
+
 def _moe_device_case(rq, orc, tokens, experts, hidden, ffn, top_k, seed):
     gate = synth.weights(Q4K, experts * ffn, hidden, seed)
     up = synth.weights(Q4K, experts * ffn, hidden, seed + 1)
