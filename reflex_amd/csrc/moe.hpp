@@ -219,24 +219,56 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
                                 const_cast<float*>(a.wts), sp[tid >> 6]);
         __syncthreads();  // (a workgroup barrier orders the global writes for the reads below)
     }
-    for (uint32_t i = tid; i < P2; i += 1024u)
-        key[i] = i < P ? (uint32_t)a.idx[i] * P2 + i : 0xFFFFFFFFu;
-    for (uint32_t e = tid; e < a.E; e += 1024u) cnt[e] = 0u;
+    // Stable counting sort of the pairs by expert into key[0, P) (values
+    // expert * P2 + pair): a histogram, its exclusive scan (base), then the
+    // pairs in chunks of 1024, one per thread: a lane's rank among the
+    // lanes of its wave with the same expert comes from ballots over the
+    // expert's bits, the waves before it from per-wave counts in LDS.
+    __shared__ uint32_t base[kRouteMaxE];
+    __shared__ uint16_t wcnt[16][kRouteMaxE];
+    const uint32_t E = a.E, lane = tid & 63u, wave = tid >> 6;
+    for (uint32_t e = tid; e < E; e += 1024u) {
+        cnt[e] = 0u;
+        base[e] = 0u;
+    }
     __syncthreads();
-    for (uint32_t size = 2; size <= P2; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = tid; i < P2 / 2u; i += 1024u) {
-                const uint32_t lo = 2u * i - (i & (stride - 1u));
-                const uint32_t hi = lo + stride;
-                const bool up = (lo & size) == 0u;
-                const uint32_t x = key[lo], y = key[hi];
-                if ((x > y) == up) {
-                    key[lo] = y;
-                    key[hi] = x;
-                }
-            }
-            __syncthreads();
+    for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[min((uint32_t)a.idx[i], E - 1u)], 1u);
+    __syncthreads();
+    const uint32_t hist = tid < E ? base[tid] : 0u;
+    for (uint32_t off = 1; off < E; off <<= 1) {
+        const uint32_t o = (tid < E && tid >= off) ? base[tid - off] : 0u;
+        __syncthreads();
+        if (tid < E) base[tid] += o;
+        __syncthreads();
+    }
+    if (tid < E) base[tid] -= hist;  // inclusive -> exclusive
+    for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
+        for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
+        __syncthreads();
+        const uint32_t i = c0 + tid;
+        const bool valid = i < P;
+        const uint32_t e = valid ? min((uint32_t)a.idx[i], E - 1u) : 0u;
+        uint64_t same = __ballot(valid);
+#pragma unroll
+        for (uint32_t bit = 0; bit < 10u; bit++) {  // E <= 1024
+            const uint64_t ones = __ballot((e >> bit) & 1u);
+            same &= ((e >> bit) & 1u) ? ones : ~ones;
         }
+        const uint32_t rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+        if (valid && rank == 0u) wcnt[wave][e] = (uint16_t)__popcll(same);
+        __syncthreads();
+        if (valid) {
+            uint32_t pos = base[e] + rank;
+            for (uint32_t w = 0; w < wave; w++) pos += wcnt[w][e];
+            key[pos] = e * P2 + i;
+        }
+        __syncthreads();
+        if (tid < E) {
+            uint32_t n = 0;
+            for (uint32_t w = 0; w < 16u; w++) n += wcnt[w][tid];
+            base[tid] += n;
+        }
+        __syncthreads();  // (the next chunk clears wcnt)
     }
     // per sorted position: gather row, combine slot, expert bounds
     for (uint32_t q = tid; q < P; q += 1024u) {
