@@ -135,14 +135,28 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
         const uint32_t e = lane + 64u * j;
         if (64u * j < E) {  // wave-uniform
             const float mine = e < E ? sp[e] : 0.0f;
+            // experts below this chunk precede on >=, above it on >, and
+            // within it on > or (== at a lower index)
+            const uint32_t lo = 64u * j, hi = min(64u * j + 64u, (E + 3u) & ~3u), end = (E + 3u) & ~3u;
             uint32_t r = 0;
 #pragma unroll 8
-            for (uint32_t c = 0; c < E; c += 4u) {
+            for (uint32_t c = 0; c < lo; c += 4u) {
+                const float4 q = *reinterpret_cast<const float4*>(sp + c);
+                r += (uint32_t)(q.x >= mine) + (uint32_t)(q.y >= mine) + (uint32_t)(q.z >= mine) +
+                     (uint32_t)(q.w >= mine);
+            }
+            for (uint32_t c = lo; c < hi; c += 4u) {
                 const float4 q = *reinterpret_cast<const float4*>(sp + c);
                 r += (q.x > mine || (q.x == mine && c < e)) ? 1u : 0u;
                 r += (q.y > mine || (q.y == mine && c + 1u < e)) ? 1u : 0u;
                 r += (q.z > mine || (q.z == mine && c + 2u < e)) ? 1u : 0u;
                 r += (q.w > mine || (q.w == mine && c + 3u < e)) ? 1u : 0u;
+            }
+#pragma unroll 8
+            for (uint32_t c = hi; c < end; c += 4u) {
+                const float4 q = *reinterpret_cast<const float4*>(sp + c);
+                r += (uint32_t)(q.x > mine) + (uint32_t)(q.y > mine) + (uint32_t)(q.z > mine) +
+                     (uint32_t)(q.w > mine);
             }
             if (e < E && r < k) {
                 slot_p[r] = p[j];
