@@ -145,6 +145,7 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
                 r += (uint32_t)(q.x >= mine) + (uint32_t)(q.y >= mine) + (uint32_t)(q.z >= mine) +
                      (uint32_t)(q.w >= mine);
             }
+#pragma unroll 4
             for (uint32_t c = lo; c < hi; c += 4u) {
                 const float4 q = *reinterpret_cast<const float4*>(sp + c);
                 r += (q.x > mine || (q.x == mine && c < e)) ? 1u : 0u;
