@@ -289,3 +289,78 @@ def rel_err_row_l2(y: np.ndarray, ref: np.ndarray) -> float:
     num = np.max(np.abs(y2 - r2), axis=1)
     den = np.maximum(np.linalg.norm(r2, axis=1), 1e-30)
     return float(np.max(num / den))
+
+
+# ---------------------------------------------------------------- f16 activation format
+#
+# The prefill GEMM's activation input (no reference counterpart beyond the f16
+# cast of src/kernels_cuda/convert.cu:91, which saturates at 65504 instead of
+# scaling): per row, e = ilogb(max|x|) - 8 clamped to [-120, 120] (0 for an
+# all-zero or non-finite max), xh = f16_rne(x * 2^-e) stored with each group of
+# four as (x0, x2, x1, x3), block sums of the 32 f16 values per 32-block in a
+# fixed f32 order (lane partials ((h0+h1)+h2)+h3 over 8 lanes, then
+# ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))) split into f16 hi and lo, and the row
+# scale 2^e.
+
+def act_f16(x: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Returns (xh u16 [rows, k] in the stored order, xsx u16 [rows, k/256, 16], xrs f32 [rows])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    mx = np.max(np.abs(x), axis=1) if k else np.zeros(rows, np.float32)
+    ok = (mx > 0) & np.isfinite(mx)
+    ex = np.frexp(np.where(ok, mx, 1.0).astype(np.float64))[1] - 1   # ilogb
+    e = np.where(ok, np.clip(ex - 8, -120, 120), 0).astype(np.int64)
+    scale = np.ldexp(np.float32(1.0), -e).astype(np.float32)
+    h = (x * scale[:, None]).astype(np.float32).astype(np.float16)
+    xh = h.reshape(rows, k // 4, 4)[:, :, [0, 2, 1, 3]].reshape(rows, k)
+    hf = h.astype(np.float32).reshape(rows, k // 32, 8, 4)
+    p = ((hf[..., 0] + hf[..., 1]) + hf[..., 2]) + hf[..., 3]           # [rows, blocks, 8] f32
+    u = (p[..., 0] + p[..., 1]) + (p[..., 2] + p[..., 3])
+    v = (p[..., 4] + p[..., 5]) + (p[..., 6] + p[..., 7])
+    s = (u + v).astype(np.float32)
+    hi = s.astype(np.float16)
+    lo = (s - hi.astype(np.float32)).astype(np.float16)
+    xsx = np.concatenate([hi.reshape(rows, k // 256, 8), lo.reshape(rows, k // 256, 8)], axis=2)
+    xrs = np.ldexp(np.float32(1.0), e).astype(np.float32)
+    return xh.view(np.uint16), xsx.view(np.uint16), xrs
+
+
+def _f16(a: np.ndarray) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float64)
+
+
+def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) -> np.ndarray:
+    """The f16-activation prefill GEMM's arithmetic in exact (f64) arithmetic on
+    its own operands: f16 activations (act_f16) and, for Q4_K, the weight
+    operands f16(16(q-8) * f16(d*sc/16)) plus the constant part
+    f16(8*d*sc - dmin*m) against the f16 hi + lo block sums; for Q6_K the
+    exact weights d*sc*(q-32). Any difference between the kernel and this is
+    the kernel's own f32 accumulation."""
+    x2 = np.ascontiguousarray(x.reshape(-1, k), dtype=np.float32)
+    rows = x2.shape[0]
+    xh, xsx, xrs = act_f16(x2)
+    hv = xh.view(np.float16).reshape(rows, k // 4, 4)[:, :, [0, 2, 1, 3]].reshape(rows, k).astype(np.float64)
+    if ty == Q4K:
+        sc, m = q4k_scale_min_np(w, n, k)
+        b = np.ascontiguousarray(w, dtype=np.uint8).reshape(n, k // 256, 144)
+        dd = np.repeat(b[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32), 8, axis=1)
+        dm = np.repeat(b[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float32), 8, axis=1)
+        scf, mf = sc.astype(np.float32), m.astype(np.float32)
+        s16 = _f16(dd * scf * np.float32(0.0625))                       # f16(d*sc/16)
+        c16 = np.float32(8.0) * dd * scf - dm * mf                        # f32 fma ~ exact here
+        c16 = _f16(c16)
+        qb = b[:, :, 16:144]
+        nib = np.empty((n, k // 256, 256), dtype=np.int64)
+        for g in range(4):
+            nib[:, :, 64 * g:64 * g + 32] = qb[:, :, 32 * g:32 * g + 32] & 15
+            nib[:, :, 64 * g + 32:64 * g + 64] = qb[:, :, 32 * g:32 * g + 32] >> 4
+        wop = _f16(16.0 * (nib.reshape(n, k) - 8) * np.repeat(s16, 32, axis=1))
+        sx = (xsx.view(np.float16)[..., :8].astype(np.float64) + xsx.view(np.float16)[..., 8:].astype(np.float64))
+        y = hv @ wop.T + sx.reshape(rows, -1) @ c16.T
+    elif ty == Q6K:
+        # the Q6_K kernel's operands are exact: sc*(q - 32) split into two
+        # f16-exact parts, d applied per super-block
+        y = hv @ dequant_matrix(ty, w, n, k).astype(np.float64).T
+    else:
+        raise ValueError("mmqh_model_reference: Q4_K and Q6_K only")
+    return (y * xrs[:, None].astype(np.float64)).astype(np.float32)

@@ -8,5 +8,5 @@
 #include "gemv.hpp"
 #include "quant.hpp"
 #include "mmq.hpp"
-#include "mmq2.hpp"
+#include "mmqh.hpp"
 #include "moe.hpp"

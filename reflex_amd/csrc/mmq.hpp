@@ -43,6 +43,7 @@ struct MmqDesc {
     uint32_t ldq, ldy, tiles_m, tiles_n;
     uint32_t splits, sb_per_split, wg_begin, pad;
     int32_t* dots_out;      // [m][n][k/32] for the rfxq_mmq_dots_* test hook
+    const float* xrs;       // f16-activation kernels (mmqh.hpp): [m] row scales 2^e
 };
 
 #define MMQ_INLINE 2

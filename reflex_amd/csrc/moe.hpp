@@ -208,7 +208,7 @@ struct MoePlanArgs {
     uint64_t w_stride_gu;       // bytes between experts in gate / up
     uint64_t w_stride_dn;       // ... in down
     uint32_t tokens, k, E, P2;  // P2: power of two >= tokens * k
-    uint32_t bm, ffn, hidden, pad;
+    uint32_t bm, ffn, hidden, f16;  // f16: descriptors read the f16 activation layout
     // GEMV form (few tokens; gemv_gu NULL: not written): per sorted pair q,
     // gemv_gu[2q], [2q+1] = gate, up of its token's row, gemv_dn[q] = down of
     // the pair's SiLU·up row, from templates whose w, x and y are the bases
@@ -324,7 +324,7 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     // per expert (one thread each): rows, tiles; workgroup offsets by an
     // inclusive scan over the experts (Hillis-Steele in LDS)
     __shared__ uint32_t scan_gu[kRouteMaxE], scan_dn[kRouteMaxE];
-    const uint32_t tn_f = (a.ffn + 127u) / 128u, tn_h = (a.hidden + 127u) / 128u;
+    const uint32_t tn_f = a.tg.tiles_n, tn_h = a.td.tiles_n;  // column tiles of gate / up and of down
     uint32_t m = 0, tm = 0;
     if (tid < a.E) {
         m = cnt[tid] ? cnt[tid] - start[tid] : 0u;
@@ -376,8 +376,15 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         g->tiles_m = u->tiles_m = d->tiles_m = tm;
         g->y = a.tg.y + (uint64_t)st * a.ffn;
         u->y = a.tu.y + (uint64_t)st * a.ffn;
-        d->xq = a.td.xq + (uint64_t)st * a.ffn;
-        d->xds = a.td.xds + (uint64_t)st * (a.ffn / 32u);
+        if (a.f16) {  // xh rows of 2*ffn bytes, xsx records of ffn/256 * 32 bytes, xrs
+            d->xq = a.td.xq + (uint64_t)st * a.ffn * 2u;
+            d->xds = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.td.xds) +
+                                                       (uint64_t)st * (a.ffn / 256u) * 32u);
+            d->xrs = a.td.xrs + st;
+        } else {
+            d->xq = a.td.xq + (uint64_t)st * a.ffn;
+            d->xds = a.td.xds + (uint64_t)st * (a.ffn / 32u);
+        }
         d->y = a.td.y + (uint64_t)st * a.hidden;
         g->wg_begin = wg_gu;
         u->wg_begin = wg_gu + tm * tn_f;

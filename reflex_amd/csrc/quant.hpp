@@ -32,16 +32,10 @@ struct QuantSrcPlain {  // x[src_rows[r] or r][c], row stride ldx
 // Rows [0, rows) of one activation, spread over `nwaves` waves (this one is
 // wave_global); 8 lanes per 32-block. `yout` (optional) receives the values
 // quantized, f32 [rows][k] (the producer's own output).
-// Optional layouts for the f16-MFMA kernels (mmq2.hpp):
-//   xh  [rows][k] f16: the int8 values, each group of four stored (q0, q2), (q1, q3)
-//   xsc [rows][k/256][32] u16: per super-block d[8], then Sx' = d*s*2^-6
-//       split exactly into f16 hi[8] and lo[8] (hi = f16(Sx'), lo = f16(Sx' - hi)),
-//       then d again in the order 0, 2, 1, 3, 4, 6, 5, 7 (dword j of that
-//       copy holds the scales of the two blocks one Q6_K 64-k stage reads)
 template <class Src>
 RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t* __restrict__ xq, uint32_t ldq,
-                              uint32_t* __restrict__ xds, uint16_t* __restrict__ xh, uint16_t* __restrict__ xsc,
-                              float* __restrict__ yout, uint64_t wave_global, uint64_t nwaves) {
+                              uint32_t* __restrict__ xds, float* __restrict__ yout, uint64_t wave_global,
+                              uint64_t nwaves) {
     const uint32_t nblk = k / 32u;
     const uint64_t total = (uint64_t)rows * nblk;
     const uint32_t lane = threadIdx.x & 63u;
@@ -68,46 +62,112 @@ RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t*
         if (valid) {
             const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
                                     ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
-            if (xq) *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
-            if (xh) {
-                const h2_t a = {(half_t)q0, (half_t)q2}, b = {(half_t)q1, (half_t)q3};
-                uint2 hv;
-                hv.x = h2_bits(a);
-                hv.y = h2_bits(b);
-                *reinterpret_cast<uint2*>(xh + (uint64_t)row * k + 32u * blk + 4u * part) = hv;
-            }
+            *reinterpret_cast<uint32_t*>(xq + (uint64_t)row * ldq + 32u * blk + 4u * part) = packed;
             if (part == 0u) {
                 const uint32_t dbits = __builtin_bit_cast(uint16_t, (half_t)d);
                 // round the product to f32 first (no fused single-rounding mixed mad)
                 float sid = sum * id;
                 asm volatile("" : "+v"(sid));
                 const uint32_t sbits = __builtin_bit_cast(uint16_t, (half_t)sid);
-                if (xds) xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
-                if (xsc) {
-                    // Sx * 2^-6 (exact): keeps block sums up to 4e6 inside f16's range
-                    const float sx = f16_bits_to_f32(dbits) * f16_bits_to_f32(sbits) * 0.015625f;
-                    const half_t hi = (half_t)sx;
-                    const half_t lo = (half_t)(sx - (float)hi);
-                    const uint32_t b8 = blk & 7u;
-                    uint16_t* rec = xsc + ((uint64_t)row * (nblk / 8u) + blk / 8u) * 32u;
-                    rec[b8] = (uint16_t)dbits;
-                    rec[8u + b8] = __builtin_bit_cast(uint16_t, hi);
-                    rec[16u + b8] = __builtin_bit_cast(uint16_t, lo);
-                    rec[24u + ((b8 & 4u) | ((b8 & 1u) << 1) | ((b8 >> 1) & 1u))] = (uint16_t)dbits;
-                }
+                xds[(uint64_t)row * nblk + blk] = dbits | (sbits << 16);
             }
         }
     }
+}
+
+// ---------------------------------------------------------------- f16 activations
+//
+// The input stage of the f16-activation prefill kernels (mmqh.hpp): one wave
+// per row. Pass 1 finds max |x| of the row; e = ilogb(max) - 8 (clamped to
+// [-120, 120]; 0 for an all-zero or non-finite maximum) so that the scaled
+// row's largest value lies in [256, 512). Pass 2 writes
+//   xh  [rows][k] f16 = RNE(x * 2^-e), groups of four stored (x0, x2), (x1, x3)
+//   xsx [rows][k/256][16] f16: per 32-block b of the super-block, the sum of
+//       the block's 32 f16 values (f32: lane partials ((h0+h1)+h2)+h3 over 8
+//       lanes, then a butterfly over lane distance 1, 2, 4) as hi[b] = f16(S),
+//       lo[b] = f16(S - hi)
+//   xrs [rows] f32 = 2^e
+// and, optionally, the source values themselves to yout (f32 [rows][k]).
+template <class Src>
+RFXQ_DEV void act_f16_row(const Src& src, uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
+                          uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
+    const uint32_t lane = threadIdx.x & 63u;
+    float mx = 0.0f;
+    for (uint32_t c = 4u * lane; c < k; c += 256u) {
+        const float4 v = src.load(r, c);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) e = min(max(ilogbf(mx) - 8, -120), 120);
+    const float scale = ldexpf(1.0f, -e);
+    const uint64_t ro = (uint64_t)r * k;
+    const uint32_t nsb = k / 256u;
+    for (uint32_t c = 4u * lane; c < k; c += 256u) {
+        const float4 v = src.load(r, c);
+        if (yout) *reinterpret_cast<float4*>(yout + ro + c) = v;
+        const half_t h0 = (half_t)(v.x * scale), h1 = (half_t)(v.y * scale);
+        const half_t h2 = (half_t)(v.z * scale), h3 = (half_t)(v.w * scale);
+        uint2 hv;
+        hv.x = h2_bits(h2_t{h0, h2});
+        hv.y = h2_bits(h2_t{h1, h3});
+        *reinterpret_cast<uint2*>(xh + ro + c) = hv;
+        float s = (((float)h0 + (float)h1) + (float)h2) + (float)h3;
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if ((lane & 7u) == 0u) {
+            const uint32_t blk = c / 32u;
+            const half_t hi = (half_t)s;
+            const half_t lo = (half_t)(s - (float)hi);
+            uint16_t* rec = xsx + ((uint64_t)r * nsb + blk / 8u) * 16u;
+            rec[blk & 7u] = __builtin_bit_cast(uint16_t, hi);
+            rec[8u + (blk & 7u)] = __builtin_bit_cast(uint16_t, lo);
+        }
+    }
+    if (lane == 0u) xrs[r] = ldexpf(1.0f, e);
+}
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16(const float* __restrict__ x, uint32_t ldx,
+                                                              const int32_t* __restrict__ src_rows, uint32_t rows,
+                                                              uint32_t k, uint16_t* __restrict__ xh,
+                                                              uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
+    const QuantSrcPlain src{x, ldx, src_rows};
+    for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4u)
+        act_f16_row(src, r, k, xh, xsx, xrs, nullptr);
+}
+
+// Several activations in one launch (grouped GEMMs): workgroups
+// [wg_begin, wg_begin + wgs) of the grid take activation i.
+struct ActF16Desc {
+    const float* x;
+    uint16_t* xh;
+    uint16_t* xsx;
+    float* xrs;
+    uint32_t rows, k, wg_begin, wgs;
+};
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_multi(const ActF16Desc* __restrict__ table,
+                                                                    uint32_t ndesc) {
+    uint32_t lo = 0, hi = ndesc - 1u;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) >> 1;
+        if (table[mid].wg_begin <= blockIdx.x) lo = mid;
+        else hi = mid - 1u;
+    }
+    const ActF16Desc d = table[lo];
+    const QuantSrcPlain src{d.x, d.k, nullptr};
+    for (uint32_t r = (blockIdx.x - d.wg_begin) * 4u + (threadIdx.x >> 6); r < d.rows; r += d.wgs * 4u)
+        act_f16_row(src, r, d.k, d.xh, d.xsx, d.xrs, nullptr);
 }
 
 extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,
                                                                     const int32_t* __restrict__ src_rows,
                                                                     uint32_t rows, uint32_t k,
                                                                     int8_t* __restrict__ xq, uint32_t ldq,
-                                                                    uint32_t* __restrict__ xds,
-                                                                    uint16_t* __restrict__ xh,
-                                                                    uint16_t* __restrict__ xsc) {
-    quant_q8_1_rows(QuantSrcPlain{x, ldx, src_rows}, rows, k, xq, ldq, xds, xh, xsc, nullptr,
+                                                                    uint32_t* __restrict__ xds) {
+    quant_q8_1_rows(QuantSrcPlain{x, ldx, src_rows}, rows, k, xq, ldq, xds, nullptr,
                     ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
 }
 
@@ -117,8 +177,6 @@ struct QuantDesc {
     const float* x;
     int8_t* xq;
     uint32_t* xds;
-    uint16_t* xh;   // optional f16 copy
-    uint16_t* xsc;  // optional super-block scale records
     uint32_t rows, k, wg_begin, wgs;
 };
 
@@ -132,7 +190,7 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1_multi(const
     }
     const QuantDesc d = table[lo];
     const uint32_t wg = blockIdx.x - d.wg_begin;
-    quant_q8_1_rows(QuantSrcPlain{d.x, d.k, nullptr}, d.rows, d.k, d.xq, d.k, d.xds, d.xh, d.xsc, nullptr,
+    quant_q8_1_rows(QuantSrcPlain{d.x, d.k, nullptr}, d.rows, d.k, d.xq, d.k, d.xds, nullptr,
                     ((uint64_t)wg * blockDim.x + threadIdx.x) >> 6, ((uint64_t)d.wgs * blockDim.x) >> 6);
 }
 
@@ -166,7 +224,8 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_rmsnorm_q8_1(const float*
                                                                    uint32_t k, float eps, int8_t* __restrict__ xq,
                                                                    uint32_t* __restrict__ xds,
                                                                    uint16_t* __restrict__ xh,
-                                                                   uint16_t* __restrict__ xsc,
+                                                                   uint16_t* __restrict__ xsx,
+                                                                   float* __restrict__ xrs,
                                                                    float* __restrict__ y) {
     // The rows pass through LDS in chunks of kNormChunk floats, double
     // buffered: waves 1-3 copy chunk c + 1 (coalesced) while lanes 0..nr-1
@@ -209,8 +268,13 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_rmsnorm_q8_1(const float*
     if (tid < nr) rinv[tid] = 1.0f / sqrtf(sum_sq / (float)k + eps);
     __syncthreads();
     const uint64_t o = (uint64_t)r0 * k, nblk = k / 32u;
-    quant_q8_1_rows(QuantSrcRms{x + o, g, rinv, k}, nr, k, xq + o, k, xds + r0 * nblk, xh + o,
-                    xsc + r0 * (nblk / 8u) * 32u, y ? y + o : nullptr, threadIdx.x >> 6, 4u);
+    const QuantSrcRms src{x + o, g, rinv, k};
+    // int8 layout (8 lanes per 32-block), then the f16 layout (one wave per
+    // row); the producer's own output y is written by the first pass run
+    if (xq) quant_q8_1_rows(src, nr, k, xq + o, k, xds + r0 * nblk, y ? y + o : nullptr, threadIdx.x >> 6, 4u);
+    const uint32_t wv = threadIdx.x >> 6;
+    if (xh && wv < nr)
+        act_f16_row(src, wv, k, xh + o, xsx + r0 * (nblk / 8u) * 16u, xrs + r0, (!xq && y) ? y + o : nullptr);
 }
 
 // SiLU(gate) * up (src/kernels_cuda/silu_and_mul.cu:7-23: g / (1 + expf(-g)) * u)
@@ -233,8 +297,14 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_silu_and_mul_q8_1(const f
                                                                         int8_t* __restrict__ xq,
                                                                         uint32_t* __restrict__ xds,
                                                                         uint16_t* __restrict__ xh,
-                                                                        uint16_t* __restrict__ xsc,
+                                                                        uint16_t* __restrict__ xsx,
+                                                                        float* __restrict__ xrs,
                                                                         float* __restrict__ y) {
-    quant_q8_1_rows(QuantSrcSilu{gate, up, k}, rows, k, xq, k, xds, xh, xsc, y,
-                    ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6, ((uint64_t)gridDim.x * blockDim.x) >> 6);
+    const QuantSrcSilu src{gate, up, k};
+    if (xq)
+        quant_q8_1_rows(src, rows, k, xq, k, xds, y, ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6,
+                        ((uint64_t)gridDim.x * blockDim.x) >> 6);
+    if (xh)
+        for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4u)
+            act_f16_row(src, r, k, xh, xsx, xrs, xq ? nullptr : y);
 }

@@ -98,6 +98,7 @@ struct MmqDesc {
     uint32_t ldq, ldy, tiles_m, tiles_n;
     uint32_t splits, sb_per_split, wg_begin, pad;
     int32_t* dots_out;
+    const float* xrs;
 };
 constexpr uint32_t kMmqInline = 2;
 struct MmqArgs {
@@ -105,7 +106,7 @@ struct MmqArgs {
     uint32_t ndesc, pad;
     MmqDesc inl[kMmqInline];
 };
-static_assert(sizeof(MmqDesc) == 96, "MmqDesc layout");
+static_assert(sizeof(MmqDesc) == 104, "MmqDesc layout");
 
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
@@ -124,7 +125,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmq2_q4k = nullptr, mmq2_q6k = nullptr;
+    hipFunction_t mmqh[2] = {}, act_f16 = nullptr, act_f16_multi = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
@@ -184,8 +185,10 @@ int load_ctx(int device, Ctx** out) {
         {&c->dots[0], "rfxq_mmq_dots_q4k"},
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
-        {&c->mmq2_q4k, "rfxq_mmq2_q4k"},
-        {&c->mmq2_q6k, "rfxq_mmq2_q6k"},
+        {&c->mmqh[0], "rfxq_mmqh_q4k"},
+        {&c->mmqh[1], "rfxq_mmqh_q6k"},
+        {&c->act_f16, "rfxq_act_f16"},
+        {&c->act_f16_multi, "rfxq_act_f16_multi"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
         {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
         {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
@@ -575,19 +578,18 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 
 // ------------------------------------------------------------------ MMQ planning
 
-
-// Q4_K and Q6_K prefill GEMMs run on the f16-MFMA kernels (rfxq_mmq2_q4k,
-// rfxq_mmq2_q6k: exact integer block dots, one FMA per element and block)
-// unless REFLEX_MMQ_F16=0 selects the int8-MFMA kernels. Gathered rows (MoE)
-// always take the int8 kernels.
-constexpr uint32_t kMmq2Threads = 256;  // rfxq_mmq2_* workgroup
+// Q4_K and Q6_K prefill GEMMs run on the f16-activation kernels
+// (rfxq_mmqh_q4k, rfxq_mmqh_q6k: f16 activations scaled per row, weights as f16
+// operands, f32 accumulation in the matrix core) unless REFLEX_MMQ_F16=0
+// selects the int8 MMQ kernels (Q8_1 activations, per-32 int32 block dots).
+// Q8_0 always takes the int8 kernels.
+constexpr uint32_t kMmqThreads = 256;  // every MMQ kernel's workgroup
 bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 1) != 0; }
 
 // an f16 kernel for this GEMM: f16 mode, Q4_K or Q6_K (the Q6_K kernel needs
-// an even number of super-blocks per row, so that rows start 4-byte
-// aligned), and every buffer offset of the kernel's copies (rows and columns
-// rounded up to the 128 tile) fits in 32 bits
-bool use_mmq2(const rfxq_weight* w, uint32_t rows) {
+// an even number of super-blocks per row, so that rows start 4-byte aligned),
+// and every buffer offset of the kernel's loads fits in 32 bits
+bool f16_kernel(const rfxq_weight* w, uint32_t rows) {
     if (!mmq_f16()) return false;
     const uint64_t k = w->in_features, n = w->out_features, nsb = k / 256u;
     uint64_t bb;
@@ -595,38 +597,56 @@ bool use_mmq2(const rfxq_weight* w, uint32_t rows) {
     else if (w->ggml_type == RFXQ_TYPE_Q6_K && nsb % 2u == 0u) bb = 210u;
     else return false;
     const uint64_t lim = 0xF0000000ull;
-    return (n + 128u) * nsb * bb < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
+    return (n + 256u) * nsb * bb < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
 }
 
-// bytes of the f16 activation copy and of the super-block scale records
-uint64_t xh_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * k * 2u); }
-uint64_t xsc_bytes(uint32_t rows, uint32_t k) { return align256((uint64_t)rows * (k / 256u) * 64u); }
+// weight columns per workgroup tile (rows: kMmqBM, or 64 for the int8 *_m64 kernels)
+uint32_t tile_bn(uint32_t ty, bool f16) { return f16 && ty == RFXQ_TYPE_Q4_K ? 256u : 128u; }
 
-struct GemmPlan {
-    uint32_t splits, sb_per_split, tiles_m, tiles_n;
-    uint64_t off_xds, off_xh, off_xsc, off_part, total;
+// One activation in the layouts its GEMMs read, each 256-byte aligned:
+// int8 (xq [rows][k], xds [rows][k/32] = d | s << 16) and f16 (xh [rows][k],
+// xsx [rows][k/256][16] f16 block sums, xrs [rows] f32 row scales).
+struct ActLayout {
+    uint64_t xq = 0, xds = 0, xh = 0, xsx = 0, xrs = 0, total = 0;
 };
 
-GemmPlan plan_gemm(const Ctx* c, uint32_t rows, uint32_t k, uint32_t n) {
-    GemmPlan p;
-    p.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-    p.tiles_n = (n + kMmqBN - 1u) / kMmqBN;
-    const uint32_t nsb = k / 256u;
-    const uint32_t tiles = p.tiles_m * p.tiles_n;
-    uint32_t splits = 1;
-    const uint32_t cus = c ? (uint32_t)c->cus : 256u;
-    if (tiles < cus) splits = std::min(nsb, (2u * cus + tiles - 1u) / tiles);
-    splits = std::max(1u, env_u32("REFLEX_QUANT_MMA_SPLITS", splits));
-    splits = std::min(splits, nsb);
-    p.sb_per_split = (nsb + splits - 1u) / splits;
-    p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
-    p.off_xds = align256((uint64_t)rows * k);
-    p.off_xh = p.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
-    const bool f16 = mmq_f16();
-    p.off_xsc = p.off_xh + (f16 ? xh_bytes(rows, k) : 0u);
-    p.off_part = p.off_xsc + (f16 ? xsc_bytes(rows, k) : 0u);
-    p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
-    return p;
+ActLayout act_layout_sel(uint32_t rows, uint32_t k, bool i8, bool h) {
+    ActLayout L;
+    uint64_t o = 0;
+    if (i8) {
+        L.xq = o;
+        o += align256((uint64_t)rows * k);
+        L.xds = o;
+        o += align256((uint64_t)rows * (k / 32u) * 4u);
+    }
+    if (h) {
+        L.xh = o;
+        o += align256((uint64_t)rows * k * 2u);
+        L.xsx = o;
+        o += align256((uint64_t)rows * (k / 256u) * 32u);
+        L.xrs = o;
+        o += align256((uint64_t)rows * 4u);
+    }
+    L.total = o;
+    return L;
+}
+
+// the public activation buffer (rfxq_act_q8_1_size): every layout
+ActLayout act_layout(uint32_t rows, uint32_t k) { return act_layout_sel(rows, k, true, true); }
+
+// the descriptor fields of a GEMM reading activation layouts L at `base`
+void act_desc(MmqDesc* d, const uint8_t* base, const ActLayout& L, bool f16, uint32_t k) {
+    if (f16) {
+        d->xq = reinterpret_cast<const int8_t*>(base + L.xh);
+        d->xds = reinterpret_cast<const uint32_t*>(base + L.xsx);
+        d->xrs = reinterpret_cast<const float*>(base + L.xrs);
+        d->ldq = 2u * k;
+    } else {
+        d->xq = reinterpret_cast<const int8_t*>(base + L.xq);
+        d->xds = reinterpret_cast<const uint32_t*>(base + L.xds);
+        d->xrs = nullptr;
+        d->ldq = k;
+    }
 }
 
 uint32_t quant_grid(uint64_t blocks) {
@@ -634,8 +654,9 @@ uint32_t quant_grid(uint64_t blocks) {
     return (uint32_t)std::min<uint64_t>(std::max<uint64_t>((waves + 3u) / 4u, 1u), 8192u);
 }
 
+// int8 layout of x (rfxq_quantize_q8_1); `src_rows` gathers rows
 int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
-                 int8_t* xq, uint32_t* xds, hipStream_t stream, uint16_t* xh = nullptr, uint16_t* xsc = nullptr) {
+                 int8_t* xq, uint32_t* xds, hipStream_t stream) {
     struct {
         const float* x;
         uint32_t ldx, pad0;
@@ -644,17 +665,43 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
         int8_t* xq;
         uint32_t ldq, pad1;
         uint32_t* xds;
-        uint16_t* xh;
-        uint16_t* xsc;
-    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds, xh, xsc};
+    } a = {x, ldx, 0, src_rows, rows, k, xq, k, 0, xds};
     return launch(c->quant, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
                   "rfxq_quantize_q8_1 launch");
 }
 
-// f16: Q4_K / Q6_K descriptors carry the f16 activations (xq, ldq = 2k
-// bytes) and the scale records (xds) and run on rfxq_mmq2_q4k / _q6k
+// f16 layout of x (rfxq_act_f16): one wave per row
+int launch_act_f16(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
+                   uint8_t* base, const ActLayout& L, hipStream_t stream) {
+    struct {
+        const float* x;
+        uint32_t ldx, pad0;
+        const int32_t* src_rows;
+        uint32_t rows, k;
+        uint16_t* xh;
+        uint16_t* xsx;
+        float* xrs;
+    } a = {x, ldx, 0, src_rows, rows, k, reinterpret_cast<uint16_t*>(base + L.xh),
+           reinterpret_cast<uint16_t*>(base + L.xsx), reinterpret_cast<float*>(base + L.xrs)};
+    const uint32_t grid = std::min<uint32_t>((rows + 3u) / 4u, 4096u);
+    return launch(c->act_f16, grid, 0, stream, &a, sizeof a, "rfxq_act_f16 launch");
+}
+
+// the activation layouts of L at `base` from x
+int launch_act(Ctx* c, const float* x, uint32_t rows, uint32_t k, uint8_t* base, const ActLayout& L, bool i8,
+               bool h, hipStream_t stream) {
+    if (i8)
+        if (int rc = launch_quant(c, x, k, nullptr, rows, k, reinterpret_cast<int8_t*>(base + L.xq),
+                                  reinterpret_cast<uint32_t*>(base + L.xds), stream))
+            return rc;
+    if (h)
+        if (int rc = launch_act_f16(c, x, k, nullptr, rows, k, base, L, stream)) return rc;
+    return RFXQ_OK;
+}
+
+// f16: Q4_K / Q6_K descriptors on rfxq_mmqh_q4k / _q6k (f16 activation layout)
 // m64: the descriptors are tiled by 64 rows (rfxq_mmq_*_m64)
-int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
+int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
                bool dots, hipStream_t stream, bool f16 = false, bool m64 = false) {
     MmqArgs a;
     std::memset(&a, 0, sizeof a);
@@ -662,10 +709,8 @@ int launch_mmq(Ctx* c, uint32_t ty, MmqDesc* descs, uint32_t count, const MmqDes
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && !dots && !m64 && ty != RFXQ_TYPE_Q8_0)
-        return launch(ty == RFXQ_TYPE_Q4_K ? c->mmq2_q4k : c->mmq2_q6k, total_wgs, 0, stream, &a, sizeof a,
-                      "rfxq_mmq2 launch", kMmq2Threads);
-    return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch");
+    if (f16 && !dots && !m64 && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)];
+    return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch", kMmqThreads);
 }
 
 int check_mmq_weight(const rfxq_weight* w, const char* what) {
@@ -676,49 +721,79 @@ int check_mmq_weight(const rfxq_weight* w, const char* what) {
     return RFXQ_OK;
 }
 
-// One GEMM's MMQ launch from quantized activations (xh / xsc for the f16
-// kernels, xq / xds otherwise), then the split-K reduce when p splits K
-// (partials in `part`).
-int gemm_run(Ctx* c, const GemmPlan& p, const int8_t* xq, const uint32_t* xds, const uint16_t* xh,
-             const uint16_t* xsc, bool f16, const rfxq_weight* w, uint32_t rows, float* y, float* part,
-             hipStream_t stream) {
+// Split-K: a GEMM whose tiles leave CUs idle splits K into ranges of whole
+// super-blocks (REFLEX_QUANT_MMA_SPLITS sets the split count).
+uint32_t split_count(const Ctx* c, uint32_t tiles, uint32_t nsb) {
+    const uint32_t cus = c ? (uint32_t)c->cus : 256u;
+    uint32_t splits = 1;
+    if (tiles < cus) splits = std::min(nsb, (2u * cus + tiles - 1u) / tiles);
+    splits = std::max(1u, env_u32("REFLEX_QUANT_MMA_SPLITS", splits));
+    return std::min(splits, nsb);
+}
+
+struct GemmPlan {
+    bool f16 = false;
+    uint32_t splits = 1, sb_per_split = 1, tiles_m = 1, tiles_n = 1;
+    ActLayout act;
+    uint64_t off_part = 0, total = 0;
+};
+
+GemmPlan plan_gemm(const Ctx* c, const rfxq_weight* w, uint32_t rows) {
+    GemmPlan p;
+    const uint32_t k = w->in_features, n = w->out_features, nsb = k / 256u;
+    p.f16 = f16_kernel(w, rows);
+    p.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
+    const uint32_t bn = tile_bn(w->ggml_type, p.f16);
+    p.tiles_n = (n + bn - 1u) / bn;
+    const uint32_t splits = split_count(c, p.tiles_m * p.tiles_n, nsb);
+    p.sb_per_split = (nsb + splits - 1u) / splits;
+    p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
+    p.act = act_layout_sel(rows, k, !p.f16, p.f16);
+    p.off_part = p.act.total;
+    p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
+    return p;
+}
+
+int launch_reduce(Ctx* c, const float* part, float* y, uint64_t n, uint32_t splits, hipStream_t stream) {
+    struct {
+        const float* ws;
+        float* y;
+        uint64_t n;
+        uint32_t splits, pad;
+    } a = {part, y, n, splits, 0};
+    const uint64_t blocks = std::min<uint64_t>((n + 255u) / 256u, 8192u);
+    return launch(c->reduce, (uint32_t)blocks, 0, stream, &a, sizeof a, "rfxq_splitk_reduce launch");
+}
+
+// One GEMM's MMQ launch from activation layouts (`act`, layouts p.act), then
+// the split-K reduce when p splits K (partials in `part`).
+int gemm_run(Ctx* c, const GemmPlan& p, const uint8_t* act, const ActLayout& L, const rfxq_weight* w,
+             uint32_t rows, float* y, float* part, hipStream_t stream) {
     const uint32_t k = w->in_features, n = w->out_features;
     MmqDesc d;
     std::memset(&d, 0, sizeof d);
     d.w = w->data;
-    d.xq = f16 ? reinterpret_cast<const int8_t*>(xh) : xq;
-    d.xds = f16 ? reinterpret_cast<const uint32_t*>(xsc) : xds;
+    act_desc(&d, act, L, p.f16, k);
     d.y = p.splits > 1 ? part : y;
     d.m = rows;
     d.n = n;
     d.k = k;
     d.type = w->ggml_type;
-    d.ldq = f16 ? 2u * k : k;
     d.ldy = n;
     d.tiles_m = p.tiles_m;
     d.tiles_n = p.tiles_n;
     d.splits = p.splits;
     d.sb_per_split = p.sb_per_split;
     const uint32_t wgs = p.tiles_m * p.tiles_n * p.splits;
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, f16)) return rc;
-    if (p.splits > 1) {
-        struct {
-            const float* ws;
-            float* y;
-            uint64_t n;
-            uint32_t splits, pad;
-        } a = {part, y, (uint64_t)rows * n, p.splits, 0};
-        const uint64_t blocks = std::min<uint64_t>(((uint64_t)rows * n + 255u) / 256u, 8192u);
-        if (int rc = launch(c->reduce, (uint32_t)blocks, 0, stream, &a, sizeof a, "rfxq_splitk_reduce launch"))
-            return rc;
-    }
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, p.f16)) return rc;
+    if (p.splits > 1)
+        if (int rc = launch_reduce(c, part, y, (uint64_t)rows * n, p.splits, stream)) return rc;
     return RFXQ_OK;
 }
 
 int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
               hipStream_t stream) {
-    const uint32_t k = w->in_features, n = w->out_features;
-    const GemmPlan p = plan_gemm(c, rows, k, n);
+    const GemmPlan p = plan_gemm(c, w, rows);
     if (!ws) {
         if (int rc = ctx_workspace(c, p.total, &ws)) return rc;
     } else if (ws_bytes < p.total) {
@@ -726,32 +801,8 @@ int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float
                     (unsigned long long)ws_bytes, (unsigned long long)p.total);
     }
     uint8_t* base = static_cast<uint8_t*>(ws);
-    int8_t* xq = reinterpret_cast<int8_t*>(base);
-    uint32_t* xds = reinterpret_cast<uint32_t*>(base + p.off_xds);
-    float* part = reinterpret_cast<float*>(base + p.off_part);
-    const bool f16 = use_mmq2(w, rows);
-    uint16_t* xh = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xh) : nullptr;
-    uint16_t* xsc = f16 ? reinterpret_cast<uint16_t*>(base + p.off_xsc) : nullptr;
-    if (int rc = launch_quant(c, x, k, nullptr, rows, k, f16 ? nullptr : xq, f16 ? nullptr : xds, stream, xh, xsc))
-        return rc;
-    return gemm_run(c, p, xq, xds, xh, xsc, f16, w, rows, y, part, stream);
-}
-
-// ------------------------------------------------------------------ quantized activation buffers
-
-// One activation quantized in every layout the MMQ kernels read: xq, xds,
-// then (f16 kernels) xh and xsc, each 256-byte aligned.
-struct ActLayout {
-    uint64_t xds, xh, xsc, total;
-};
-
-ActLayout act_layout(uint32_t rows, uint32_t k) {
-    ActLayout L;
-    L.xds = align256((uint64_t)rows * k);
-    L.xh = L.xds + align256((uint64_t)rows * (k / 32u) * 4u);
-    L.xsc = L.xh + xh_bytes(rows, k);
-    L.total = L.xsc + xsc_bytes(rows, k);
-    return L;
+    if (int rc = launch_act(c, x, rows, w->in_features, base, p.act, !p.f16, p.f16, stream)) return rc;
+    return gemm_run(c, p, base, p.act, w, rows, y, reinterpret_cast<float*>(base + p.off_part), stream);
 }
 
 int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
@@ -762,29 +813,23 @@ int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
     return RFXQ_OK;
 }
 
-// the descriptor fields of a GEMM reading activation buffer `act`
-void act_desc(MmqDesc* d, const void* act, const ActLayout& L, bool f16, uint32_t k) {
-    const uint8_t* a = static_cast<const uint8_t*>(act);
-    d->xq = reinterpret_cast<const int8_t*>(f16 ? a + L.xh : a);
-    d->xds = reinterpret_cast<const uint32_t*>(f16 ? a + L.xsc : a + L.xds);
-    d->ldq = f16 ? 2u * k : k;
-}
-
 // ------------------------------------------------------------------ grouped GEMMs
 
 // GEMMs of one row count over several weights, grouped: each distinct
-// activation (by address) is quantized once, and each weight type runs as one
-// MMQ launch over all of its GEMMs (no split-K: a group has tiles enough).
+// activation (by address) is brought into the layouts its GEMMs read once,
+// and each weight type runs as one MMQ launch over all of its GEMMs.
 struct GemmGroup {
     struct Act {
         const float* x;
         uint32_t k;
-        uint64_t off_xq, off_xds, off_xh, off_xsc;  // off_xh, off_xsc: f16 mode
-        bool need_i8 = false, need_h = false;      // layouts its GEMMs read
+        uint64_t off = 0;  // workspace offset of the layouts L
+        ActLayout L;
+        bool need_i8 = false, need_h = false;
     };
     bool f16[3] = {false, false, false};  // per type_index: the f16 kernel
     std::vector<Act> acts;
     std::vector<MmqDesc> descs[3];  // per type_index
+    std::vector<uint32_t> act_of[3];  // per descriptor: its activation
     uint32_t wgs[3] = {0, 0, 0};
     // GEMMs split along K (a type with fewer tiles than two per CU):
     // partials at workspace offset `off`, reduced into y after the type's launch
@@ -798,60 +843,81 @@ struct GemmGroup {
     };
     std::vector<Reduce> reduces;
     uint64_t ws_bytes = 0;
+    // f16 mode: Q8_0 GEMMs run as one GEMV per row (f16 activations; there
+    // is no f16-activation Q8_0 MMQ kernel and the int8 format's error floor
+    // exceeds the north star's bound)
+    std::vector<rfxq_gemv_item> q8_rows;
 };
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
     // the f16 kernel for the group's GEMMs of one type only if every one of them can take it
     g->f16[0] = g->f16[1] = mmq_f16();
-    for (uint32_t i = 0; i < count; i++)
-        if (items[i].w && items[i].w->ggml_type != RFXQ_TYPE_Q8_0 && !use_mmq2(items[i].w, rows))
-            g->f16[type_index(items[i].w->ggml_type)] = false;
-    const bool any_f16 = g->f16[0] || g->f16[1];
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
         if (!it.x || !it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: item %u has a NULL x or y", i);
         if (reinterpret_cast<uintptr_t>(it.x) % 16u)
             return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not 16-byte aligned", i);
+        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !f16_kernel(it.w, rows)) g->f16[type_index(it.w->ggml_type)] = false;
+    }
+    // activations and the layouts they need
+    const bool q8_gemv = mmq_f16();
+    std::vector<uint32_t> item_act(count);
+    for (uint32_t i = 0; i < count; i++) {
+        const rfxq_gemm_item& it = items[i];
+        if (q8_gemv && it.w->ggml_type == RFXQ_TYPE_Q8_0) {
+            for (uint32_t r = 0; r < rows; r++)
+                g->q8_rows.push_back({it.x + (uint64_t)r * it.w->in_features, it.w,
+                                      it.y + (uint64_t)r * it.w->out_features});
+            item_act[i] = ~0u;
+            continue;
+        }
         const uint32_t k = it.w->in_features;
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
-            GemmGroup::Act act{it.x, k, 0, 0, 0, 0, false, false};
-            act.off_xq = g->ws_bytes;
-            act.off_xds = act.off_xq + align256((uint64_t)rows * k);
-            act.off_xh = act.off_xds + align256((uint64_t)rows * (k / 32u) * 4u);
-            act.off_xsc = act.off_xh + (any_f16 ? xh_bytes(rows, k) : 0u);
-            g->ws_bytes = act.off_xsc + (any_f16 ? xsc_bytes(rows, k) : 0u);
+            GemmGroup::Act act;
+            act.x = it.x;
+            act.k = k;
             g->acts.push_back(act);
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
         }
-        const bool f16 = g->f16[type_index(it.w->ggml_type)];
-        if (f16) g->acts[ai].need_h = true;
+        item_act[i] = (uint32_t)ai;
+        if (g->f16[type_index(it.w->ggml_type)]) g->acts[ai].need_h = true;
         else g->acts[ai].need_i8 = true;
+    }
+    for (auto& a : g->acts) {
+        a.L = act_layout_sel(rows, a.k, a.need_i8, a.need_h);
+        a.off = g->ws_bytes;
+        g->ws_bytes += a.L.total;
+    }
+    for (uint32_t i = 0; i < count; i++) {
+        const rfxq_gemm_item& it = items[i];
+        if (item_act[i] == ~0u) continue;
+        const uint32_t k = it.w->in_features, t = type_index(it.w->ggml_type);
+        const GemmGroup::Act& a = g->acts[item_act[i]];
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;
         // offsets until the workspace is known
-        d.xq = reinterpret_cast<const int8_t*>(f16 ? g->acts[ai].off_xh : g->acts[ai].off_xq);
-        d.xds = reinterpret_cast<const uint32_t*>(f16 ? g->acts[ai].off_xsc : g->acts[ai].off_xds);
+        act_desc(&d, reinterpret_cast<const uint8_t*>(a.off), a.L, g->f16[t], k);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
         d.k = k;
         d.type = it.w->ggml_type;
-        d.ldq = f16 ? 2u * k : k;
         d.ldy = d.n;
         d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-        d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
+        const uint32_t bn = tile_bn(d.type, g->f16[t]);
+        d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = k / 256u;
-        const uint32_t t = type_index(d.type);
         d.wg_begin = g->wgs[t];
         g->wgs[t] += d.tiles_m * d.tiles_n;
         g->descs[t].push_back(d);
+        g->act_of[t].push_back(item_act[i]);
     }
     // a type whose tiles would leave CUs idle splits K (fixed-order reduce)
     // (REFLEX_QUANT_MMA_SPLITS sets the split count, as for single GEMMs)
@@ -880,17 +946,6 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
     return RFXQ_OK;
 }
 
-int launch_reduce(Ctx* c, const float* part, float* y, uint64_t n, uint32_t splits, hipStream_t stream) {
-    struct {
-        const float* ws;
-        float* y;
-        uint64_t n;
-        uint32_t splits, pad;
-    } a = {part, y, n, splits, 0};
-    const uint64_t blocks = std::min<uint64_t>((n + 255u) / 256u, 8192u);
-    return launch(c->reduce, (uint32_t)blocks, 0, stream, &a, sizeof a, "rfxq_splitk_reduce launch");
-}
-
 // the split-K reduces of type t
 int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream) {
     for (const auto& r : g.reduces)
@@ -901,10 +956,11 @@ int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream
 
 // workspace offsets -> addresses
 void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
-    for (auto& v : g->descs)
-        for (MmqDesc& d : v) {
-            d.xq = reinterpret_cast<const int8_t*>(ws + reinterpret_cast<uintptr_t>(d.xq));
-            d.xds = reinterpret_cast<const uint32_t*>(ws + reinterpret_cast<uintptr_t>(d.xds));
+    for (uint32_t t = 0; t < 3; t++)
+        for (size_t i = 0; i < g->descs[t].size(); i++) {
+            MmqDesc& d = g->descs[t][i];
+            const GemmGroup::Act& a = g->acts[g->act_of[t][i]];
+            act_desc(&d, ws + a.off, a.L, g->f16[t], d.k);
         }
     for (auto& r : g->reduces) {
         r.part = reinterpret_cast<float*>(ws + r.off);
@@ -914,12 +970,7 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
 
 int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
     for (const auto& a : g.acts)
-        if (int rc = launch_quant(c, a.x, a.k, nullptr, rows, a.k,
-                                  a.need_i8 ? reinterpret_cast<int8_t*>(ws + a.off_xq) : nullptr,
-                                  a.need_i8 ? reinterpret_cast<uint32_t*>(ws + a.off_xds) : nullptr, stream,
-                                  a.need_h ? reinterpret_cast<uint16_t*>(ws + a.off_xh) : nullptr,
-                                  a.need_h ? reinterpret_cast<uint16_t*>(ws + a.off_xsc) : nullptr))
-            return rc;
+        if (int rc = launch_act(c, a.x, rows, a.k, ws + a.off, a.L, a.need_i8, a.need_h, stream)) return rc;
     return RFXQ_OK;
 }
 
@@ -982,15 +1033,21 @@ int expert_slice(const rfxq_weight* w, uint32_t e, rfxq_weight* out, const char*
 
 // ====================================================================== C ABI
 
-struct QuantDesc {
+struct QuantDesc {  // rfxq_quantize_q8_1_multi
     const float* x;
     int8_t* xq;
     uint32_t* xds;
-    uint16_t* xh;
-    uint16_t* xsc;
     uint32_t rows, k, wg_begin, wgs;
 };
-static_assert(sizeof(QuantDesc) == 56, "QuantDesc layout");
+static_assert(sizeof(QuantDesc) == 40, "QuantDesc layout");
+struct ActF16Desc {  // rfxq_act_f16_multi
+    const float* x;
+    uint16_t* xh;
+    uint16_t* xsx;
+    float* xrs;
+    uint32_t rows, k, wg_begin, wgs;
+};
+static_assert(sizeof(ActF16Desc) == 48, "ActF16Desc layout");
 
 struct rfxq_gemm_plan {
     int device;
@@ -998,8 +1055,11 @@ struct rfxq_gemm_plan {
     void* dev = nullptr;  // quantized activations, one descriptor table per weight type, the quantize table
     GemmGroup g;
     MmqDesc* table[3] = {nullptr, nullptr, nullptr};
-    QuantDesc* qtable = nullptr;
-    uint32_t qgrid = 0;
+    QuantDesc* qtable = nullptr;  // int8 layouts: one rfxq_quantize_q8_1_multi launch
+    uint32_t nq = 0, qgrid = 0;
+    ActF16Desc* htable = nullptr;  // f16 layouts: one rfxq_act_f16_multi launch
+    uint32_t nh = 0, hgrid = 0;
+    rfxq_gemv_plan* q8 = nullptr;  // Q8_0 rows as GEMVs (f16 mode)
 };
 
 struct rfxq_gemv_plan {
@@ -1212,7 +1272,7 @@ uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows) {
         auto it = g_ctx.find(dev);
         if (it != g_ctx.end()) c = it->second.get();
     }
-    return plan_gemm(c, rows, w->in_features, w->out_features).total;
+    return plan_gemm(c, w, rows).total;
 }
 
 int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
@@ -1224,6 +1284,8 @@ int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t row
     if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm: x or y is NULL");
     if (rows == 1) return rfxq_gemv_to(x, x_len, w, y, stream);
     if (env_u32("REFLEX_QUANT_MMA", 1) == 0) return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
+    // f16 mode: Q8_0 rows as GEMVs (f16 activations), as in grouped GEMMs
+    if (w->ggml_type == RFXQ_TYPE_Q8_0 && mmq_f16()) return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
     if (int rc = check_mmq_weight(w, "gemm")) return rc;
     if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemm: x is not 16-byte aligned");
     Ctx* c;
@@ -1258,6 +1320,8 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
         }
         if (int rc = run_group_reduces(c, g, t, stream)) return rc;
     }
+    if (!g.q8_rows.empty())
+        if (int rc = gemv_items(c, g.q8_rows.data(), (uint32_t)g.q8_rows.size(), stream)) return rc;
     return ok();
 }
 
@@ -1271,11 +1335,7 @@ int rfxq_quantize_act_q8_1(const float* x, uint32_t rows, uint32_t k, void* act,
         return fail(RFXQ_ERR_OTHER, "quantize_act_q8_1: x is NULL or not 16-byte aligned");
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    const ActLayout L = act_layout(rows, k);
-    uint8_t* b = static_cast<uint8_t*>(act);
-    if (int rc = launch_quant(c, x, k, nullptr, rows, k, reinterpret_cast<int8_t*>(b),
-                              reinterpret_cast<uint32_t*>(b + L.xds), stream, reinterpret_cast<uint16_t*>(b + L.xh),
-                              reinterpret_cast<uint16_t*>(b + L.xsc)))
+    if (int rc = launch_act(c, x, rows, k, static_cast<uint8_t*>(act), act_layout(rows, k), true, true, stream))
         return rc;
     return ok();
 }
@@ -1299,10 +1359,12 @@ int rfxq_rmsnorm_q8_1(const float* x, const float* weight, uint32_t rows, uint32
         int8_t* xq;
         uint32_t* xds;
         uint16_t* xh;
-        uint16_t* xsc;
+        uint16_t* xsx;
+        float* xrs;
         float* y;
-    } a = {x, weight, rows, k, eps, 0, reinterpret_cast<int8_t*>(b), reinterpret_cast<uint32_t*>(b + L.xds),
-           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsc), y};
+    } a = {x, weight, rows, k, eps, 0, reinterpret_cast<int8_t*>(b + L.xq), reinterpret_cast<uint32_t*>(b + L.xds),
+           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsx),
+           reinterpret_cast<float*>(b + L.xrs), y};
     const uint32_t grid = (rows + kNormRowsPerWg - 1u) / kNormRowsPerWg;
     if (int rc = launch(c->rms_q, grid, 0, stream, &a, sizeof a, "rfxq_rmsnorm_q8_1 launch")) return rc;
     return ok();
@@ -1325,10 +1387,12 @@ int rfxq_silu_and_mul_q8_1(const float* gate, const float* up, uint32_t rows, ui
         int8_t* xq;
         uint32_t* xds;
         uint16_t* xh;
-        uint16_t* xsc;
+        uint16_t* xsx;
+        float* xrs;
         float* y;
-    } a = {gate, up, rows, k, reinterpret_cast<int8_t*>(b), reinterpret_cast<uint32_t*>(b + L.xds),
-           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsc), y};
+    } a = {gate, up, rows, k, reinterpret_cast<int8_t*>(b + L.xq), reinterpret_cast<uint32_t*>(b + L.xds),
+           reinterpret_cast<uint16_t*>(b + L.xh), reinterpret_cast<uint16_t*>(b + L.xsx),
+           reinterpret_cast<float*>(b + L.xrs), y};
     if (int rc = launch(c->silu_q, quant_grid((uint64_t)rows * (k / 32u)), 0, stream, &a, sizeof a,
                         "rfxq_silu_and_mul_q8_1 launch"))
         return rc;
@@ -1343,7 +1407,7 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
     if (!y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1: y is NULL");
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    const GemmPlan p = plan_gemm(c, rows, k, n);
+    const GemmPlan p = plan_gemm(c, w, rows);
     float* part = nullptr;
     if (p.splits > 1) {
         const uint64_t need = (uint64_t)p.splits * rows * n * 4u;
@@ -1356,11 +1420,7 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
         }
         part = static_cast<float*>(ws);
     }
-    const ActLayout L = act_layout(rows, k);
-    const uint8_t* b = static_cast<const uint8_t*>(act);
-    if (int rc = gemm_run(c, p, reinterpret_cast<const int8_t*>(b), reinterpret_cast<const uint32_t*>(b + L.xds),
-                          reinterpret_cast<const uint16_t*>(b + L.xh), reinterpret_cast<const uint16_t*>(b + L.xsc),
-                          use_mmq2(w, rows), w, rows, y, part, stream))
+    if (int rc = gemm_run(c, p, static_cast<const uint8_t*>(act), act_layout(rows, k), w, rows, y, part, stream))
         return rc;
     return ok();
 }
@@ -1374,7 +1434,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         if (int rc = check_mmq_weight(it.w, "gemm_q8_1_batch")) return rc;
         if (int rc = check_act(it.act, rows, it.w->in_features, "gemm_q8_1_batch")) return rc;
         if (!it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: item %u has a NULL y", i);
-        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !use_mmq2(it.w, rows)) f16[type_index(it.w->ggml_type)] = false;
+        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !f16_kernel(it.w, rows)) f16[type_index(it.w->ggml_type)] = false;
     }
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
@@ -1385,7 +1445,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;
-        act_desc(&d, it.act, act_layout(rows, k), f16[t], k);
+        act_desc(&d, static_cast<const uint8_t*>(it.act), act_layout(rows, k), f16[t], k);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
@@ -1393,7 +1453,8 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         d.type = it.w->ggml_type;
         d.ldy = d.n;
         d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-        d.tiles_n = (d.n + kMmqBN - 1u) / kMmqBN;
+        const uint32_t bn = tile_bn(d.type, f16[t]);
+        d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = k / 256u;
         descs[t].push_back(d);
@@ -1430,7 +1491,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
     if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g, (uint32_t)c->cus);
     uint64_t tables = 0;
     if (rc == RFXQ_OK) {
-        tables = align256(plan->g.acts.size() * sizeof(QuantDesc));
+        tables = align256(plan->g.acts.size() * sizeof(QuantDesc)) + align256(plan->g.acts.size() * sizeof(ActF16Desc));
         for (const auto& v : plan->g.descs) tables += align256(v.size() * sizeof(MmqDesc));
         hipError_t e = hipMalloc(&plan->dev, std::max<uint64_t>(1u, plan->g.ws_bytes + tables));
         if (e != hipSuccess) rc = fail(RFXQ_ERR_OUT_OF_MEMORY, "gemm_plan_create: %s", hipGetErrorString(e));
@@ -1448,23 +1509,41 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
             }
             off += align256(v.size() * sizeof(MmqDesc));
         }
-        // one quantize launch for all activations
+        // one launch per layout kind for all activations
         std::vector<QuantDesc> q;
+        std::vector<ActF16Desc> hq;
         for (const auto& a : plan->g.acts) {
-            const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
-            q.push_back(QuantDesc{a.x, a.need_i8 ? reinterpret_cast<int8_t*>(base + a.off_xq) : nullptr,
-                                  a.need_i8 ? reinterpret_cast<uint32_t*>(base + a.off_xds) : nullptr,
-                                  a.need_h ? reinterpret_cast<uint16_t*>(base + a.off_xh) : nullptr,
-                                  a.need_h ? reinterpret_cast<uint16_t*>(base + a.off_xsc) : nullptr, rows, a.k,
-                                  plan->qgrid, wgs});
-            plan->qgrid += wgs;
+            uint8_t* ab = base + a.off;
+            if (a.need_i8) {
+                const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
+                q.push_back(QuantDesc{a.x, reinterpret_cast<int8_t*>(ab + a.L.xq),
+                                      reinterpret_cast<uint32_t*>(ab + a.L.xds), rows, a.k, plan->qgrid, wgs});
+                plan->qgrid += wgs;
+            }
+            if (a.need_h) {
+                const uint32_t wgs = std::min<uint32_t>((rows + 3u) / 4u, 4096u);
+                hq.push_back(ActF16Desc{a.x, reinterpret_cast<uint16_t*>(ab + a.L.xh),
+                                        reinterpret_cast<uint16_t*>(ab + a.L.xsx), reinterpret_cast<float*>(ab + a.L.xrs),
+                                        rows, a.k, plan->hgrid, wgs});
+                plan->hgrid += wgs;
+            }
         }
+        plan->nq = (uint32_t)q.size();
+        plan->nh = (uint32_t)hq.size();
         plan->qtable = reinterpret_cast<QuantDesc*>(base + off);
-        if (rc == RFXQ_OK) {
+        off += align256(q.size() * sizeof(QuantDesc));
+        plan->htable = reinterpret_cast<ActF16Desc*>(base + off);
+        if (rc == RFXQ_OK && !q.empty()) {
             hipError_t e = hipMemcpy(plan->qtable, q.data(), q.size() * sizeof(QuantDesc), hipMemcpyHostToDevice);
             if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemm_plan_create upload: %s", hipGetErrorString(e));
         }
+        if (rc == RFXQ_OK && !hq.empty()) {
+            hipError_t e = hipMemcpy(plan->htable, hq.data(), hq.size() * sizeof(ActF16Desc), hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemm_plan_create upload: %s", hipGetErrorString(e));
+        }
     }
+    if (rc == RFXQ_OK && !plan->g.q8_rows.empty())
+        rc = rfxq_gemv_plan_create(plan->g.q8_rows.data(), (uint32_t)plan->g.q8_rows.size(), device, &plan->q8);
     (void)hipSetDevice(prev);
     if (rc != RFXQ_OK) {
         if (plan->dev) (void)hipFree(plan->dev);
@@ -1478,12 +1557,22 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
     if (!plan) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_plan_run: NULL plan");
     Ctx* c;
     if (int rc = load_ctx(plan->device, &c)) return rc;
-    struct {
-        const QuantDesc* table;
-        uint32_t ndesc, pad;
-    } qa = {plan->qtable, (uint32_t)plan->g.acts.size(), 0};
-    if (int rc = launch(c->quant_multi, plan->qgrid, 0, stream, &qa, sizeof qa, "rfxq_quantize_q8_1_multi launch"))
-        return rc;
+    if (plan->nq) {
+        struct {
+            const QuantDesc* table;
+            uint32_t ndesc, pad;
+        } qa = {plan->qtable, plan->nq, 0};
+        if (int rc = launch(c->quant_multi, plan->qgrid, 0, stream, &qa, sizeof qa, "rfxq_quantize_q8_1_multi launch"))
+            return rc;
+    }
+    if (plan->nh) {
+        struct {
+            const ActF16Desc* table;
+            uint32_t ndesc, pad;
+        } ha = {plan->htable, plan->nh, 0};
+        if (int rc = launch(c->act_f16_multi, plan->hgrid, 0, stream, &ha, sizeof ha, "rfxq_act_f16_multi launch"))
+            return rc;
+    }
     for (uint32_t t = 0; t < 3; t++) {
         const auto& v = plan->g.descs[t];
         if (v.empty()) continue;
@@ -1495,11 +1584,14 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
             return rc;
         if (int rc = run_group_reduces(c, plan->g, t, stream)) return rc;
     }
+    if (plan->q8)
+        if (int rc = rfxq_gemv_plan_run(plan->q8, stream)) return rc;
     return ok();
 }
 
 void rfxq_gemm_plan_destroy(rfxq_gemm_plan* plan) {
     if (!plan) return;
+    rfxq_gemv_plan_destroy(plan->q8);
     if (plan->dev) (void)hipFree(plan->dev);
     delete plan;
 }
@@ -1724,14 +1816,16 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         return ok();
     }
 
-    // workspace layout
-    const uint64_t o_xq = 0;
-    const uint64_t o_xds = o_xq + align256((uint64_t)rows * hidden);
-    const uint64_t o_gate = o_xds + align256((uint64_t)rows * (hidden / 32u) * 4u);
+    // workspace layout: x and the SiLU·up rows in the layouts the expert
+    // GEMMs read (f16 kernels for Q4_K / Q6_K experts, int8 otherwise)
+    const bool f16 = f16_kernel(&g0, rows) && f16_kernel(&u0, rows) && f16_kernel(&d0, P);
+    const ActLayout Lx = act_layout_sel(rows, hidden, !f16, f16);
+    const ActLayout Ls = act_layout_sel(P, ffn, !f16, f16);
+    const uint64_t o_x = 0;
+    const uint64_t o_gate = o_x + Lx.total;
     const uint64_t o_up = o_gate + align256((uint64_t)P * ffn * 4u);
-    const uint64_t o_xq2 = o_up + align256((uint64_t)P * ffn * 4u);
-    const uint64_t o_xds2 = o_xq2 + align256((uint64_t)P * ffn);
-    const uint64_t o_down = o_xds2 + align256((uint64_t)P * (ffn / 32u) * 4u);
+    const uint64_t o_s = o_up + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_down = o_s + Ls.total;
     const uint64_t o_tab = o_down + align256((uint64_t)P * hidden * 4u);
     // tables: pair_row[P], comb_idx[rows*k], comb_w[rows*k], descs (up to 3E)
     const uint64_t o_pr = o_tab;
@@ -1742,45 +1836,48 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     void* ws;
     if (int rc = ctx_workspace(c, total, &ws)) return rc;
     uint8_t* B = static_cast<uint8_t*>(ws);
-    int8_t* xq = reinterpret_cast<int8_t*>(B + o_xq);
-    uint32_t* xds = reinterpret_cast<uint32_t*>(B + o_xds);
     float* gout = reinterpret_cast<float*>(B + o_gate);
     float* uout = reinterpret_cast<float*>(B + o_up);
-    int8_t* xq2 = reinterpret_cast<int8_t*>(B + o_xq2);
-    uint32_t* xds2 = reinterpret_cast<uint32_t*>(B + o_xds2);
     float* dout = reinterpret_cast<float*>(B + o_down);
     int32_t* d_pr = reinterpret_cast<int32_t*>(B + o_pr);
     int32_t* d_ci = reinterpret_cast<int32_t*>(B + o_ci);
     float* d_cw = reinterpret_cast<float*>(B + o_cw);
     MmqDesc* d_desc = reinterpret_cast<MmqDesc*>(B + o_desc);
 
-    // descriptor tables: [gate+up descs][down descs]; experts averaging at
-    // most 48 routed rows take 64-row tiles
+    // descriptor tables: [gate+up descs][down descs]; on the int8 kernels
+    // experts averaging at most 48 routed rows take 64-row tiles
     uint32_t used = 0;
     for (uint32_t e = 0; e < expert_count; e++) used += off[e + 1] > off[e];
-    const bool m64 = used && P <= 48u * used;
+    const bool m64 = !f16 && used && P <= 48u * used;
     const uint32_t bm = m64 ? 64u : kMmqBM;
     std::vector<MmqDesc> descs;
     uint32_t wg_gu = 0;
-    auto add = [&](const rfxq_weight* w, uint32_t e, const int8_t* q, const uint32_t* s, const int32_t* rws,
-                   uint32_t m, uint32_t ldq, float* y, uint32_t n, uint32_t& wg) {
+    // act: the activation layouts (rows gathered through rws, or starting at row r0)
+    auto add = [&](const rfxq_weight* w, uint32_t e, const uint8_t* act, const ActLayout& L, uint32_t r0,
+                   const int32_t* rws, uint32_t m, float* y, uint32_t n, uint32_t& wg) {
         rfxq_weight ew;
         expert_slice(w, e, &ew, "moe_ffn_grouped");
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = ew.data;
-        d.xq = q;
-        d.xds = s;
+        act_desc(&d, act, L, f16, ew.in_features);
+        if (r0) {
+            d.xq += (uint64_t)r0 * d.ldq;
+            d.xds = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(d.xds) +
+                                                      (uint64_t)r0 * (f16 ? ew.in_features / 256u * 32u
+                                                                          : ew.in_features / 32u * 4u));
+            if (f16) d.xrs += r0;
+        }
         d.rows = rws;
         d.y = y;
         d.m = m;
         d.n = n;
         d.k = ew.in_features;
         d.type = ew.ggml_type;
-        d.ldq = ldq;
         d.ldy = n;
         d.tiles_m = (m + bm - 1u) / bm;
-        d.tiles_n = (n + kMmqBN - 1u) / kMmqBN;
+        const uint32_t bn = tile_bn(d.type, f16);
+        d.tiles_n = (n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = d.k / 256u;
         d.wg_begin = wg;
@@ -1790,16 +1887,15 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     for (uint32_t e = 0; e < expert_count; e++) {
         const uint32_t m = off[e + 1] - off[e];
         if (!m) continue;
-        add(gate, e, xq, xds, d_pr + off[e], m, hidden, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
-        add(up, e, xq, xds, d_pr + off[e], m, hidden, uout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+        add(gate, e, B + o_x, Lx, 0, d_pr + off[e], m, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+        add(up, e, B + o_x, Lx, 0, d_pr + off[e], m, uout + (uint64_t)off[e] * ffn, ffn, wg_gu);
     }
     const uint32_t n_gu = (uint32_t)descs.size();
     uint32_t wg_dn = 0;
     for (uint32_t e = 0; e < expert_count; e++) {
         const uint32_t m = off[e + 1] - off[e];
         if (!m) continue;
-        add(down, e, xq2 + (uint64_t)off[e] * ffn, xds2 + (uint64_t)off[e] * (ffn / 32u), nullptr, m, ffn,
-            dout + (uint64_t)off[e] * hidden, hidden, wg_dn);
+        add(down, e, B + o_s, Ls, off[e], nullptr, m, dout + (uint64_t)off[e] * hidden, hidden, wg_dn);
     }
     const uint32_t n_dn = (uint32_t)descs.size() - n_gu;
 
@@ -1812,16 +1908,16 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     std::memcpy(host.data() + (o_desc - o_tab), descs.data(), descs.size() * sizeof(MmqDesc));
     if (int rc = stage_upload(c, B + o_tab, host.data(), host.size(), stream)) return rc;
 
-    if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
+    if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
     if (n_gu) {
-        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, false, m64))
+        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, m64))
             return rc;
     }
     if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-    if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
+    if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
     if (n_dn) {
         if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
-                                false, m64))
+                                f16, m64))
             return rc;
     }
     {
@@ -1873,7 +1969,7 @@ struct MoePlanArgs {
     MmqDesc tg, tu, td;
     uint64_t w_stride_gu, w_stride_dn;
     uint32_t tokens, k, E, P2;
-    uint32_t bm, ffn, hidden, pad;
+    uint32_t bm, ffn, hidden, f16;
     GemvDesc* gemv_gu;
     GemvDesc* gemv_dn;
     GemvDesc vg, vu, vd;
@@ -1881,7 +1977,7 @@ struct MoePlanArgs {
     uint32_t normalize;
     float scale;
 };
-static_assert(sizeof(MoePlanArgs) == 592, "MoePlanArgs layout");
+static_assert(sizeof(MoePlanArgs) == 616, "MoePlanArgs layout");
 
 int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
                                 uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
@@ -1922,13 +2018,14 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
 
     // workspace: quantized tokens, gate/up outputs, quantized SiLU·up, down
     // outputs, routing, grouping and descriptor tables
-    const uint64_t o_xq = 0;
-    const uint64_t o_xds = o_xq + align256((uint64_t)rows * hidden);
-    const uint64_t o_gate = o_xds + align256((uint64_t)rows * (hidden / 32u) * 4u);
+    const bool f16 = f16_kernel(&g0, rows) && f16_kernel(&u0, rows) && f16_kernel(&d0, P);
+    const ActLayout Lx = act_layout_sel(rows, hidden, !f16, f16);
+    const ActLayout Ls = act_layout_sel(P, ffn, !f16, f16);
+    const uint64_t o_x = 0;
+    const uint64_t o_gate = o_x + Lx.total;
     const uint64_t o_up = o_gate + align256((uint64_t)P * ffn * 4u);
-    const uint64_t o_xq2 = o_up + align256((uint64_t)P * ffn * 4u);
-    const uint64_t o_xds2 = o_xq2 + align256((uint64_t)P * ffn);
-    const uint64_t o_down = o_xds2 + align256((uint64_t)P * (ffn / 32u) * 4u);
+    const uint64_t o_s = o_up + align256((uint64_t)P * ffn * 4u);
+    const uint64_t o_down = o_s + Ls.total;
     const uint64_t o_idx = o_down + align256((uint64_t)P * hidden * 4u);
     const uint64_t o_w = o_idx + align256((uint64_t)P * 4u);
     const uint64_t o_pr = o_w + align256((uint64_t)P * 4u);
@@ -1944,20 +2041,16 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     void* ws;
     if (int rc = ctx_workspace(c, total, &ws)) return rc;
     uint8_t* B = static_cast<uint8_t*>(ws);
-    int8_t* xq = reinterpret_cast<int8_t*>(B + o_xq);
-    uint32_t* xds = reinterpret_cast<uint32_t*>(B + o_xds);
     float* gout = reinterpret_cast<float*>(B + o_gate);
     float* uout = reinterpret_cast<float*>(B + o_up);
-    int8_t* xq2 = reinterpret_cast<int8_t*>(B + o_xq2);
-    uint32_t* xds2 = reinterpret_cast<uint32_t*>(B + o_xds2);
     float* dout = reinterpret_cast<float*>(B + o_down);
     int32_t* d_idx = reinterpret_cast<int32_t*>(B + o_idx);
     float* d_w = reinterpret_cast<float*>(B + o_w);
     MmqDesc* d_gu = reinterpret_cast<MmqDesc*>(B + o_dgu);
     MmqDesc* d_dn = reinterpret_cast<MmqDesc*>(B + o_ddn);
 
-    // 64-row tiles when the experts would average at most 48 rows
-    const bool m64 = P <= 48u * std::min(expert_count, P);
+    // int8 kernels: 64-row tiles when the experts would average at most 48 rows
+    const bool m64 = !f16 && P <= 48u * std::min(expert_count, P);
     const uint32_t bm = m64 ? 64u : kMmqBM;
     MoePlanArgs pa;
     std::memset(&pa, 0, sizeof pa);
@@ -1968,24 +2061,24 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     pa.comb_w = reinterpret_cast<float*>(B + o_cw);
     pa.descs_gu = d_gu;
     pa.descs_dn = d_dn;
-    auto tmpl = [&](MmqDesc* d, const rfxq_weight* w0, const int8_t* q, const uint32_t* s, float* y, uint32_t n,
+    auto tmpl = [&](MmqDesc* d, const rfxq_weight* w0, const uint8_t* act, const ActLayout& L, float* y, uint32_t n,
                     uint32_t k) {
         d->w = static_cast<const uint8_t*>(w0->data);
-        d->xq = q;
-        d->xds = s;
+        act_desc(d, act, L, f16, k);
         d->y = y;
         d->n = n;
         d->k = k;
         d->type = w0->ggml_type;
-        d->ldq = k;
         d->ldy = n;
-        d->tiles_n = (n + kMmqBN - 1u) / kMmqBN;
+        const uint32_t bn = tile_bn(d->type, f16);
+        d->tiles_n = (n + bn - 1u) / bn;
         d->splits = 1;
         d->sb_per_split = k / 256u;
     };
-    tmpl(&pa.tg, &g0, xq, xds, gout, ffn, hidden);
-    tmpl(&pa.tu, &u0, xq, xds, uout, ffn, hidden);
-    tmpl(&pa.td, &d0, xq2, xds2, dout, hidden, ffn);
+    tmpl(&pa.tg, &g0, B + o_x, Lx, gout, ffn, hidden);
+    tmpl(&pa.tu, &u0, B + o_x, Lx, uout, ffn, hidden);
+    tmpl(&pa.td, &d0, B + o_s, Ls, dout, hidden, ffn);
+    pa.f16 = f16 ? 1u : 0u;
     pa.w_stride_gu = gate->len / expert_count;
     pa.w_stride_dn = down->len / expert_count;
     pa.tokens = rows;
@@ -2028,17 +2121,17 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
         if (int rc = gemv_launch_counted(c, dn, pa.gemv_dn, stream)) return rc;
     } else {
-        if (int rc = launch_quant(c, x, hidden, nullptr, rows, hidden, xq, xds, stream)) return rc;
+        if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
         // launch grids: upper bounds on the tiles (sum over experts of
         // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
         const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
         if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
-                                2u * tiles_bound * pa.tg.tiles_n, false, stream, false, m64))
+                                2u * tiles_bound * pa.tg.tiles_n, false, stream, f16, m64))
             return rc;
         if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-        if (int rc = launch_quant(c, gout, ffn, nullptr, P, ffn, xq2, xds2, stream)) return rc;
+        if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
         if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
-                                stream, false, m64))
+                                stream, f16, m64))
             return rc;
     }
     struct {

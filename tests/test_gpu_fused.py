@@ -26,13 +26,15 @@ def _a256(n):
 
 
 def _layouts(act, rows, k):
-    """The written regions of an activation buffer: xq, xds, xh, xsc."""
+    """The written regions of an activation buffer: the int8 layout (xq, xds)
+    and the f16 layout (xh, xsx, xrs)."""
     b = act.cpu().numpy()
-    xds = _a256(rows * k)
-    xh = xds + _a256(rows * k // 32 * 4)
-    xsc = xh + _a256(rows * k * 2)
-    return (b[:rows * k], b[xds:xds + rows * k // 32 * 4], b[xh:xh + rows * k * 2],
-            b[xsc:xsc + rows * (k // 256) * 64])
+    sizes = [rows * k, rows * k // 32 * 4, rows * k * 2, rows * (k // 256) * 32, rows * 4]
+    out, o = [], 0
+    for sz in sizes:
+        out.append(b[o:o + sz])
+        o += _a256(sz)
+    return out
 
 
 def _same_act(a, b, rows, k):
@@ -68,10 +70,16 @@ def test_silu_and_mul_q8_1(rq, rows, k):
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("rows,n,k", [(512, 1024, 1024), (64, 512, 4096), (300, 136, 2048)])
-def test_gemm_from_activation_buffer(rq, ty, rows, n, k):
+def test_gemm_from_activation_buffer(rq, monkeypatch, ty, rows, n, k):
+    """GEMMs from a buffer equal rfxq_gemm on the f32 activation. A buffer holds
+    no f32 copy, so Q8_0 reads its int8 layout: compared with rfxq_gemm on the
+    int8 kernels (REFLEX_MMQ_F16=0), where f16 mode runs Q8_0 rows as GEMVs."""
     x = _dev(synth.activations(rows * k, 5 + rows))
     w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, 6 + n), k, n, device=DEV)
+    if ty == Q8_0:
+        monkeypatch.setenv("REFLEX_MMQ_F16", "0")
     want = rq.gemm(x, w, rows)
+    monkeypatch.delenv("REFLEX_MMQ_F16", raising=False)
     act = rq.quantize_act_q8_1(x, rows, k)
     assert torch.equal(rq.gemm_q8_1(act, w, rows), want)
 
@@ -90,7 +98,10 @@ def test_gemm_q8_1_batch(rq, monkeypatch):
     refs = []
     for (act, w, _), (ty, n, k) in zip(items, shapes):
         r = torch.empty(rows * n, device=DEV)
+        if ty == Q8_0:   # the buffer's int8 layout (see test_gemm_from_activation_buffer)
+            monkeypatch.setenv("REFLEX_MMQ_F16", "0")
         rq.gemm_batch([(xa if k == 1024 else xb, w, r)], rows)
+        monkeypatch.delenv("REFLEX_MMQ_F16", raising=False)
         refs.append(r)
     rq.gemm_q8_1_batch(items, rows)
     for (_, _, y), r in zip(items, refs):

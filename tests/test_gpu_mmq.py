@@ -1,16 +1,21 @@
-"""GPU parity of the prefill path: Q8_1 activation quantization (bit-exact),
-the MMQ kernel's per-32 int32 dots (bit-exact with the CPU emulation), and the
-GEMM output within the north star's 1e-3 bound (max error normalised by the
-output row's L2 norm) of dequant.rs + f64 host matmul.
+"""GPU parity of the prefill GEMM path.
 
-Two references: the model reference (oracle.mmq_model_reference: the same
-algorithm in f64 on the quantized activations) isolates the kernel's own
-rounding, which must stay below 3e-5; the unquantized reference measures the
-end result, which must meet 1e-3 unless the quantization floor of the spec'd
-activation format itself (the model reference's own error) is above 1e-3 on the
-worst row, in which case the kernel may add at most 2% to that floor. Per-32
-int8 quantization of N(0,1) activations has a relative RMS error of about 4.8e-3
-per element; on the worst of 512 rows at N = K = 1024 the floor is ~1.05e-3."""
+Default path (f16 activations; rfxq_act_f16 + rfxq_mmqh_q4k / rfxq_mmqh_q6k):
+the activation stage is bit-exact with the oracle's act_f16; every GEMM output
+is within the north star's literal 1e-3 (max error over a row normalised by
+the row's L2 norm) of dequant.rs + f64 host matmul, at every BASELINE config 3
+and config 4 shape (the 8B layer and the tied 151936 x 1024 Q6_K LM head at
+M = 512 on sampled rows), and within 2e-5 of an exact-arithmetic model of the
+kernel's own operands (oracle.mmqh_model_reference), which isolates the
+kernel's f32 accumulation.
+
+int8 path (REFLEX_MMQ_F16=0: Q8_1 activations, per-32 int8 with an f16 scale):
+the quantizer and the per-32 int32 block dots are bit-exact with the CPU
+emulation, and the GEMM is within 3e-5 of the exact model of that format
+(oracle.mmq_model_reference). The format's own quantization error reaches
+~1.05e-3 (config 3 k_proj) and ~1.25e-3 (v_proj, Q6_K) on the worst of 512
+rows, above the north star's bound, so it is not the default; its tests
+check the kernel, not the format."""
 import os
 
 import numpy as np
@@ -23,7 +28,8 @@ pytestmark = pytest.mark.gpu
 
 Q8_0, Q4K, Q6K = 8, 12, 14
 DEV = "cuda:0"
-TOL = 1e-3
+TOL = 1e-3          # the north star's bound, asserted as written
+MODEL_TOL = 2e-5    # kernel rounding against the exact model of its operands
 
 
 def _dev(a):
@@ -34,7 +40,7 @@ def _weight(rq, ty, blocks, n, k):
     return rq.Weight(rq.GgmlType(ty), _dev(blocks), [k, n])
 
 
-# ------------------------------------------------------------------ quantizer
+# ------------------------------------------------------------------ int8 path: quantizer and block dots
 
 def test_quantize_q8_1_bit_exact(rq, orc):
     rng = np.random.default_rng(1)
@@ -60,8 +66,6 @@ def test_quantize_committed_fixtures(rq):
     assert np.array_equal((d & 0xFFFF).astype(np.uint16), f["xds"][..., 0])
 
 
-# ------------------------------------------------------------------ int32 block dots
-
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("m,n,k", [(3, 8, 512), (37, 70, 512), (130, 129, 768), (1, 300, 256)])
 def test_mmq_block_dots_bit_exact(rq, orc, ty, m, n, k):
@@ -85,26 +89,87 @@ def test_mmq_block_dots_committed_fixtures(rq):
         assert np.array_equal(got, f[f"{name}_dots"]), name
 
 
-# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("m,n,k", [(7, 200, 1024), (129, 300, 512), (512, 1024, 1024)])
+def test_int8_gemm_kernel_matches_format_model(rq, orc, monkeypatch, ty, m, n, k):
+    """The int8 MMQ kernels against the exact model of the Q8_1 format."""
+    monkeypatch.setenv("REFLEX_MMQ_F16", "0")
+    w_np = synth.weights(ty, n, k, 40 + m)
+    x = synth.activations(m * k, 41 + m).reshape(m, k)
+    y = rq.gemm(_dev(x), _weight(rq, ty, w_np, n, k), m).cpu().numpy().reshape(m, n)
+    e = orc.rel_err_row_l2(y, orc.mmq_model_reference(ty, w_np, n, k, x))
+    print(f"int8 kernel type {ty} M={m} [{n}x{k}]: {e:.2e} from the format model")
+    assert e < 3e-5
+
+
+# ------------------------------------------------------------------ default path: f16 activations
+
+def _act_regions(rq, act, rows, k):
+    """(xh u16 [rows, k], xsx u16 [rows, k/256, 16], xrs f32 [rows]) of an activation buffer."""
+    a256 = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    b = act.cpu().numpy()
+    o = a256(rows * k) + a256(rows * k // 32 * 4)
+    xh = b[o:o + rows * k * 2].view(np.uint16).reshape(rows, k)
+    o += a256(rows * k * 2)
+    xsx = b[o:o + rows * (k // 256) * 32].view(np.uint16).reshape(rows, k // 256, 16)
+    o += a256(rows * (k // 256) * 32)
+    xrs = b[o:o + rows * 4].view(np.float32)
+    return xh, xsx, xrs
+
+
+def test_act_f16_bit_exact(rq, orc):
+    """rfxq_act_f16 (the f16 kernels' input stage) against oracle.act_f16: row
+    scales, f16 values in the stored order, and block sums, bit for bit, with
+    rows at the edges of the f16 range."""
+    rng = np.random.default_rng(3)
+    rows, k = 41, 1024
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[0] = 0
+    x[1] *= np.float32(1e6)                  # beyond f16 as plain values
+    x[2] *= np.float32(1e-30)                # below f16's normal range
+    x[3, :] = np.float32(-3.0)               # constant row
+    x[4, 5] = np.float32(7e4)                # one large value
+    x[5] = rng.standard_normal(k).astype(np.float32) * np.float32(2.0) ** rng.integers(-20, 20, k)
+    x[6, 100:] = 0
+    act = rq.quantize_act_q8_1(_dev(x), rows, k)
+    xh, xsx, xrs = _act_regions(rq, act, rows, k)
+    wh, wsx, wrs = orc.act_f16(x)
+    assert np.array_equal(xrs, wrs)
+    assert np.array_equal(xh, wh)
+    assert np.array_equal(xsx, wsx)
+
+
+def _ref_rows(orc, ty, w_np, n, k, xs, chunk=16384):
+    """dequant.rs + f64 host matmul for rows xs, in column chunks (bounded memory)."""
+    qk, bb = orc.BLOCK_DIMS[ty]
+    rb = k // qk * bb
+    out = np.empty((xs.shape[0], n), np.float32)
+    for c0 in range(0, n, chunk):
+        c1 = min(n, c0 + chunk)
+        out[:, c0:c1] = orc.reference_gemm(ty, np.ascontiguousarray(w_np[c0 * rb:c1 * rb]), c1 - c0, k, xs)
+    return out
+
 
 def _check_gemm(rq, orc, ty, m, n, k, w_np, x_np, rows_checked=None):
     w = _weight(rq, ty, w_np, n, k)
     y = rq.gemm(_dev(x_np), w, m).cpu().numpy().reshape(m, n)
     rows = np.arange(m) if rows_checked is None else rows_checked
-    xs = x_np.reshape(m, k)[rows]
-    ref = orc.reference_gemm(ty, w_np, n, k, xs)
-    model = orc.mmq_model_reference(ty, w_np, n, k, xs)
-    e_kernel = orc.rel_err_row_l2(y[rows], model)
-    floor = orc.rel_err_row_l2(model, ref)
+    xs = np.ascontiguousarray(x_np.reshape(m, k)[rows])
+    ref = _ref_rows(orc, ty, w_np, n, k, xs)
     e = orc.rel_err_row_l2(y[rows], ref)
-    print(f"type {ty} M={m} [{n}x{k}]: error {e:.3e} (quantization floor {floor:.3e}, kernel {e_kernel:.1e})")
-    assert e_kernel < 3e-5, f"kernel rounding {e_kernel}"
-    assert e < max(TOL, 1.02 * floor + 2e-5), f"type {ty} M={m} [{n}x{k}] row-L2 error {e} (floor {floor})"
+    msg = f"type {ty} M={m} [{n}x{k}]: row-L2 error {e:.3e}"
+    if ty in (Q4K, Q6K) and (ty == Q4K or (k // 256) % 2 == 0):
+        e_kernel = orc.rel_err_row_l2(y[rows], orc.mmqh_model_reference(ty, w_np, n, k, xs))
+        msg += f", kernel {e_kernel:.1e} from its model"
+        assert e_kernel < MODEL_TOL, msg
+    print(msg)
+    assert e < TOL, msg
     return y, e
 
 
 @pytest.mark.parametrize("name,ty,n,k", synth.QWEN3_06B_LAYER, ids=[c[0] for c in synth.QWEN3_06B_LAYER])
 def test_gemm_prefill_qwen3_06b(rq, orc, name, ty, n, k):
+    """M = 512, every row checked."""
     seed = synth.seed_for(3, 0, [c[0] for c in synth.QWEN3_06B_LAYER].index(name))
     x = synth.activations(512 * k, seed + 1000).reshape(512, k)
     _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x)
@@ -112,11 +177,22 @@ def test_gemm_prefill_qwen3_06b(rq, orc, name, ty, n, k):
 
 @pytest.mark.parametrize("name,ty,n,k", synth.QWEN3_8B_LAYER, ids=[c[0] for c in synth.QWEN3_8B_LAYER])
 def test_gemm_prefill_8b_sampled_rows(rq, orc, name, ty, n, k):
-    """Full M=512 on the GPU; 24 sampled rows checked (rows are independent)."""
+    """BASELINE config 4 at M = 512: the full GEMM on the GPU, 96 sampled rows checked
+    (rows are independent)."""
     seed = synth.seed_for(4, 1, [c[0] for c in synth.QWEN3_8B_LAYER].index(name))
     x = synth.activations(512 * k, seed + 1000).reshape(512, k)
-    rows = np.random.default_rng(seed).choice(512, 24, replace=False)
+    rows = np.sort(np.random.default_rng(seed).choice(512, 96, replace=False))
     _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x, rows)
+
+
+def test_gemm_prefill_lm_head_m512(rq, orc):
+    """BASELINE config 4's tied LM head, 151936 x 1024 Q6_K, at M = 512: 12 sampled
+    rows against the reference over all 151936 columns."""
+    _, _, n, k = synth.LM_HEAD
+    seed = synth.seed_for(4, 2, 0)
+    x = synth.activations(512 * k, seed + 1000).reshape(512, k)
+    rows = np.sort(np.random.default_rng(seed).choice(512, 12, replace=False))
+    _check_gemm(rq, orc, Q6K, 512, n, k, synth.weights(Q6K, n, k, seed), x, rows)
 
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
@@ -128,7 +204,23 @@ def test_gemm_row_counts(rq, orc, ty, m):
     _check_gemm(rq, orc, ty, m, n, k, w_np, x)
 
 
-def test_gemm_rows_independent_and_deterministic(rq, orc):
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("m,n,k", [(33, 200, 256), (129, 1000, 2048), (300, 136, 4096), (64, 130, 768),
+                                   (513, 3072, 1024)])
+def test_gemm_ragged_shapes(rq, orc, ty, m, n, k):
+    """Ragged M and N, K from one super-block up (Q6_K rows with an odd
+    super-block count, k = 256 and 768, run on the int8 kernel and are held to
+    its format model only)."""
+    w_np = synth.weights(ty, n, k, 90 + m)
+    x = synth.activations(m * k, 91 + m).reshape(m, k)
+    if ty == Q6K and (k // 256) % 2:
+        y = rq.gemm(_dev(x), _weight(rq, ty, w_np, n, k), m).cpu().numpy().reshape(m, n)
+        assert orc.rel_err_row_l2(y, orc.mmq_model_reference(ty, w_np, n, k, x)) < 3e-5
+    else:
+        _check_gemm(rq, orc, ty, m, n, k, w_np, x)
+
+
+def test_gemm_rows_independent_and_deterministic(rq, orc, monkeypatch):
     """Row r of the output depends only on row r of x, and repeats give identical bits."""
     n, k = 1024, 2048
     w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 9), n, k)
@@ -136,34 +228,25 @@ def test_gemm_rows_independent_and_deterministic(rq, orc):
     ya = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
     yb = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
     assert np.array_equal(ya, yb)
-    yc = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
-    # same tile decomposition along K -> same bits for the shared rows
-    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
-    try:
-        y1 = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
-        y2 = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
-    finally:
-        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
+    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")   # same K decomposition on both sides
+    y1 = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
+    y2 = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
     assert np.array_equal(y1[:130], y2)
-    model = orc.mmq_model_reference(Q4K, synth.weights(Q4K, n, k, 9), n, k, x[:130])
-    assert orc.rel_err_row_l2(yc, model) < 3e-5
 
 
-def test_gemm_split_k_matches_unsplit(rq, orc):
-    n, k = 1024, 4096
-    w_np = synth.weights(Q4K, n, k, 12)
-    w = _weight(rq, Q4K, w_np, n, k)
-    x = synth.activations(64 * k, 13).reshape(64, k)
-    outs = []
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
+def test_gemm_split_k_matches_unsplit(rq, orc, monkeypatch, ty):
+    n, k, m = 512, 4096, 64
+    w_np = synth.weights(ty, n, k, 12)
+    w = _weight(rq, ty, w_np, n, k)
+    x = _dev(synth.activations(m * k, 13))
+    ys = []
     for s in ("1", "4", "16"):
-        os.environ["REFLEX_QUANT_MMA_SPLITS"] = s
-        try:
-            outs.append(rq.gemm(_dev(x), w, 64).cpu().numpy().reshape(64, n))
-        finally:
-            del os.environ["REFLEX_QUANT_MMA_SPLITS"]
-    scale = np.abs(outs[0]).max()
-    for o in outs[1:]:
-        assert np.max(np.abs(o - outs[0])) <= 1e-5 * scale
+        monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", s)
+        ys.append(rq.gemm(x, w, m).cpu().numpy().reshape(m, n))
+    assert np.array_equal(rq.gemm(x, w, m).cpu().numpy().reshape(m, n), ys[-1])   # repeatable
+    for y in ys[1:]:
+        assert orc.rel_err_row_l2(y, ys[0].astype(np.float64)) < 1e-6
 
 
 def test_gemm_one_row_is_decode_gemv(rq):
@@ -180,44 +263,50 @@ def test_gemm_caller_workspace(rq, orc):
     x = synth.activations(m * k, 17).reshape(m, k)
     ws = torch.empty(rq.gemm_workspace_size(w, m), dtype=torch.uint8, device=DEV)
     y = rq.gemm(_dev(x), w, m, workspace=ws).cpu().numpy().reshape(m, n)
-    assert orc.rel_err_row_l2(y, orc.mmq_model_reference(Q6K, w_np, n, k, x)) < 3e-5
+    assert orc.rel_err_row_l2(y, orc.mmqh_model_reference(Q6K, w_np, n, k, x)) < MODEL_TOL
     with pytest.raises(rq.ReflexError):
         rq.gemm(_dev(x), w, m, workspace=ws[:100])
 
 
-def test_gemm_batch_and_plan_match_single_gemms(rq, orc):
-    """Grouped GEMMs (shared activations quantized once, one launch per weight
-    type) give the single-GEMM results bit for bit (split-K off on both sides;
-    by default a group this small would split K)."""
+def test_gemm_batch_and_plan_match_single_gemms(rq, orc, monkeypatch):
+    """Grouped GEMMs (each activation brought into its layouts once, one launch
+    per weight type, Q8_0 rows as GEMVs) give the single-GEMM results bit for
+    bit (split-K off on both sides; by default a group this small splits K)."""
     rows = 300
     shapes = [(Q4K, 768, 1024), (Q4K, 256, 1024), (Q6K, 256, 1024), (Q8_0, 512, 1024), (Q4K, 640, 2048)]
     xa = _dev(synth.activations(rows * 1024, 71))
     xb = _dev(synth.activations(rows * 2048, 72))
-    ws, items = [], []
+    items = []
     for i, (ty, n, k) in enumerate(shapes):
         w = _weight(rq, ty, synth.weights(ty, n, k, 80 + i), n, k)
-        ws.append(w)
         items.append((xa if k == 1024 else xb, w, torch.empty(rows * n, device=DEV)))
-    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
-    try:
-        singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
-        rq.gemm_batch(items, rows)
-        for (x, w, y), ref in zip(items, singles):
+    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")
+    singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
+    rq.gemm_batch(items, rows)
+    for (_, _, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)
+    for _, _, y in items:
+        y.zero_()
+    plan = rq.GemmPlan(items, rows)
+    for _ in range(2):
+        plan.run()
+        for (_, _, y), ref in zip(items, singles):
             assert np.array_equal(y.cpu().numpy(), ref)
-        for _, _, y in items:
-            y.zero_()
-        plan = rq.GemmPlan(items, rows)
-        for _ in range(2):
-            plan.run()
-            for (x, w, y), ref in zip(items, singles):
-                assert np.array_equal(y.cpu().numpy(), ref)
-    finally:
-        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
-    # model-reference parity of one grouped result
+    monkeypatch.delenv("REFLEX_QUANT_MMA_SPLITS")
+    # by default this group splits K: fixed-order partial sums, within f32
+    # rounding of the unsplit result, identical between batch and plan
+    rq.gemm_batch(items, rows)
+    first = [y.cpu().numpy() for _, _, y in items]
+    plan = rq.GemmPlan(items, rows)
+    plan.run()
+    for (_, _, y), a, ref in zip(items, first, singles):
+        assert np.array_equal(y.cpu().numpy(), a)
+        assert np.abs(a - ref).max() <= 1e-5 * np.abs(ref).max()
+    # parity of one grouped result
     n, k = shapes[2][1], shapes[2][2]
-    model = orc.mmq_model_reference(Q6K, synth.weights(Q6K, n, k, 82), n, k,
-                                    synth.activations(rows * 1024, 71).reshape(rows, k))
-    assert orc.rel_err_row_l2(items[2][2].cpu().numpy().reshape(rows, n), model) < 3e-5
+    ref = orc.reference_gemm(Q6K, synth.weights(Q6K, n, k, 82), n, k,
+                             synth.activations(rows * 1024, 71).reshape(rows, k))
+    assert orc.rel_err_row_l2(first[2].reshape(rows, n), ref) < TOL
 
 
 def test_gemm_batch_errors(rq):
@@ -229,102 +318,20 @@ def test_gemm_batch_errors(rq):
         rq.gemm_batch([(x, w1, y), (x, w2, y)], 64)   # one x with two in_features
 
 
-# ------------------------------------------------------------------ f16-MFMA kernels
-
-@pytest.fixture
-def f16_mode(monkeypatch):
-    """Q4_K / Q6_K GEMMs on rfxq_mmq2_q4k / rfxq_mmq2_q6k (REFLEX_MMQ_F16=1)."""
-    monkeypatch.setenv("REFLEX_MMQ_F16", "1")
-    yield
-
-
 @pytest.mark.parametrize("ty", [Q4K, Q6K])
-@pytest.mark.parametrize("m,n,k", [(2, 200, 1024), (33, 200, 256), (129, 1000, 2048), (512, 1024, 1024),
-                                   (513, 3072, 1024), (300, 136, 4096), (64, 130, 768)])
-def test_gemm_f16_kernel(rq, orc, monkeypatch, ty, m, n, k):
-    """Same block dots as the int8 kernel (exact), other f32 rounding: the two
-    kernels agree to f32 accumulation noise and both meet the model bound.
-    (Q6_K rows with an odd super-block count, k = 256 and 768, stay on the
-    int8 kernel.)"""
-    w_np = synth.weights(ty, n, k, 90 + m)
-    x = synth.activations(m * k, 91 + m).reshape(m, k)
-    w = _weight(rq, ty, w_np, n, k)
-    monkeypatch.setenv("REFLEX_MMQ_F16", "0")
-    y8 = rq.gemm(_dev(x), w, m).cpu().numpy().reshape(m, n)
-    monkeypatch.setenv("REFLEX_MMQ_F16", "1")
-    yh, _ = _check_gemm(rq, orc, ty, m, n, k, w_np, x)
-    d = orc.rel_err_row_l2(yh, y8.astype(np.float64))
-    print(f"f16 vs int8 kernel: {d:.2e}")
-    assert d < 1e-5
-
-
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
-def test_gemm_f16_kernel_split_k_and_repeat(rq, orc, f16_mode, monkeypatch, ty):
-    n, k, m = 512, 4096, 64
-    w_np = synth.weights(ty, n, k, 7)
-    x = _dev(synth.activations(m * k, 8))
-    w = _weight(rq, ty, w_np, n, k)
-    ys = []
-    for s in ("1", "4", "16"):
-        monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", s)
-        ys.append(rq.gemm(x, w, m).cpu().numpy())
-    assert np.array_equal(rq.gemm(x, w, m).cpu().numpy(), ys[-1])
-    for y in ys[1:]:
-        assert orc.rel_err_row_l2(y.reshape(m, n), ys[0].reshape(m, n).astype(np.float64)) < 1e-6
-
-
-def test_gemm_f16_plan_matches_single_gemms(rq, f16_mode):
-    rows = 300
-    shapes = [(Q4K, 768, 1024), (Q6K, 256, 1024), (Q4K, 640, 2048)]
-    xa = _dev(synth.activations(rows * 1024, 73))
-    xb = _dev(synth.activations(rows * 2048, 74))
-    items = []
-    for i, (ty, n, k) in enumerate(shapes):
-        w = _weight(rq, ty, synth.weights(ty, n, k, 85 + i), n, k)
-        items.append((xa if k == 1024 else xb, w, torch.empty(rows * n, device=DEV)))
-    os.environ["REFLEX_QUANT_MMA_SPLITS"] = "1"
-    try:
-        singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
-        rq.gemm_batch(items, rows)
-        for (_, _, y), ref in zip(items, singles):
-            assert np.array_equal(y.cpu().numpy(), ref)
-        plan = rq.GemmPlan(items, rows)
-        for _ in range(2):
-            for _, _, y in items:
-                y.zero_()
-            plan.run()
-            for (_, _, y), ref in zip(items, singles):
-                assert np.array_equal(y.cpu().numpy(), ref)
-    finally:
-        del os.environ["REFLEX_QUANT_MMA_SPLITS"]
-    # by default a group this small splits K (fewer tiles than two per CU):
-    # fixed-order partial sums, within f32 rounding of the unsplit result
-    rq.gemm_batch(items, rows)
-    first = [y.cpu().numpy() for _, _, y in items]
-    plan = rq.GemmPlan(items, rows)
-    plan.run()
-    for (_, _, y), a, ref in zip(items, first, singles):
-        assert np.array_equal(y.cpu().numpy(), a)
-        assert np.abs(a - ref).max() <= 1e-5 * np.abs(ref).max()
-
-
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
-@pytest.mark.parametrize("f16", ["1", "0"])
-def test_gemm_large_activations(rq, orc, monkeypatch, f16, ty):
-    """Activations of ~3e3 (32-block sums near 1e5, beyond f16's range as
-    plain values): the f16 and int8 kernels stay within the model bound."""
-    monkeypatch.setenv("REFLEX_MMQ_F16", f16)
+@pytest.mark.parametrize("scale,offset", [(3000.0, 2500.0), (1e5, 0.0), (1e-6, 0.0)])
+def test_gemm_activation_range(rq, orc, ty, scale, offset):
+    """Activations far from N(0,1) (SiLU·up outputs of MoE layers reach 1e5):
+    the per-row power-of-two scale keeps them inside f16's range."""
     m, n, k = 64, 256, 1024
     w_np = synth.weights(ty, n, k, 33)
-    x = synth.activations(m * k, 34).reshape(m, k) * np.float32(3000.0) + np.float32(2500.0)
+    x = synth.activations(m * k, 34).reshape(m, k) * np.float32(scale) + np.float32(offset)
     _check_gemm(rq, orc, ty, m, n, k, w_np, x)
 
 
-def test_gemm_q6k_f16_extreme_codes(rq, orc, f16_mode, monkeypatch):
-    """Q6_K blocks at the limits of the f16 operand split: scales -128 and
-    127 with codes 0 and 63 (|sc*(q - 32)| = 4096 and 3937), so every block
-    dot sits near 2^24; full-scale activations. The f16 kernel's dots are
-    exact, so it agrees with the int8 kernel to f32 rounding."""
+def test_gemm_q6k_extreme_codes(rq, orc):
+    """Q6_K blocks at the limits of the weight operands: scales -128 and 127 with
+    codes 0 and 63 (|sc*(q - 32)| = 4096 and 3937), full-scale activations."""
     m, n, k = 96, 256, 1024
     rng = np.random.default_rng(5)
     nb = n * k // 256
@@ -332,10 +339,18 @@ def test_gemm_q6k_f16_extreme_codes(rq, orc, f16_mode, monkeypatch):
     blk[:, 0:192] = rng.choice(np.array([0x00, 0xFF], np.uint8), size=(nb, 192))
     blk[:, 192:208] = rng.choice(np.array([0x80, 0x7F], np.uint8), size=(nb, 16))
     blk[:, 208:210] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
-    w_np = blk.reshape(-1)
     x = np.where(rng.random((m, k)) < 0.5, np.float32(-1.0), np.float32(1.0)).astype(np.float32)
-    w = _weight(rq, Q6K, w_np, n, k)
-    yh, _ = _check_gemm(rq, orc, Q6K, m, n, k, w_np, x)
-    monkeypatch.setenv("REFLEX_MMQ_F16", "0")
-    y8 = rq.gemm(_dev(x), w, m).cpu().numpy().reshape(m, n)
-    assert orc.rel_err_row_l2(yh, y8.astype(np.float64)) < 1e-5
+    _check_gemm(rq, orc, Q6K, m, n, k, blk.reshape(-1), x)
+
+
+def test_gemm_q4k_extreme_scales(rq, orc):
+    """Q4_K super-blocks with 6-bit scales and mins at 0 and 63 and codes 0 and 15
+    (the weight operand's range ends and a constant part of either sign)."""
+    m, n, k = 64, 256, 2048
+    rng = np.random.default_rng(6)
+    nb = n * k // 256
+    blk = synth.weights(Q4K, n, k, 7).reshape(nb, 144).copy()
+    blk[:, 4:16] = rng.choice(np.array([0x00, 0xFF], np.uint8), size=(nb, 12))
+    blk[:, 16:144] = rng.choice(np.array([0x00, 0xFF, 0x0F, 0xF0], np.uint8), size=(nb, 128))
+    x = synth.activations(m * k, 8).reshape(m, k)
+    _check_gemm(rq, orc, Q4K, m, n, k, blk.reshape(-1), x)

@@ -91,9 +91,11 @@ def test_gemm_preconditions_fail_before_gpu():
     w = _w(rq, 12, 512, 8)
     rc = L.rfxq_gemm(ctypes.c_void_p(4096), 512 * 3 - 1, ctypes.byref(w), 3, ctypes.c_void_p(4096), None, 0, None)
     assert rc == 12 and "rows*in_features" in L.rfxq_last_error().decode()
-    # Q8_0 MMQ needs K % 256
-    w8 = _w(rq, 8, 96, 8)
-    rc = L.rfxq_gemm(ctypes.c_void_p(4096), 96 * 3, ctypes.byref(w8), 3, ctypes.c_void_p(4096), None, 0, None)
+    # the MMQ kernels need K % 256 (Q4_K / Q6_K always; Q8_0 on the int8
+    # kernels; in f16 mode Q8_0 rows run as GEMVs, which take K % 32)
+    w6 = _w(rq, 14, 256, 8)
+    w6.in_features = 96
+    rc = L.rfxq_gemm(ctypes.c_void_p(4096), 96 * 3, ctypes.byref(w6), 3, ctypes.c_void_p(4096), None, 0, None)
     assert rc == 12 and "multiple of 256" in L.rfxq_last_error().decode()
 
 
