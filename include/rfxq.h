@@ -75,6 +75,50 @@ int rfxq_last_error_code(void);
 /* Load the embedded gfx950 code object on `device` now (otherwise on first use),
  * like the reference's lazy module load (src/aot.rs:136-160, kernels.rs:948-959). */
 int rfxq_init(int device);
+/* ---- options and the GEMM path policy ----------------------------------- */
+
+/* The prefill path's switches. They are read from the environment once, on
+ * first use, with the reference's strict parsing (QuantMmaKernels::from_env,
+ * src/model/kernels.rs:747-802; quant_fused_max_rows, :4180-4194). An
+ * invalid value makes every call that needs the options fail with
+ * RFXQ_ERR_INVALID_INPUT and the reference's message ("REFLEX_QUANT_MMA must be
+ * 1 (the default) or 0, got \"2\""); like the reference, an unparsable
+ * REFLEX_QUANT_FUSED_MAX_ROWS keeps its default. */
+typedef struct rfxq_options {
+    int32_t quant_mma;           /* REFLEX_QUANT_MMA: 1 (default) MMA prefill, 0: every row as a GEMV */
+    uint32_t quant_mma_splits;   /* REFLEX_QUANT_MMA_SPLITS: 0 = chosen per GEMM, else the split-K count */
+    uint32_t quant_mma_max_rows; /* REFLEX_QUANT_MMA_MAX_ROWS: 0 = no cap; above it rows run as GEMVs */
+    uint32_t quant_mma_tile;     /* REFLEX_QUANT_MMA_TILE: 0 = chosen, 64 or 128 rows (int8 kernels) */
+    int32_t mmq_f16;             /* REFLEX_MMQ_F16: 1 (default) f16-activation kernels, 0: int8 (Q8_1) kernels */
+    uint32_t fused_max_rows;     /* REFLEX_QUANT_FUSED_MAX_ROWS (default 16): up to this many rows run as GEMVs */
+} rfxq_options;
+
+/* The current options (the environment's, or the last rfxq_set_options). */
+int rfxq_get_options(rfxq_options* out);
+/* Replace the options for later calls, like the reference's test setters
+ * (QuantMmaKernels::set_enabled / set_splits, kernels.rs:804-830). Calls
+ * already running keep the options they started with. Rejects
+ * (RFXQ_ERR_INVALID_INPUT) quant_mma or mmq_f16 other than 0/1 and a tile
+ * other than 0, 64 or 128. */
+int rfxq_set_options(const rfxq_options* options);
+
+#define RFXQ_PATH_GEMV_ROWS 0  /* one decode GEMV per row (f16 activations) */
+#define RFXQ_PATH_MMQ_INT8 1   /* int8 MMQ kernels on Q8_1 activations */
+#define RFXQ_PATH_MMQ_F16 2    /* f16-activation MMQ kernels (Q4_K, Q6_K) */
+
+/* How rfxq_gemm runs a GEMM: the path, the workgroup tile and the split-K
+ * (splits ranges of sb_per_split super-blocks); tile and splits are 0/1 on the
+ * GEMV path. Counterpart of quant_mma_splits / quant_mma_block_rows /
+ * quant_mma_max_rows (kernels.rs:628-713) and the fused-GEMV crossover
+ * (:2144-2169), re-derived for MI355X; `compute_units` as the device reports. */
+typedef struct rfxq_gemm_policy {
+    uint32_t path;
+    uint32_t tile_m, tile_n;
+    uint32_t splits, sb_per_split;
+} rfxq_gemm_policy;
+int rfxq_gemm_policy_for(uint32_t ggml_type, uint32_t in_features, uint32_t out_features, uint32_t rows,
+                         uint32_t compute_units, rfxq_gemm_policy* out);
+
 /* (elements per block, bytes per block) of a ggml type (src/gguf.rs:366-400). */
 int rfxq_block_dims(uint32_t ggml_type, uint32_t* block_elems, uint32_t* block_bytes);
 

@@ -34,6 +34,25 @@ class RfxqGemvItem(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.POINTER(RfxqWeight)), ("y", ctypes.c_void_p)]
 
 
+class RfxqOptions(ctypes.Structure):
+    """``rfxq_options`` (include/rfxq.h)."""
+
+    _fields_ = [
+        ("quant_mma", ctypes.c_int32),
+        ("quant_mma_splits", ctypes.c_uint32),
+        ("quant_mma_max_rows", ctypes.c_uint32),
+        ("quant_mma_tile", ctypes.c_uint32),
+        ("mmq_f16", ctypes.c_int32),
+        ("fused_max_rows", ctypes.c_uint32),
+    ]
+
+
+class RfxqGemmPolicy(ctypes.Structure):
+    """``rfxq_gemm_policy`` (include/rfxq.h)."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in ("path", "tile_m", "tile_n", "splits", "sb_per_split")]
+
+
 # name -> (restype, argtypes); every symbol declared in include/rfxq.h
 _P, _U32, _U64, _I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
 _WP = ctypes.POINTER(RfxqWeight)
@@ -41,6 +60,9 @@ SIGNATURES = {
     "rfxq_last_error": (ctypes.c_char_p, []),
     "rfxq_last_error_code": (_I, []),
     "rfxq_init": (_I, [_I]),
+    "rfxq_get_options": (_I, [ctypes.POINTER(RfxqOptions)]),
+    "rfxq_set_options": (_I, [ctypes.POINTER(RfxqOptions)]),
+    "rfxq_gemm_policy_for": (_I, [_U32, _U32, _U32, _U32, _U32, ctypes.POINTER(RfxqGemmPolicy)]),
     "rfxq_block_dims": (_I, [_U32, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
     "rfxq_dequantize": (_I, [_U32, _P, _U64, _P, _I, _P]),
     "rfxq_gemv_to": (_I, [_P, _U64, _WP, _P, _P]),

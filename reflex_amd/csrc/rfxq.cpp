@@ -144,6 +144,8 @@ struct Ctx {
     };
     Stage stage[4];
     uint32_t stage_next = 0;
+    std::mutex mu;                // guards ws / tab growth
+    std::vector<void*> retired;  // replaced areas: kept until the process ends
 };
 
 std::mutex g_mu;
@@ -214,24 +216,44 @@ int load_ctx(int device, Ctx** out) {
     return RFXQ_OK;
 }
 
-// Grow-only device area for per-call tables; growth waits for the device
-// (earlier launches may still read the old area).
-int ctx_tables(Ctx* c, uint64_t bytes, void** out) {
-    if (bytes > c->tab_bytes) {
-        if (c->tab) {
-            HIPCHK(hipDeviceSynchronize(), "hipDeviceSynchronize before table area growth");
-            HIPCHK(hipFree(c->tab), "hipFree(table area)");
-            c->tab = nullptr;
-            c->tab_bytes = 0;
-        }
-        const uint64_t sz = std::max<uint64_t>(bytes, 64u << 10);
-        hipError_t e = hipMalloc(&c->tab, sz);
-        if (e != hipSuccess) return fail(RFXQ_ERR_OUT_OF_MEMORY, "table area alloc of %llu bytes: %s",
-                                         (unsigned long long)sz, hipGetErrorString(e));
-        c->tab_bytes = sz;
+// true if `stream` is capturing a graph
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Grow-only device areas shared by a device's calls (the workspace and the
+// per-call tables). A grown area replaces the old one, which stays allocated
+// until the process ends: launches still in flight and graphs captured
+// earlier may hold its address, so no area is ever freed and growth never
+// waits for the device. Growth is refused while `stream` captures a graph (run
+// the call once before capturing, or pass a caller workspace). Calls that use
+// an area without a caller workspace must be ordered on one stream.
+int grow_area(Ctx* c, void** area, uint64_t* size, uint64_t bytes, uint64_t min_bytes, hipStream_t stream,
+              const char* what, void** out) {
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (bytes > *size) {
+        if (capturing(stream))
+            return fail(RFXQ_ERR_INVALID_INPUT,
+                        "%s: needs %llu bytes (has %llu) while the stream captures a graph; run the call once "
+                        "before capturing or pass a workspace",
+                        what, (unsigned long long)bytes, (unsigned long long)*size);
+        const uint64_t sz = std::max<uint64_t>({bytes, 2u * *size, min_bytes});
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess)
+            return fail(RFXQ_ERR_OUT_OF_MEMORY, "%s alloc of %llu bytes: %s", what, (unsigned long long)sz,
+                        hipGetErrorString(e));
+        if (*area) c->retired.push_back(*area);
+        *area = p;
+        *size = sz;
     }
-    *out = c->tab;
+    *out = *area;
     return RFXQ_OK;
+}
+
+int ctx_tables(Ctx* c, uint64_t bytes, void** out, hipStream_t stream) {
+    return grow_area(c, &c->tab, &c->tab_bytes, bytes, 64u << 10, stream, "table area", out);
 }
 
 // Stream-ordered upload of `bytes` from host memory to `dst` through a pinned
@@ -239,6 +261,11 @@ int ctx_tables(Ctx* c, uint64_t bytes, void** out) {
 // stream (the reference's per-expert pageable copies synchronise).
 int stage_upload(Ctx* c, void* dst, const void* src, size_t bytes, hipStream_t stream) {
     if (bytes == 0) return RFXQ_OK;
+    // a captured copy would replay from a staging buffer that later calls reuse
+    if (capturing(stream))
+        return fail(RFXQ_ERR_INVALID_INPUT,
+                    "per-call tables cannot be captured into a graph; use a plan (rfxq_gemv_plan_create / "
+                    "rfxq_gemm_plan_create) or the device-routed MoE entry point");
     Ctx::Stage& s = c->stage[c->stage_next];
     c->stage_next = (c->stage_next + 1u) % 4u;
     if (s.pending) {
@@ -268,24 +295,10 @@ int current_ctx(Ctx** out) {
     return load_ctx(dev, out);
 }
 
-// Grow-only per-device scratch (the reference allocates per call, alloc_out
-// kernels.rs:1001); freed at process exit.
-int ctx_workspace(Ctx* c, uint64_t bytes, void** out) {
-    if (bytes > c->ws_bytes) {
-        if (c->ws) {
-            HIPCHK(hipDeviceSynchronize(), "hipDeviceSynchronize before workspace growth");
-            HIPCHK(hipFree(c->ws), "hipFree(workspace)");
-            c->ws = nullptr;
-            c->ws_bytes = 0;
-        }
-        const uint64_t sz = std::max<uint64_t>(bytes, 1u << 20);
-        hipError_t e = hipMalloc(&c->ws, sz);
-        if (e != hipSuccess) return fail(RFXQ_ERR_OUT_OF_MEMORY, "workspace alloc of %llu bytes: %s",
-                                         (unsigned long long)sz, hipGetErrorString(e));
-        c->ws_bytes = sz;
-    }
-    *out = c->ws;
-    return RFXQ_OK;
+// Per-device scratch for calls without a caller workspace (the reference
+// allocates per call, alloc_out kernels.rs:1001); see grow_area.
+int ctx_workspace(Ctx* c, uint64_t bytes, void** out, hipStream_t stream) {
+    return grow_area(c, &c->ws, &c->ws_bytes, bytes, 1u << 20, stream, "workspace", out);
 }
 
 int launch(hipFunction_t f, uint32_t grid, uint32_t lds, hipStream_t stream, void* args, size_t args_size,
@@ -354,13 +367,121 @@ int check_weight(const rfxq_weight* w, const char* what) {
     return RFXQ_OK;
 }
 
-uint32_t env_u32(const char* name, uint32_t dflt) {
-    const char* v = std::getenv(name);
-    if (!v || !*v) return dflt;
-    char* end = nullptr;
-    unsigned long x = std::strtoul(v, &end, 10);
-    if (end == v || *end) return dflt;
-    return (uint32_t)x;
+// ------------------------------------------------------------------ options
+
+// The prefill path's switches (rfxq_options), read from the environment once,
+// on first use, with the reference's strict parsing
+// (QuantMmaKernels::from_env, src/model/kernels.rs:747-802; quant_fused_max_rows,
+// :4180-4194): an invalid value is an RFXQ_ERR_INVALID_INPUT error, with the
+// reference's message, from every call that needs the options.
+struct Options {
+    rfxq_options o;
+    int code = RFXQ_OK;
+    std::string msg;
+};
+
+// Rust's `str::parse::<usize>`: an optional '+', then decimal digits only;
+// values beyond 32 bits saturate (they act as "no limit" here)
+bool parse_usize(const char* v, uint32_t* out) {
+    if (*v == '+') v++;
+    if (!*v) return false;
+    uint64_t x = 0;
+    for (; *v; v++) {
+        if (*v < '0' || *v > '9') return false;
+        x = std::min<uint64_t>(x * 10u + (uint64_t)(*v - '0'), 0xFFFFFFFFull);
+    }
+    *out = (uint32_t)x;
+    return true;
+}
+
+Options load_options() {
+    Options O;
+    rfxq_options& o = O.o;
+    o.quant_mma = 1;
+    o.mmq_f16 = 1;
+    o.fused_max_rows = 16;
+    auto env = [](const char* name) -> const char* {
+        const char* v = std::getenv(name);
+        return v && *v ? v : nullptr;  // unset and "" both take the default
+    };
+    auto bad = [&](const char* name, const char* want, const char* v) {
+        if (O.code != RFXQ_OK) return;  // the first bad variable is reported
+        char buf[320];
+        std::snprintf(buf, sizeof buf, "%s must be %s, got \"%s\"", name, want, v);
+        O.code = RFXQ_ERR_INVALID_INPUT;
+        O.msg = buf;
+    };
+    if (const char* v = env("REFLEX_QUANT_MMA")) {
+        if (!std::strcmp(v, "0")) o.quant_mma = 0;
+        else if (std::strcmp(v, "1")) bad("REFLEX_QUANT_MMA", "1 (the default) or 0", v);
+    }
+    if (const char* v = env("REFLEX_QUANT_MMA_SPLITS")) {
+        if (!parse_usize(v, &o.quant_mma_splits) || o.quant_mma_splits == 0) {
+            o.quant_mma_splits = 0;
+            bad("REFLEX_QUANT_MMA_SPLITS", "a positive integer", v);
+        }
+    }
+    if (const char* v = env("REFLEX_QUANT_MMA_MAX_ROWS")) {
+        if (!parse_usize(v, &o.quant_mma_max_rows)) {
+            o.quant_mma_max_rows = 0;
+            bad("REFLEX_QUANT_MMA_MAX_ROWS", "a non-negative integer", v);
+        }
+    }
+    if (const char* v = env("REFLEX_QUANT_MMA_TILE")) {
+        if (!std::strcmp(v, "64")) o.quant_mma_tile = 64;
+        else if (!std::strcmp(v, "128")) o.quant_mma_tile = 128;
+        else bad("REFLEX_QUANT_MMA_TILE", "64 or 128", v);
+    }
+    // this build's switch, parsed like REFLEX_QUANT_MMA
+    if (const char* v = env("REFLEX_MMQ_F16")) {
+        if (!std::strcmp(v, "0")) o.mmq_f16 = 0;
+        else if (std::strcmp(v, "1")) bad("REFLEX_MMQ_F16", "1 (the default) or 0", v);
+    }
+    // the reference keeps its default for a value that does not parse
+    // (quant_fused_max_rows, kernels.rs:4186-4194)
+    if (const char* v = env("REFLEX_QUANT_FUSED_MAX_ROWS")) {
+        if (!parse_usize(v, &o.fused_max_rows)) o.fused_max_rows = 16;
+    }
+    return O;
+}
+
+// the process's options: the environment's on first use, rfxq_set_options' after
+std::mutex g_opt_mu;
+Options& options_locked() {
+    static Options O = load_options();
+    return O;
+}
+
+// the options, or the environment's parse error
+int get_options(rfxq_options* out) {
+    Options O;
+    {
+        std::lock_guard<std::mutex> lk(g_opt_mu);
+        O = options_locked();
+    }
+    if (O.code != RFXQ_OK) return fail(O.code, "%s", O.msg.c_str());
+    *out = O.o;
+    return RFXQ_OK;
+}
+
+// a snapshot of the options of a call that already checked them (get_options)
+rfxq_options opt() {
+    std::lock_guard<std::mutex> lk(g_opt_mu);
+    return options_locked().o;
+}
+bool options_ok() {
+    std::lock_guard<std::mutex> lk(g_opt_mu);
+    return options_locked().code == RFXQ_OK;
+}
+
+int check_options(const rfxq_options& o) {
+    if (o.quant_mma != 0 && o.quant_mma != 1)
+        return fail(RFXQ_ERR_INVALID_INPUT, "quant_mma must be 0 or 1, got %d", o.quant_mma);
+    if (o.quant_mma_tile != 0 && o.quant_mma_tile != 64 && o.quant_mma_tile != 128)
+        return fail(RFXQ_ERR_INVALID_INPUT, "quant_mma_tile must be 0, 64 or 128, got %u", o.quant_mma_tile);
+    if (o.mmq_f16 != 0 && o.mmq_f16 != 1)
+        return fail(RFXQ_ERR_INVALID_INPUT, "mmq_f16 must be 0 or 1, got %d", o.mmq_f16);
+    return RFXQ_OK;
 }
 
 // ------------------------------------------------------------------ GEMV planning
@@ -407,8 +528,7 @@ void gemv_shape(GemvItem* it, uint32_t k) {
     GemvDesc* d = &it->d;
     const uint32_t units = d->type == RFXQ_TYPE_Q8_0 ? k / 32u : k / 64u;
     uint32_t lpr_log2 = 0;
-    const uint32_t lpr_max = std::min<uint32_t>(6u, env_u32("RFXQ_GEMV_LPR_LOG2_MAX", 6));
-    while (lpr_log2 < lpr_max && (units % (2u << lpr_log2)) == 0) lpr_log2++;
+    while (lpr_log2 < 6u && (units % (2u << lpr_log2)) == 0) lpr_log2++;
     if (lpr_log2 < 2) lpr_log2 = 2;  // >= 4 lanes per row (units is always a multiple of 4 here)
     d->k = k;
     d->lpr_log2 = lpr_log2;
@@ -418,7 +538,7 @@ void gemv_shape(GemvItem* it, uint32_t k) {
     it->passes = (units >> lpr_log2) > 1u;
 }
 
-// Workgroups of a launch: about RFXQ_GEMV_WG_KB (default 128) KB of weights
+// Workgroups of a launch: about 128 KB of weights
 // each, so the x staging is amortised and each wave's load ring reaches a
 // steady state; launches too small for 2 workgroups per CU at that size use
 // smaller ranges (down to one iteration). A launch with more workgroups than
@@ -436,7 +556,7 @@ uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) {
         total_bytes += it.iters * it.iter_bytes;
         kmax = std::max(kmax, it.d.k);
     }
-    const uint64_t kb = std::max<uint32_t>(1u, env_u32("RFXQ_GEMV_WG_KB", 128));
+    const uint64_t kb = 128u;
     uint64_t g = (total_bytes + kb * 1024u - 1u) / (kb * 1024u);
     g = std::max<uint64_t>(g, 2u * (uint32_t)c->cus);
     // LDS per workgroup: the 32 KB weight ring, x and its sums, and up to 4 KB of row results
@@ -511,7 +631,7 @@ int gemv_launch_table(Ctx* c, const std::vector<GemvItem>& v, uint64_t at, hipSt
     for (size_t i = 0; i < v.size(); i++) std::memcpy(host.data() + i * sizeof(GemvDesc), &v[i].d, sizeof(GemvDesc));
     std::memcpy(host.data() + tb, ranges.data(), rb);
     void* area;
-    if (int rc = ctx_tables(c, at + host.size(), &area)) return rc;
+    if (int rc = ctx_tables(c, at + host.size(), &area, stream)) return rc;
     uint8_t* dst = static_cast<uint8_t*>(area) + at;
     if (int rc = stage_upload(c, dst, host.data(), host.size(), stream)) return rc;
     a.ndesc = (uint32_t)v.size();
@@ -584,24 +704,71 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 // selects the int8 MMQ kernels (Q8_1 activations, per-32 int32 block dots).
 // Q8_0 always takes the int8 kernels.
 constexpr uint32_t kMmqThreads = 256;  // every MMQ kernel's workgroup
-bool mmq_f16() { return env_u32("REFLEX_MMQ_F16", 1) != 0; }
+bool mmq_f16() { return opt().mmq_f16 != 0; }
+
+bool f16_capable(uint32_t ty, uint64_t k, uint64_t n, uint64_t rows) {
+    const uint64_t nsb = k / 256u;
+    uint64_t bb;
+    if (ty == RFXQ_TYPE_Q4_K) bb = 144u;
+    else if (ty == RFXQ_TYPE_Q6_K && nsb % 2u == 0u) bb = 210u;
+    else return false;
+    const uint64_t lim = 0xF0000000ull;  // every buffer offset of the kernel's loads fits in 32 bits
+    return (n + 256u) * nsb * bb < lim && (rows + 128u) * k * 2u < lim;
+}
 
 // an f16 kernel for this GEMM: f16 mode, Q4_K or Q6_K (the Q6_K kernel needs
 // an even number of super-blocks per row, so that rows start 4-byte aligned),
 // and every buffer offset of the kernel's loads fits in 32 bits
 bool f16_kernel(const rfxq_weight* w, uint32_t rows) {
-    if (!mmq_f16()) return false;
-    const uint64_t k = w->in_features, n = w->out_features, nsb = k / 256u;
-    uint64_t bb;
-    if (w->ggml_type == RFXQ_TYPE_Q4_K) bb = 144u;
-    else if (w->ggml_type == RFXQ_TYPE_Q6_K && nsb % 2u == 0u) bb = 210u;
-    else return false;
-    const uint64_t lim = 0xF0000000ull;
-    return (n + 256u) * nsb * bb < lim && ((uint64_t)rows + 128u) * k * 2u < lim;
+    return mmq_f16() && f16_capable(w->ggml_type, w->in_features, w->out_features, rows);
 }
 
 // weight columns per workgroup tile (rows: kMmqBM, or 64 for the int8 *_m64 kernels)
 uint32_t tile_bn(uint32_t ty, bool f16) { return f16 && ty == RFXQ_TYPE_Q4_K ? 256u : 128u; }
+
+// How a GEMM of `rows` rows runs (Model::gemm's choice between the fused GEMV,
+// the MMA kernel and its split-K, kernels.rs:628-713 quant_mma_splits /
+// block_rows / max_rows and :2144-2169, re-derived for MI355X):
+// - one GEMV per row (PATH_GEMV_ROWS) for a single row, with the MMA path off
+//   (REFLEX_QUANT_MMA=0), above REFLEX_QUANT_MMA_MAX_ROWS, up to
+//   REFLEX_QUANT_FUSED_MAX_ROWS rows (default 16: a 128-row tile would be
+//   mostly idle), and for Q8_0 in f16 mode (no f16-activation Q8_0 kernel; the
+//   int8 format's error floor exceeds the north star's bound) or with
+//   in_features not a multiple of 256;
+// - otherwise the f16-activation kernels (PATH_MMQ_F16: Q4_K, and Q6_K with an
+//   even super-block count per row) or the int8 kernels (PATH_MMQ_INT8; 64-row
+//   tiles with REFLEX_QUANT_MMA_TILE=64);
+// - split-K: none once the tiles cover half the CUs (each CU holds two
+//   workgroups; a split costs a partials round trip and a reduce launch),
+//   else enough splits for about two workgroups per CU, each of at least two
+//   super-blocks; REFLEX_QUANT_MMA_SPLITS forces the count.
+enum : uint32_t { PATH_GEMV_ROWS = RFXQ_PATH_GEMV_ROWS, PATH_MMQ_INT8 = RFXQ_PATH_MMQ_INT8, PATH_MMQ_F16 = RFXQ_PATH_MMQ_F16 };
+
+
+rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o) {
+    rfxq_gemm_policy p;
+    std::memset(&p, 0, sizeof p);
+    p.splits = 1;
+    const bool gemv = rows <= 1 || !o.quant_mma || (o.quant_mma_max_rows && rows > o.quant_mma_max_rows) ||
+                      rows <= o.fused_max_rows || k % 256u != 0 || (ty == RFXQ_TYPE_Q8_0 && o.mmq_f16);
+    if (gemv) {
+        p.path = PATH_GEMV_ROWS;
+        return p;
+    }
+    const bool f16 = o.mmq_f16 && f16_capable(ty, k, n, rows);
+    p.path = f16 ? PATH_MMQ_F16 : PATH_MMQ_INT8;
+    p.tile_m = !f16 && o.quant_mma_tile == 64 ? 64u : kMmqBM;
+    p.tile_n = tile_bn(ty, f16);
+    const uint32_t nsb = k / 256u;
+    const uint32_t tiles = ((rows + p.tile_m - 1u) / p.tile_m) * ((n + p.tile_n - 1u) / p.tile_n);
+    uint32_t splits = 1;
+    if (o.quant_mma_splits) splits = o.quant_mma_splits;
+    else if (2u * tiles < std::max(cus, 1u)) splits = std::min((2u * cus + tiles - 1u) / tiles, std::max(1u, nsb / 2u));
+    splits = std::min(std::max(1u, splits), nsb);
+    p.sb_per_split = (nsb + splits - 1u) / splits;
+    p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
+    return p;
+}
 
 // One activation in the layouts its GEMMs read, each 256-byte aligned:
 // int8 (xq [rows][k], xds [rows][k/32] = d | s << 16) and f16 (xh [rows][k],
@@ -721,36 +888,26 @@ int check_mmq_weight(const rfxq_weight* w, const char* what) {
     return RFXQ_OK;
 }
 
-// Split-K: a GEMM whose tiles leave CUs idle splits K into ranges of whole
-// super-blocks (REFLEX_QUANT_MMA_SPLITS sets the split count).
-uint32_t split_count(const Ctx* c, uint32_t tiles, uint32_t nsb) {
-    const uint32_t cus = c ? (uint32_t)c->cus : 256u;
-    uint32_t splits = 1;
-    if (tiles < cus) splits = std::min(nsb, (2u * cus + tiles - 1u) / tiles);
-    splits = std::max(1u, env_u32("REFLEX_QUANT_MMA_SPLITS", splits));
-    return std::min(splits, nsb);
-}
-
 struct GemmPlan {
+    rfxq_gemm_policy pol;
     bool f16 = false;
-    uint32_t splits = 1, sb_per_split = 1, tiles_m = 1, tiles_n = 1;
+    uint32_t tiles_m = 1, tiles_n = 1;
     ActLayout act;
     uint64_t off_part = 0, total = 0;
 };
 
-GemmPlan plan_gemm(const Ctx* c, const rfxq_weight* w, uint32_t rows) {
+// an MMQ plan for a GEMM the policy sends to an MMQ path
+GemmPlan plan_gemm(const Ctx* c, const rfxq_weight* w, uint32_t rows, const rfxq_options& o) {
     GemmPlan p;
-    const uint32_t k = w->in_features, n = w->out_features, nsb = k / 256u;
-    p.f16 = f16_kernel(w, rows);
-    p.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-    const uint32_t bn = tile_bn(w->ggml_type, p.f16);
-    p.tiles_n = (n + bn - 1u) / bn;
-    const uint32_t splits = split_count(c, p.tiles_m * p.tiles_n, nsb);
-    p.sb_per_split = (nsb + splits - 1u) / splits;
-    p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
+    const uint32_t k = w->in_features, n = w->out_features;
+    p.pol = gemm_policy(w->ggml_type, k, n, rows, c ? (uint32_t)c->cus : 256u, o);
+    p.f16 = p.pol.path == PATH_MMQ_F16;
+    if (p.pol.path == PATH_GEMV_ROWS) return p;  // no MMQ launch: tiles, layouts and workspace stay 0
+    p.tiles_m = (rows + p.pol.tile_m - 1u) / p.pol.tile_m;
+    p.tiles_n = (n + p.pol.tile_n - 1u) / p.pol.tile_n;
     p.act = act_layout_sel(rows, k, !p.f16, p.f16);
     p.off_part = p.act.total;
-    p.total = p.off_part + (p.splits > 1 ? align256((uint64_t)p.splits * rows * n * 4u) : 0u);
+    p.total = p.off_part + (p.pol.splits > 1 ? align256((uint64_t)p.pol.splits * rows * n * 4u) : 0u);
     return p;
 }
 
@@ -774,7 +931,7 @@ int gemm_run(Ctx* c, const GemmPlan& p, const uint8_t* act, const ActLayout& L, 
     std::memset(&d, 0, sizeof d);
     d.w = w->data;
     act_desc(&d, act, L, p.f16, k);
-    d.y = p.splits > 1 ? part : y;
+    d.y = p.pol.splits > 1 ? part : y;
     d.m = rows;
     d.n = n;
     d.k = k;
@@ -782,20 +939,21 @@ int gemm_run(Ctx* c, const GemmPlan& p, const uint8_t* act, const ActLayout& L, 
     d.ldy = n;
     d.tiles_m = p.tiles_m;
     d.tiles_n = p.tiles_n;
-    d.splits = p.splits;
-    d.sb_per_split = p.sb_per_split;
-    const uint32_t wgs = p.tiles_m * p.tiles_n * p.splits;
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, p.f16)) return rc;
-    if (p.splits > 1)
-        if (int rc = launch_reduce(c, part, y, (uint64_t)rows * n, p.splits, stream)) return rc;
+    d.splits = p.pol.splits;
+    d.sb_per_split = p.pol.sb_per_split;
+    const uint32_t wgs = p.tiles_m * p.tiles_n * p.pol.splits;
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, p.f16, p.pol.tile_m == 64u))
+        return rc;
+    if (p.pol.splits > 1)
+        if (int rc = launch_reduce(c, part, y, (uint64_t)rows * n, p.pol.splits, stream)) return rc;
     return RFXQ_OK;
 }
 
 int gemm_impl(Ctx* c, const float* x, const rfxq_weight* w, uint32_t rows, float* y, void* ws, uint64_t ws_bytes,
-              hipStream_t stream) {
-    const GemmPlan p = plan_gemm(c, w, rows);
+              const rfxq_options& o, hipStream_t stream) {
+    const GemmPlan p = plan_gemm(c, w, rows, o);
     if (!ws) {
-        if (int rc = ctx_workspace(c, p.total, &ws)) return rc;
+        if (int rc = ctx_workspace(c, p.total, &ws, stream)) return rc;
     } else if (ws_bytes < p.total) {
         return fail(RFXQ_ERR_INVALID_INPUT, "gemm: workspace of %llu bytes, needs %llu",
                     (unsigned long long)ws_bytes, (unsigned long long)p.total);
@@ -817,7 +975,10 @@ int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
 
 // GEMMs of one row count over several weights, grouped: each distinct
 // activation (by address) is brought into the layouts its GEMMs read once,
-// and each weight type runs as one MMQ launch over all of its GEMMs.
+// and each MMQ kernel runs as one launch over all of its GEMMs. Each GEMM
+// takes the single-GEMM policy's path (gemm_policy); GEMMs on the GEMV path
+// run as one GEMV per row in one table-driven launch.
+constexpr uint32_t kGroupKernels = 9;  // type_index + 3 * variant (0: int8, 1: int8 64-row, 2: f16)
 struct GemmGroup {
     struct Act {
         const float* x;
@@ -826,13 +987,12 @@ struct GemmGroup {
         ActLayout L;
         bool need_i8 = false, need_h = false;
     };
-    bool f16[3] = {false, false, false};  // per type_index: the f16 kernel
     std::vector<Act> acts;
-    std::vector<MmqDesc> descs[3];  // per type_index
-    std::vector<uint32_t> act_of[3];  // per descriptor: its activation
-    uint32_t wgs[3] = {0, 0, 0};
-    // GEMMs split along K (a type with fewer tiles than two per CU):
-    // partials at workspace offset `off`, reduced into y after the type's launch
+    std::vector<MmqDesc> descs[kGroupKernels];
+    std::vector<uint32_t> act_of[kGroupKernels];  // per descriptor: its activation
+    uint32_t wgs[kGroupKernels] = {};
+    // GEMMs split along K (a kernel with fewer tiles than two per CU):
+    // partials at workspace offset `off`, reduced into y after the kernel's launch
     struct Reduce {
         uint32_t t, i;
         uint64_t off;
@@ -843,37 +1003,32 @@ struct GemmGroup {
     };
     std::vector<Reduce> reduces;
     uint64_t ws_bytes = 0;
-    // f16 mode: Q8_0 GEMMs run as one GEMV per row (f16 activations; there
-    // is no f16-activation Q8_0 MMQ kernel and the int8 format's error floor
-    // exceeds the north star's bound)
-    std::vector<rfxq_gemv_item> q8_rows;
+    std::vector<rfxq_gemv_item> gemv_rows;  // GEMMs on the GEMV path, one item per row
 };
+
+bool group_f16(uint32_t g) { return g >= 6u; }
+bool group_m64(uint32_t g) { return g >= 3u && g < 6u; }
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
-    // the f16 kernel for the group's GEMMs of one type only if every one of them can take it
-    g->f16[0] = g->f16[1] = mmq_f16();
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    std::vector<uint32_t> item_act(count, ~0u), item_kernel(count, 0);
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
-        if (int rc = check_mmq_weight(it.w, "gemm group")) return rc;
+        if (int rc = check_weight(it.w, "gemm group")) return rc;
         if (!it.x || !it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: item %u has a NULL x or y", i);
         if (reinterpret_cast<uintptr_t>(it.x) % 16u)
             return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not 16-byte aligned", i);
-        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !f16_kernel(it.w, rows)) g->f16[type_index(it.w->ggml_type)] = false;
-    }
-    // activations and the layouts they need
-    const bool q8_gemv = mmq_f16();
-    std::vector<uint32_t> item_act(count);
-    for (uint32_t i = 0; i < count; i++) {
-        const rfxq_gemm_item& it = items[i];
-        if (q8_gemv && it.w->ggml_type == RFXQ_TYPE_Q8_0) {
+        const uint32_t k = it.w->in_features;
+        const rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o);
+        if (pol.path == PATH_GEMV_ROWS) {
             for (uint32_t r = 0; r < rows; r++)
-                g->q8_rows.push_back({it.x + (uint64_t)r * it.w->in_features, it.w,
-                                      it.y + (uint64_t)r * it.w->out_features});
-            item_act[i] = ~0u;
+                g->gemv_rows.push_back({it.x + (uint64_t)r * k, it.w, it.y + (uint64_t)r * it.w->out_features});
             continue;
         }
-        const uint32_t k = it.w->in_features;
+        const bool f16 = pol.path == PATH_MMQ_F16;
+        item_kernel[i] = type_index(it.w->ggml_type) + 3u * (f16 ? 2u : pol.tile_m == 64u ? 1u : 0u);
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
@@ -885,7 +1040,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
         }
         item_act[i] = (uint32_t)ai;
-        if (g->f16[type_index(it.w->ggml_type)]) g->acts[ai].need_h = true;
+        if (f16) g->acts[ai].need_h = true;
         else g->acts[ai].need_i8 = true;
     }
     for (auto& a : g->acts) {
@@ -894,23 +1049,23 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         g->ws_bytes += a.L.total;
     }
     for (uint32_t i = 0; i < count; i++) {
-        const rfxq_gemm_item& it = items[i];
         if (item_act[i] == ~0u) continue;
-        const uint32_t k = it.w->in_features, t = type_index(it.w->ggml_type);
+        const rfxq_gemm_item& it = items[i];
+        const uint32_t k = it.w->in_features, t = item_kernel[i];
         const GemmGroup::Act& a = g->acts[item_act[i]];
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;
         // offsets until the workspace is known
-        act_desc(&d, reinterpret_cast<const uint8_t*>(a.off), a.L, g->f16[t], k);
+        act_desc(&d, reinterpret_cast<const uint8_t*>(a.off), a.L, group_f16(t), k);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
         d.k = k;
         d.type = it.w->ggml_type;
         d.ldy = d.n;
-        d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-        const uint32_t bn = tile_bn(d.type, g->f16[t]);
+        const uint32_t bm = group_m64(t) ? 64u : kMmqBM, bn = tile_bn(d.type, group_f16(t));
+        d.tiles_m = (rows + bm - 1u) / bm;
         d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = k / 256u;
@@ -919,18 +1074,18 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         g->descs[t].push_back(d);
         g->act_of[t].push_back(item_act[i]);
     }
-    // a type whose tiles would leave CUs idle splits K (fixed-order reduce)
-    // (REFLEX_QUANT_MMA_SPLITS sets the split count, as for single GEMMs)
-    const uint32_t forced = env_u32("REFLEX_QUANT_MMA_SPLITS", 0);
-    for (uint32_t t = 0; t < 3; t++) {
+    // a kernel whose tiles would leave CUs idle splits K (fixed-order reduce);
+    // REFLEX_QUANT_MMA_SPLITS sets the split count, as for single GEMMs
+    const uint32_t forced = o.quant_mma_splits;
+    for (uint32_t t = 0; t < kGroupKernels; t++) {
         auto& v = g->descs[t];
-        if (v.empty() || (!forced && g->wgs[t] >= 2u * cus)) continue;
+        if (v.empty() || (!forced && 2u * g->wgs[t] >= cus)) continue;
         const uint32_t want = forced ? forced : (2u * cus + g->wgs[t] - 1u) / g->wgs[t];
         uint32_t wg = 0;
         for (uint32_t i = 0; i < v.size(); i++) {
             MmqDesc& d = v[i];
             const uint32_t nsb = d.k / 256u;
-            const uint32_t s = std::min(want, nsb);
+            const uint32_t s = std::min(want, forced ? nsb : std::max(1u, nsb / 2u));
             d.sb_per_split = (nsb + s - 1u) / s;
             d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
             if (d.splits > 1u) {
@@ -946,7 +1101,15 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
     return RFXQ_OK;
 }
 
-// the split-K reduces of type t
+// the MMQ launch of kernel t of a group (descriptors inline or from `table`)
+int launch_group_kernel(Ctx* c, const GemmGroup& g, uint32_t t, const MmqDesc* table, hipStream_t stream) {
+    const auto& v = g.descs[t];
+    if (v.empty()) return RFXQ_OK;
+    return launch_mmq(c, v[0].type, v.data(), (uint32_t)v.size(), table, g.wgs[t], false, stream, group_f16(t),
+                      group_m64(t));
+}
+
+// the split-K reduces of kernel t
 int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream) {
     for (const auto& r : g.reduces)
         if (r.t == t)
@@ -956,11 +1119,11 @@ int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream
 
 // workspace offsets -> addresses
 void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
-    for (uint32_t t = 0; t < 3; t++)
+    for (uint32_t t = 0; t < kGroupKernels; t++)
         for (size_t i = 0; i < g->descs[t].size(); i++) {
             MmqDesc& d = g->descs[t][i];
             const GemmGroup::Act& a = g->acts[g->act_of[t][i]];
-            act_desc(&d, ws + a.off, a.L, g->f16[t], d.k);
+            act_desc(&d, ws + a.off, a.L, group_f16(t), d.k);
         }
     for (auto& r : g->reduces) {
         r.part = reinterpret_cast<float*>(ws + r.off);
@@ -1054,12 +1217,12 @@ struct rfxq_gemm_plan {
     uint32_t rows;
     void* dev = nullptr;  // quantized activations, one descriptor table per weight type, the quantize table
     GemmGroup g;
-    MmqDesc* table[3] = {nullptr, nullptr, nullptr};
+    MmqDesc* table[kGroupKernels] = {};
     QuantDesc* qtable = nullptr;  // int8 layouts: one rfxq_quantize_q8_1_multi launch
     uint32_t nq = 0, qgrid = 0;
     ActF16Desc* htable = nullptr;  // f16 layouts: one rfxq_act_f16_multi launch
     uint32_t nh = 0, hgrid = 0;
-    rfxq_gemv_plan* q8 = nullptr;  // Q8_0 rows as GEMVs (f16 mode)
+    rfxq_gemv_plan* q8 = nullptr;  // GEMMs on the GEMV path, one item per row
 };
 
 struct rfxq_gemv_plan {
@@ -1086,6 +1249,36 @@ int rfxq_init(int device) {
     const int rc = load_ctx(device, &c);
     (void)hipSetDevice(prev);
     return rc ? rc : ok();
+}
+
+int rfxq_get_options(rfxq_options* out) {
+    if (!out) return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_get_options: NULL output");
+    if (int rc = get_options(out)) return rc;
+    return ok();
+}
+
+int rfxq_set_options(const rfxq_options* o) {
+    if (!o) return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_set_options: NULL options");
+    if (int rc = check_options(*o)) return rc;
+    std::lock_guard<std::mutex> lk(g_opt_mu);
+    Options& O = options_locked();
+    O.o = *o;
+    O.code = RFXQ_OK;
+    O.msg.clear();
+    return ok();
+}
+
+int rfxq_gemm_policy_for(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, rfxq_gemm_policy* out) {
+    if (!out) return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_gemm_policy_for: NULL output");
+    uint32_t qk = 0, bb = 0;
+    if (!block_dims(ty, &qk, &bb) || !(ty == RFXQ_TYPE_Q4_K || ty == RFXQ_TYPE_Q6_K || ty == RFXQ_TYPE_Q8_0))
+        return fail(RFXQ_ERR_GGUF, "rfxq_gemm_policy_for: ggml_type=%u has no GEMM", ty);
+    if (k == 0 || n == 0 || rows == 0 || cus == 0)
+        return fail(RFXQ_ERR_INVALID_INPUT, "rfxq_gemm_policy_for: zero dimension");
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    *out = gemm_policy(ty, k, n, rows, cus, o);
+    return ok();
 }
 
 int rfxq_block_dims(uint32_t ty, uint32_t* qk, uint32_t* bb) {
@@ -1272,7 +1465,9 @@ uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows) {
         auto it = g_ctx.find(dev);
         if (it != g_ctx.end()) c = it->second.get();
     }
-    return plan_gemm(c, w, rows).total;
+    if (!options_ok()) return 0;
+    const GemmPlan p = plan_gemm(c, w, rows, opt());
+    return p.pol.path == PATH_GEMV_ROWS ? 0 : p.total;
 }
 
 int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
@@ -1283,14 +1478,15 @@ int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t row
                     (unsigned long long)rows * w->in_features);
     if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm: x or y is NULL");
     if (rows == 1) return rfxq_gemv_to(x, x_len, w, y, stream);
-    if (env_u32("REFLEX_QUANT_MMA", 1) == 0) return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
-    // f16 mode: Q8_0 rows as GEMVs (f16 activations), as in grouped GEMMs
-    if (w->ggml_type == RFXQ_TYPE_Q8_0 && mmq_f16()) return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    if (gemm_policy(w->ggml_type, w->in_features, w->out_features, rows, 256u, o).path == PATH_GEMV_ROWS)
+        return rfxq_gemv_rows(x, x_len, w, rows, y, stream);
     if (int rc = check_mmq_weight(w, "gemm")) return rc;
     if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemm: x is not 16-byte aligned");
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    if (int rc = gemm_impl(c, x, w, rows, y, workspace, workspace_bytes, stream)) return rc;
+    if (int rc = gemm_impl(c, x, w, rows, y, workspace, workspace_bytes, o, stream)) return rc;
     return ok();
 }
 
@@ -1301,11 +1497,11 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
     GemmGroup g;
     if (int rc = build_gemm_group(items, count, rows, &g, (uint32_t)c->cus)) return rc;
     void* ws = nullptr;
-    if (int rc = ctx_workspace(c, g.ws_bytes, &ws)) return rc;
+    if (int rc = ctx_workspace(c, g.ws_bytes, &ws, stream)) return rc;
     bind_gemm_group(&g, static_cast<uint8_t*>(ws));
     if (int rc = run_gemm_quant(c, g, static_cast<uint8_t*>(ws), rows, stream)) return rc;
     // descriptors inline, kMmqInline per launch
-    for (uint32_t t = 0; t < 3; t++) {
+    for (uint32_t t = 0; t < kGroupKernels; t++) {
         auto& v = g.descs[t];
         for (size_t i0 = 0; i0 < v.size(); i0 += kMmqInline) {
             const uint32_t cnt = (uint32_t)std::min<size_t>(kMmqInline, v.size() - i0);
@@ -1316,12 +1512,13 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n * d[j].splits;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, g.f16[t])) return rc;
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_m64(t)))
+                return rc;
         }
         if (int rc = run_group_reduces(c, g, t, stream)) return rc;
     }
-    if (!g.q8_rows.empty())
-        if (int rc = gemv_items(c, g.q8_rows.data(), (uint32_t)g.q8_rows.size(), stream)) return rc;
+    if (!g.gemv_rows.empty())
+        if (int rc = gemv_items(c, g.gemv_rows.data(), (uint32_t)g.gemv_rows.size(), stream)) return rc;
     return ok();
 }
 
@@ -1407,13 +1604,24 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
     if (!y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1: y is NULL");
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    const GemmPlan p = plan_gemm(c, w, rows);
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    if (gemm_policy(w->ggml_type, k, n, rows, (uint32_t)c->cus, o).path == PATH_GEMV_ROWS) {
+        // a buffer holds no f32 copy for GEMVs: its few rows run on the MMQ kernel
+        // (f16 layout when the weight allows it, else int8)
+        o.fused_max_rows = 0;
+        o.quant_mma = 1;
+        o.quant_mma_max_rows = 0;
+        o.mmq_f16 = o.mmq_f16 && w->ggml_type != RFXQ_TYPE_Q8_0;
+    }
+    // one row plans as two (same tiles): the policy sends single rows to the GEMV
+    const GemmPlan p = plan_gemm(c, w, std::max(rows, 2u), o);
     float* part = nullptr;
-    if (p.splits > 1) {
-        const uint64_t need = (uint64_t)p.splits * rows * n * 4u;
+    if (p.pol.splits > 1) {
+        const uint64_t need = (uint64_t)p.pol.splits * rows * n * 4u;
         void* ws = workspace;
         if (!ws) {
-            if (int rc = ctx_workspace(c, need, &ws)) return rc;
+            if (int rc = ctx_workspace(c, need, &ws, stream)) return rc;
         } else if (workspace_bytes < need) {
             return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1: workspace of %llu bytes, needs %llu",
                         (unsigned long long)workspace_bytes, (unsigned long long)need);
@@ -1428,38 +1636,42 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
 int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, hipStream_t stream) {
     if (count == 0) return ok();
     if (!items) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: items is NULL");
-    bool f16[3] = {mmq_f16(), mmq_f16(), false};
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_q8_1_item& it = items[i];
         if (int rc = check_mmq_weight(it.w, "gemm_q8_1_batch")) return rc;
         if (int rc = check_act(it.act, rows, it.w->in_features, "gemm_q8_1_batch")) return rc;
         if (!it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: item %u has a NULL y", i);
-        if (it.w->ggml_type != RFXQ_TYPE_Q8_0 && !f16_kernel(it.w, rows)) f16[type_index(it.w->ggml_type)] = false;
     }
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    std::vector<MmqDesc> descs[3];
+    // a buffer holds both layouts: f16 kernels where the weight allows them, else int8
+    std::vector<MmqDesc> descs[kGroupKernels];
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_q8_1_item& it = items[i];
-        const uint32_t k = it.w->in_features, t = type_index(it.w->ggml_type);
+        const uint32_t k = it.w->in_features;
+        const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, it.w->out_features, rows);
+        const bool m64 = !f16 && o.quant_mma_tile == 64u;
+        const uint32_t t = type_index(it.w->ggml_type) + 3u * (f16 ? 2u : m64 ? 1u : 0u);
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;
-        act_desc(&d, static_cast<const uint8_t*>(it.act), act_layout(rows, k), f16[t], k);
+        act_desc(&d, static_cast<const uint8_t*>(it.act), act_layout(rows, k), f16, k);
         d.y = it.y;
         d.m = rows;
         d.n = it.w->out_features;
         d.k = k;
         d.type = it.w->ggml_type;
         d.ldy = d.n;
-        d.tiles_m = (rows + kMmqBM - 1u) / kMmqBM;
-        const uint32_t bn = tile_bn(d.type, f16[t]);
+        const uint32_t bm = m64 ? 64u : kMmqBM, bn = tile_bn(d.type, f16);
+        d.tiles_m = (rows + bm - 1u) / bm;
         d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = k / 256u;
         descs[t].push_back(d);
     }
-    for (uint32_t t = 0; t < 3; t++) {
+    for (uint32_t t = 0; t < kGroupKernels; t++) {
         auto& v = descs[t];
         for (size_t i0 = 0; i0 < v.size(); i0 += kMmqInline) {
             const uint32_t cnt = (uint32_t)std::min<size_t>(kMmqInline, v.size() - i0);
@@ -1470,7 +1682,8 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, f16[t])) return rc;
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_m64(t)))
+                return rc;
         }
     }
     return ok();
@@ -1500,7 +1713,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
         uint8_t* base = static_cast<uint8_t*>(plan->dev);
         bind_gemm_group(&plan->g, base);
         uint64_t off = plan->g.ws_bytes;
-        for (uint32_t t = 0; t < 3 && rc == RFXQ_OK; t++) {
+        for (uint32_t t = 0; t < kGroupKernels && rc == RFXQ_OK; t++) {
             const auto& v = plan->g.descs[t];
             plan->table[t] = reinterpret_cast<MmqDesc*>(base + off);
             if (!v.empty()) {
@@ -1542,8 +1755,8 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
             if (e != hipSuccess) rc = fail(RFXQ_ERR_GPU, "gemm_plan_create upload: %s", hipGetErrorString(e));
         }
     }
-    if (rc == RFXQ_OK && !plan->g.q8_rows.empty())
-        rc = rfxq_gemv_plan_create(plan->g.q8_rows.data(), (uint32_t)plan->g.q8_rows.size(), device, &plan->q8);
+    if (rc == RFXQ_OK && !plan->g.gemv_rows.empty())
+        rc = rfxq_gemv_plan_create(plan->g.gemv_rows.data(), (uint32_t)plan->g.gemv_rows.size(), device, &plan->q8);
     (void)hipSetDevice(prev);
     if (rc != RFXQ_OK) {
         if (plan->dev) (void)hipFree(plan->dev);
@@ -1573,14 +1786,10 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
         if (int rc = launch(c->act_f16_multi, plan->hgrid, 0, stream, &ha, sizeof ha, "rfxq_act_f16_multi launch"))
             return rc;
     }
-    for (uint32_t t = 0; t < 3; t++) {
+    for (uint32_t t = 0; t < kGroupKernels; t++) {
         const auto& v = plan->g.descs[t];
         if (v.empty()) continue;
-        MmqDesc tmp[kMmqInline];
-        const uint32_t n = (uint32_t)v.size();
-        if (n <= kMmqInline) std::copy(v.begin(), v.end(), tmp);
-        if (int rc = launch_mmq(c, v[0].type, tmp, n, n <= kMmqInline ? nullptr : plan->table[t], plan->g.wgs[t],
-                                false, stream, plan->g.f16[t]))
+        if (int rc = launch_group_kernel(c, plan->g, t, v.size() <= kMmqInline ? nullptr : plan->table[t], stream))
             return rc;
         if (int rc = run_group_reduces(c, plan->g, t, stream)) return rc;
     }
@@ -1772,7 +1981,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         const uint64_t g_cw = g_ci + align256((uint64_t)rows * top_k * 4u);
         const uint64_t g_total = g_cw + align256((uint64_t)rows * top_k * 4u);
         void* ws;
-        if (int rc = ctx_workspace(c, g_total, &ws)) return rc;
+        if (int rc = ctx_workspace(c, g_total, &ws, stream)) return rc;
         uint8_t* B = static_cast<uint8_t*>(ws);
         float* gout = reinterpret_cast<float*>(B + g_gate);
         float* uout = reinterpret_cast<float*>(B + g_up);
@@ -1834,7 +2043,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     const uint64_t o_desc = o_cw + align256((uint64_t)rows * top_k * 4u);
     const uint64_t total = o_desc + align256((uint64_t)3u * expert_count * sizeof(MmqDesc));
     void* ws;
-    if (int rc = ctx_workspace(c, total, &ws)) return rc;
+    if (int rc = ctx_workspace(c, total, &ws, stream)) return rc;
     uint8_t* B = static_cast<uint8_t*>(ws);
     float* gout = reinterpret_cast<float*>(B + o_gate);
     float* uout = reinterpret_cast<float*>(B + o_up);
@@ -2039,7 +2248,7 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     const uint64_t o_vdn = o_vgu + (gemv_form ? align256((uint64_t)2u * P * sizeof(GemvDesc)) : 0u);
     const uint64_t total = o_vdn + (gemv_form ? align256((uint64_t)P * sizeof(GemvDesc)) : 0u);
     void* ws;
-    if (int rc = ctx_workspace(c, total, &ws)) return rc;
+    if (int rc = ctx_workspace(c, total, &ws, stream)) return rc;
     uint8_t* B = static_cast<uint8_t*>(ws);
     float* gout = reinterpret_cast<float*>(B + o_gate);
     float* uout = reinterpret_cast<float*>(B + o_up);

@@ -15,7 +15,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from . import RfxqGemvItem, RfxqWeight, lib
+from . import RfxqGemmPolicy, RfxqGemvItem, RfxqOptions, RfxqWeight, lib
 
 __all__ = [
     "ReflexError", "GgmlError", "GpuError", "OutOfMemoryError", "InvalidInputError", "IoError", "GgufFile",
@@ -27,6 +27,7 @@ __all__ = [
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
     "moe_route_device", "moe_ffn_grouped_device",
     "act_q8_1_size", "quantize_act_q8_1", "rmsnorm_q8_1", "silu_and_mul_q8_1", "gemm_q8_1", "gemm_q8_1_batch",
+    "get_options", "set_options", "options", "gemm_policy", "PATH_GEMV_ROWS", "PATH_MMQ_INT8", "PATH_MMQ_F16",
 ]
 
 
@@ -173,6 +174,54 @@ class Weight:
 
 def _dev(t: torch.Tensor):
     return torch.cuda.device(t.device)
+
+
+# ------------------------------------------------------------------ options
+
+PATH_GEMV_ROWS, PATH_MMQ_INT8, PATH_MMQ_F16 = 0, 1, 2
+_OPTION_FIELDS = [f for f, _ in RfxqOptions._fields_]
+
+
+def get_options() -> dict:
+    """The library's prefill switches (the environment's ``REFLEX_QUANT_MMA*``,
+    ``REFLEX_MMQ_F16``, ``REFLEX_QUANT_FUSED_MAX_ROWS``, read once) as a dict;
+    raises InvalidInputError with the reference's message on a bad value."""
+    o = RfxqOptions()
+    _check(lib().rfxq_get_options(ctypes.byref(o)))
+    return {f: getattr(o, f) for f in _OPTION_FIELDS}
+
+
+def set_options(**changes) -> dict:
+    """Change some options (``QuantMmaKernels::set_enabled`` / ``set_splits``,
+    kernels.rs:804-830); returns the previous ones, for ``set_options(**prev)``."""
+    prev = get_options()
+    unknown = set(changes) - set(_OPTION_FIELDS)
+    if unknown:
+        raise TypeError(f"unknown options {sorted(unknown)}")
+    new = dict(prev, **changes)
+    _check(lib().rfxq_set_options(ctypes.byref(RfxqOptions(**new))))
+    return prev
+
+
+class options:
+    """Context manager: ``with options(mmq_f16=0): ...`` restores the previous options."""
+
+    def __init__(self, **changes):
+        self._changes = changes
+
+    def __enter__(self):
+        self._prev = set_options(**self._changes)
+        return self
+
+    def __exit__(self, *exc):
+        set_options(**self._prev)
+
+
+def gemm_policy(ty: int, in_features: int, out_features: int, rows: int, compute_units: int = 256) -> dict:
+    """How ``gemm`` runs a GEMM of this shape on a device with ``compute_units`` CUs."""
+    p = RfxqGemmPolicy()
+    _check(lib().rfxq_gemm_policy_for(int(ty), in_features, out_features, rows, compute_units, ctypes.byref(p)))
+    return {f: getattr(p, f) for f, _ in RfxqGemmPolicy._fields_}
 
 
 # ------------------------------------------------------------------ dequant

@@ -39,3 +39,14 @@ def rqh():
     import reflex_amd
 
     return reflex_amd
+
+
+@pytest.fixture
+def opts():
+    """Setter of the library's prefill switches (rfxq_set_options) for one
+    test; the previous options come back afterwards."""
+    import reflex_amd
+
+    prev = reflex_amd.get_options()
+    yield lambda **changes: reflex_amd.set_options(**changes)
+    reflex_amd.set_options(**prev)

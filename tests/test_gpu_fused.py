@@ -70,22 +70,22 @@ def test_silu_and_mul_q8_1(rq, rows, k):
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("rows,n,k", [(512, 1024, 1024), (64, 512, 4096), (300, 136, 2048)])
-def test_gemm_from_activation_buffer(rq, monkeypatch, ty, rows, n, k):
+def test_gemm_from_activation_buffer(rq, opts, ty, rows, n, k):
     """GEMMs from a buffer equal rfxq_gemm on the f32 activation. A buffer holds
     no f32 copy, so Q8_0 reads its int8 layout: compared with rfxq_gemm on the
     int8 kernels (REFLEX_MMQ_F16=0), where f16 mode runs Q8_0 rows as GEMVs."""
     x = _dev(synth.activations(rows * k, 5 + rows))
     w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, 6 + n), k, n, device=DEV)
     if ty == Q8_0:
-        monkeypatch.setenv("REFLEX_MMQ_F16", "0")
+        opts(mmq_f16=0)
     want = rq.gemm(x, w, rows)
-    monkeypatch.delenv("REFLEX_MMQ_F16", raising=False)
+    opts(mmq_f16=1)
     act = rq.quantize_act_q8_1(x, rows, k)
     assert torch.equal(rq.gemm_q8_1(act, w, rows), want)
 
 
-def test_gemm_q8_1_batch(rq, monkeypatch):
-    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")  # the reference groups unsplit, as the batch
+def test_gemm_q8_1_batch(rq, opts):
+    opts(quant_mma_splits=1)  # the reference groups unsplit, as the batch
     rows = 200
     shapes = [(Q4K, 768, 1024), (Q6K, 256, 1024), (Q4K, 640, 2048), (Q8_0, 128, 1024)]
     xa, xb = _dev(synth.activations(rows * 1024, 1)), _dev(synth.activations(rows * 2048, 2))
@@ -99,9 +99,9 @@ def test_gemm_q8_1_batch(rq, monkeypatch):
     for (act, w, _), (ty, n, k) in zip(items, shapes):
         r = torch.empty(rows * n, device=DEV)
         if ty == Q8_0:   # the buffer's int8 layout (see test_gemm_from_activation_buffer)
-            monkeypatch.setenv("REFLEX_MMQ_F16", "0")
+            opts(mmq_f16=0)
         rq.gemm_batch([(xa if k == 1024 else xb, w, r)], rows)
-        monkeypatch.delenv("REFLEX_MMQ_F16", raising=False)
+        opts(mmq_f16=1)
         refs.append(r)
     rq.gemm_q8_1_batch(items, rows)
     for (_, _, y), r in zip(items, refs):

@@ -91,9 +91,9 @@ def test_mmq_block_dots_committed_fixtures(rq):
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("m,n,k", [(7, 200, 1024), (129, 300, 512), (512, 1024, 1024)])
-def test_int8_gemm_kernel_matches_format_model(rq, orc, monkeypatch, ty, m, n, k):
+def test_int8_gemm_kernel_matches_format_model(rq, orc, opts, ty, m, n, k):
     """The int8 MMQ kernels against the exact model of the Q8_1 format."""
-    monkeypatch.setenv("REFLEX_MMQ_F16", "0")
+    opts(mmq_f16=0, fused_max_rows=0)   # the int8 kernel at every row count
     w_np = synth.weights(ty, n, k, 40 + m)
     x = synth.activations(m * k, 41 + m).reshape(m, k)
     y = rq.gemm(_dev(x), _weight(rq, ty, w_np, n, k), m).cpu().numpy().reshape(m, n)
@@ -158,7 +158,7 @@ def _check_gemm(rq, orc, ty, m, n, k, w_np, x_np, rows_checked=None):
     ref = _ref_rows(orc, ty, w_np, n, k, xs)
     e = orc.rel_err_row_l2(y[rows], ref)
     msg = f"type {ty} M={m} [{n}x{k}]: row-L2 error {e:.3e}"
-    if ty in (Q4K, Q6K) and (ty == Q4K or (k // 256) % 2 == 0):
+    if rq.gemm_policy(ty, k, n, m)["path"] == rq.PATH_MMQ_F16:   # the f16 kernels: checked against their model
         e_kernel = orc.rel_err_row_l2(y[rows], orc.mmqh_model_reference(ty, w_np, n, k, xs))
         msg += f", kernel {e_kernel:.1e} from its model"
         assert e_kernel < MODEL_TOL, msg
@@ -220,7 +220,7 @@ def test_gemm_ragged_shapes(rq, orc, ty, m, n, k):
         _check_gemm(rq, orc, ty, m, n, k, w_np, x)
 
 
-def test_gemm_rows_independent_and_deterministic(rq, orc, monkeypatch):
+def test_gemm_rows_independent_and_deterministic(rq, orc, opts):
     """Row r of the output depends only on row r of x, and repeats give identical bits."""
     n, k = 1024, 2048
     w = _weight(rq, Q4K, synth.weights(Q4K, n, k, 9), n, k)
@@ -228,21 +228,21 @@ def test_gemm_rows_independent_and_deterministic(rq, orc, monkeypatch):
     ya = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
     yb = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
     assert np.array_equal(ya, yb)
-    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")   # same K decomposition on both sides
+    opts(quant_mma_splits=1)   # same K decomposition on both sides
     y1 = rq.gemm(_dev(x), w, 300).cpu().numpy().reshape(300, n)
     y2 = rq.gemm(_dev(x[:130]), w, 130).cpu().numpy().reshape(130, n)
     assert np.array_equal(y1[:130], y2)
 
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K])
-def test_gemm_split_k_matches_unsplit(rq, orc, monkeypatch, ty):
+def test_gemm_split_k_matches_unsplit(rq, orc, opts, ty):
     n, k, m = 512, 4096, 64
     w_np = synth.weights(ty, n, k, 12)
     w = _weight(rq, ty, w_np, n, k)
     x = _dev(synth.activations(m * k, 13))
     ys = []
-    for s in ("1", "4", "16"):
-        monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", s)
+    for s in (1, 4, 16):
+        opts(quant_mma_splits=s)
         ys.append(rq.gemm(x, w, m).cpu().numpy().reshape(m, n))
     assert np.array_equal(rq.gemm(x, w, m).cpu().numpy().reshape(m, n), ys[-1])   # repeatable
     for y in ys[1:]:
@@ -268,7 +268,7 @@ def test_gemm_caller_workspace(rq, orc):
         rq.gemm(_dev(x), w, m, workspace=ws[:100])
 
 
-def test_gemm_batch_and_plan_match_single_gemms(rq, orc, monkeypatch):
+def test_gemm_batch_and_plan_match_single_gemms(rq, orc, opts):
     """Grouped GEMMs (each activation brought into its layouts once, one launch
     per weight type, Q8_0 rows as GEMVs) give the single-GEMM results bit for
     bit (split-K off on both sides; by default a group this small splits K)."""
@@ -280,7 +280,7 @@ def test_gemm_batch_and_plan_match_single_gemms(rq, orc, monkeypatch):
     for i, (ty, n, k) in enumerate(shapes):
         w = _weight(rq, ty, synth.weights(ty, n, k, 80 + i), n, k)
         items.append((xa if k == 1024 else xb, w, torch.empty(rows * n, device=DEV)))
-    monkeypatch.setenv("REFLEX_QUANT_MMA_SPLITS", "1")
+    opts(quant_mma_splits=1)
     singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
     rq.gemm_batch(items, rows)
     for (_, _, y), ref in zip(items, singles):
@@ -292,7 +292,7 @@ def test_gemm_batch_and_plan_match_single_gemms(rq, orc, monkeypatch):
         plan.run()
         for (_, _, y), ref in zip(items, singles):
             assert np.array_equal(y.cpu().numpy(), ref)
-    monkeypatch.delenv("REFLEX_QUANT_MMA_SPLITS")
+    opts(quant_mma_splits=0)
     # by default this group splits K: fixed-order partial sums, within f32
     # rounding of the unsplit result, identical between batch and plan
     rq.gemm_batch(items, rows)
