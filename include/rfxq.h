@@ -176,13 +176,29 @@ int rfxq_quantize_q8_1(const float* x, uint32_t rows, uint32_t k, int8_t* xq, ui
 uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows);
 
 /* Model::gemm (src/model/kernels.rs:2197) on a quantized-resident weight:
- * y[rows][N] = x[rows][K] . W^T. rows == 1 takes the decode GEMV; rows >= 2
- * quantize x per 32 to int8 and run the int8-MFMA MMQ kernel (replacing
- * gemm_quant_mma, kernels.rs:2262-2340). `workspace` may be NULL (the library
- * then uses its own per-device buffer; concurrent calls on different streams
- * must then not overlap) or hold rfxq_gemm_workspace_size() bytes. */
+ * y[rows][N] = x[rows][K] . W^T, on the path rfxq_gemm_policy_for names: one
+ * decode GEMV per row (a single row, up to fused_max_rows rows, Q8_0 in f16
+ * mode), or activations brought into the f16 (Q4_K, Q6_K) or int8 Q8_1
+ * layout and the MFMA MMQ kernel (replacing gemm_quant_mma,
+ * kernels.rs:2262-2340). `workspace` may be NULL (the library then uses its
+ * own grow-only per-device buffer: calls on different streams must then not
+ * overlap, and a call that would grow it fails under graph capture) or hold
+ * rfxq_gemm_workspace_size() bytes. */
 int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y, void* workspace,
               uint64_t workspace_bytes, hipStream_t stream);
+
+/* rfxq_gemm with no device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. Same path, kernels and
+ * results as rfxq_gemm with a NULL workspace; the workspace is a fixed
+ * 128 MiB device array per GPU (a file-scope __device__ array, held until the
+ * process ends), so GEMMs whose workspace (rfxq_gemm_workspace_size) exceeds
+ * it fail with RFXQ_ERR_INVALID_INPUT. The device must be initialised first
+ * (rfxq_init), which resolves the array's address. Every call on a GPU shares
+ * its array and leaves its contents there: calls that overlap on one GPU (on
+ * different streams) race. */
+int rfxq_gemm_no_alloc(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y,
+                       hipStream_t stream);
 
 /* One GEMM of a grouped launch: y[rows, N] = x[rows, K] . W^T. */
 typedef struct rfxq_gemm_item {

@@ -79,6 +79,7 @@ SIGNATURES = {
     "rfxq_quantize_q8_1": (_I, [_P, _U32, _U32, _P, _P, _P]),
     "rfxq_gemm_workspace_size": (_U64, [_WP, _U32]),
     "rfxq_gemm": (_I, [_P, _U64, _WP, _U32, _P, _P, _U64, _P]),
+    "rfxq_gemm_no_alloc": (_I, [_P, _U64, _WP, _U32, _P, _P]),
     "rfxq_mmq_block_dots": (_I, [_P, _P, _U32, _WP, _P, _P]),
     "rfxq_route_top_k": (_I, [_P, _U32, _U32, _I, _P, _P]),
     "rfxq_quant_expert_weight": (_I, [_WP, _U32, _WP]),

@@ -5,7 +5,9 @@ run nvcc per .cu file and embed the images as bytes):
   1. hipcc --offload-arch=gfx950 --cuda-device-only --no-gpu-bundle-output
      compiles csrc/kernels.hip to a raw code object (_build/rfxq_gfx950.co).
   2. An assembler stub .incbin's that file into .rodata (_build/embed.o).
-  3. The host C++ (csrc/rfxq.cpp, no device code) is linked with it against
+  3. hipcc compiles csrc/scratch.hip (host code plus the fixed device scratch
+     array of rfxq_gemm_no_alloc) to an ordinary object.
+  4. The host C++ (csrc/rfxq.cpp, no device code) is linked with them against
      libamdhip64 into reflex_amd/librfxq.so, which hipModuleLoadData's the
      embedded image on first use.
 
@@ -63,11 +65,16 @@ def build(verbose: bool = False) -> str:
         )
     embed_o = os.path.join(BUILD, "embed.o")
     _run(["gcc", "-c", embed_s, "-o", embed_o], verbose)
+    # the fixed scratch array of rfxq_gemm_no_alloc: host + gfx950 device code
+    scratch_o = os.path.join(BUILD, "scratch.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-x", "hip", "-O2", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
+          "-c", os.path.join(CSRC, "scratch.hip"), "-o", scratch_o], verbose)
     tmp = LIB + ".tmp"
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall", "-Wextra", "-Wno-unused-parameter",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
-        os.path.join(CSRC, "rfxq.cpp"), embed_o,
+        os.path.join(CSRC, "rfxq.cpp"), embed_o, scratch_o,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp,
     ], verbose)
     os.replace(tmp, LIB)

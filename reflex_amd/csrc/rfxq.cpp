@@ -31,6 +31,7 @@
 #include <cerrno>
 
 #include "gguf.hpp"
+#include "scratch.hpp"
 
 
 extern "C" const unsigned char rfxq_code_object[];
@@ -131,6 +132,7 @@ struct Ctx {
     hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
+    void* scratch = nullptr;  // this device's fixed scratch array (rfxq_gemm_no_alloc)
     // device area for per-call descriptor tables (grow-only, separate from ws)
     void* tab = nullptr;
     uint64_t tab_bytes = 0;
@@ -211,6 +213,9 @@ int load_ctx(int device, Ctx** out) {
         if (e != hipSuccess)
             return fail(RFXQ_ERR_GPU, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
     }
+    // the fixed scratch of rfxq_gemm_no_alloc, resolved now (the device is current)
+    if (hipError_t e = rfxq_scratch::setup(device, &c->scratch); e != hipSuccess)
+        return fail(RFXQ_ERR_GPU, "scratch symbol address on device %d: %s", device, hipGetErrorString(e));
     *out = c.get();
     g_ctx[device] = std::move(c);
     return RFXQ_OK;
@@ -1487,6 +1492,56 @@ int rfxq_gemm(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t row
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
     if (int rc = gemm_impl(c, x, w, rows, y, workspace, workspace_bytes, o, stream)) return rc;
+    return ok();
+}
+
+int rfxq_gemm_no_alloc(const float* x, uint64_t x_len, const rfxq_weight* w, uint32_t rows, float* y,
+                       hipStream_t stream) {
+    if (int rc = check_weight(w, "gemm_no_alloc")) return rc;
+    if (rows == 0 || x_len != (uint64_t)rows * w->in_features)
+        return fail(RFXQ_ERR_OTHER, "gemm_no_alloc: x.len()=%llu != rows*in_features=%llu", (unsigned long long)x_len,
+                    (unsigned long long)rows * w->in_features);
+    if (!x || !y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_no_alloc: x or y is NULL");
+    // the device's context and scratch exist already (rfxq_init): loading them would allocate
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev), "hipGetDevice");
+    Ctx* c = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_ctx.find(dev);
+        if (it != g_ctx.end()) c = it->second.get();
+    }
+    if (!c || !c->scratch)
+        return fail(RFXQ_ERR_INVALID_INPUT, "gemm_no_alloc: device %d is not initialised; call rfxq_init(%d) first",
+                    dev, dev);
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    if (rows == 1 ||
+        gemm_policy(w->ggml_type, w->in_features, w->out_features, rows, 256u, o).path == PATH_GEMV_ROWS) {
+        // rfxq_gemv_to / rfxq_gemv_rows: one GEMV per row, launched with inline
+        // descriptors (no descriptor table to upload); per-row results do not
+        // depend on how rows group into launches
+        for (uint32_t r0 = 0; r0 < rows; r0 += kGemvInline) {
+            const uint32_t cnt = std::min<uint32_t>(kGemvInline, rows - r0);
+            GemvItem v[kGemvInline];
+            for (uint32_t j = 0; j < cnt; j++)
+                if (int rc = make_gemv_item(x + (uint64_t)(r0 + j) * w->in_features, w,
+                                            y + (uint64_t)(r0 + j) * w->out_features, &v[j]))
+                    return rc;
+            if (int rc = gemv_launch_counted(c, std::vector<GemvItem>(v, v + cnt), nullptr, stream)) return rc;
+        }
+        return ok();
+    }
+    if (int rc = check_mmq_weight(w, "gemm_no_alloc")) return rc;
+    if (reinterpret_cast<uintptr_t>(x) % 16u) return fail(RFXQ_ERR_OTHER, "gemm_no_alloc: x is not 16-byte aligned");
+    const GemmPlan p = plan_gemm(c, w, rows, o);
+    if (p.total > rfxq_scratch::kScratchBytes)
+        return fail(RFXQ_ERR_INVALID_INPUT,
+                    "gemm_no_alloc: rows=%u in_features=%u out_features=%u needs %llu bytes of scratch; the fixed "
+                    "scratch holds %llu (use rfxq_gemm with a workspace)",
+                    rows, w->in_features, w->out_features, (unsigned long long)p.total,
+                    (unsigned long long)rfxq_scratch::kScratchBytes);
+    if (int rc = gemm_impl(c, x, w, rows, y, c->scratch, rfxq_scratch::kScratchBytes, o, stream)) return rc;
     return ok();
 }
 

@@ -22,7 +22,7 @@ __all__ = [
     "GgmlType", "ggml_type_block_dims", "Weight", "QuantArena",
     "dequantize", "gemv", "gemv_to", "gemv_q4k", "gemv_q6k", "gemv_q8_0", "gemv_batch", "GemvPlan",
     "gemv_gather",
-    "gemm", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
+    "gemm", "gemm_no_alloc", "gemm_workspace_size", "gemm_batch", "GemmPlan", "quantize_q8_1", "mmq_block_dots",
     "route_top_k", "route_top_k_with_norm", "quant_expert_weight", "expert_gemv", "expert_gemm",
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
     "moe_route_device", "moe_ffn_grouped_device",
@@ -350,6 +350,14 @@ def gemm(x: torch.Tensor, w: Weight, rows: int, workspace: torch.Tensor | None =
         _check(lib().rfxq_gemm(x.data_ptr(), x.numel(), w.cref(), rows, y.data_ptr(), _ptr(workspace),
                                workspace.numel() if workspace is not None else 0, _stream()))
     return y
+
+
+def gemm_no_alloc(x: torch.Tensor, w: Weight, rows: int, out: torch.Tensor) -> torch.Tensor:
+    """``gemm`` without device allocation (the library's fixed per-GPU scratch;
+    ``init`` the device first). Calls that overlap on one GPU race."""
+    with _dev(x):
+        _check(lib().rfxq_gemm_no_alloc(x.data_ptr(), x.numel(), w.cref(), rows, out.data_ptr(), _stream()))
+    return out
 
 
 def gemm_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int) -> None:
