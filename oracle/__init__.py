@@ -331,11 +331,13 @@ def _f16(a: np.ndarray) -> np.ndarray:
 
 def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) -> np.ndarray:
     """The f16-activation prefill GEMM's arithmetic in exact (f64) arithmetic on
-    its own operands: f16 activations (act_f16) and, for Q4_K, the weight
-    operands f16(16(q-8) * f16(d*sc/16)) plus the constant part
-    f16(8*d*sc - dmin*m) against the f16 hi + lo block sums; for Q6_K the
-    exact weights d*sc*(q-32). Any difference between the kernel and this is
-    the kernel's own f32 accumulation."""
+    its own operands: f16 activations (act_f16) and the f16 weight operands.
+    Q4_K: f16((q-8) * f16(d*sc)) for the low-nibble blocks and
+    f16(16(q-8) * f16(d*sc/16)) for the high-nibble ones, plus the constant
+    part f16(8*d*sc - dmin*m) against the f16 hi + lo block sums. Q6_K:
+    f16((q-32) * f16(d*sc)) for codes from low nibbles, f16(16(q-32) *
+    f16(d*sc/16)) for codes from high nibbles. Any difference between the kernel and this is the
+    kernel's own f32 accumulation."""
     x2 = np.ascontiguousarray(x.reshape(-1, k), dtype=np.float32)
     rows = x2.shape[0]
     xh, xsx, xrs = act_f16(x2)
@@ -346,7 +348,8 @@ def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) 
         dd = np.repeat(b[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32), 8, axis=1)
         dm = np.repeat(b[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float32), 8, axis=1)
         scf, mf = sc.astype(np.float32), m.astype(np.float32)
-        s16 = _f16(dd * scf * np.float32(0.0625))                       # f16(d*sc/16)
+        odd = (np.arange(scf.shape[1]) % 2 == 1)[None, :]
+        s16 = _f16(dd * scf * np.where(odd, np.float32(0.0625), np.float32(1.0)))   # the block multipliers
         c16 = np.float32(8.0) * dd * scf - dm * mf                        # f32 fma ~ exact here
         c16 = _f16(c16)
         qb = b[:, :, 16:144]
@@ -354,13 +357,29 @@ def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) 
         for g in range(4):
             nib[:, :, 64 * g:64 * g + 32] = qb[:, :, 32 * g:32 * g + 32] & 15
             nib[:, :, 64 * g + 32:64 * g + 64] = qb[:, :, 32 * g:32 * g + 32] >> 4
-        wop = _f16(16.0 * (nib.reshape(n, k) - 8) * np.repeat(s16, 32, axis=1))
+        code = (nib.reshape(n, k) - 8).astype(np.float64) * np.repeat(np.where(odd, 16.0, 1.0), 32, axis=1)
+        wop = _f16(code * np.repeat(s16, 32, axis=1))
         sx = (xsx.view(np.float16)[..., :8].astype(np.float64) + xsx.view(np.float16)[..., 8:].astype(np.float64))
         y = hv @ wop.T + sx.reshape(rows, -1) @ c16.T
     elif ty == Q6K:
-        # the Q6_K kernel's operands are exact: sc*(q - 32) split into two
-        # f16-exact parts, d applied per super-block
-        y = hv @ dequant_matrix(ty, w, n, k).astype(np.float64).T
+        b = np.ascontiguousarray(w, dtype=np.uint8).reshape(n, k // 256, 210)
+        d = b[:, :, 208:210].copy().view(np.float16)[..., 0].astype(np.float32)
+        sc = b[:, :, 192:208].view(np.int8).astype(np.float32)
+        # per 16 codes f16(d*sc), applied to 16(q-32) as f16(d*sc/16) in the
+        # groups whose codes come from the high nibbles (scales 4-7, 12-15)
+        hi = (np.arange(16) % 8 >= 4)[None, None, :]
+        s16 = _f16(d[:, :, None] * sc * np.where(hi, np.float32(0.0625), np.float32(1.0)))
+        ql, qh = b[:, :, 0:128].astype(np.int64), b[:, :, 128:192].astype(np.int64)
+        q = np.empty((n, k // 256, 256), dtype=np.int64)
+        for h in range(2):
+            L, H = ql[:, :, 64 * h:64 * h + 64], qh[:, :, 32 * h:32 * h + 32]
+            q[:, :, 128 * h + 0:128 * h + 32] = (L[:, :, :32] & 15) | ((H & 3) << 4)
+            q[:, :, 128 * h + 32:128 * h + 64] = (L[:, :, 32:] & 15) | (((H >> 2) & 3) << 4)
+            q[:, :, 128 * h + 64:128 * h + 96] = (L[:, :, :32] >> 4) | (((H >> 4) & 3) << 4)
+            q[:, :, 128 * h + 96:128 * h + 128] = (L[:, :, 32:] >> 4) | (((H >> 6) & 3) << 4)
+        code = (q - 32).astype(np.float64) * np.repeat(np.where(hi, 16.0, 1.0), 16, axis=2)
+        wop = _f16(code.reshape(n, k) * np.repeat(s16.reshape(n, -1), 16, axis=1))
+        y = hv @ wop.T
     else:
         raise ValueError("mmqh_model_reference: Q4_K and Q6_K only")
     return (y * xrs[:, None].astype(np.float64)).astype(np.float32)

@@ -45,13 +45,19 @@
 #include "common.hpp"
 #include "mmq.hpp"
 
+// Phase probes of the tile loops: empty in the library; a timing harness
+// defines them to accumulate cycle counts per phase.
+#ifndef MMQH_PROBE
+#define MMQH_PROBE_BEGIN()
+#define MMQH_PROBE(i)
+#define MMQH_PROBE_END()
+#endif
+
 namespace mmqh {
 
 constexpr uint32_t BM = 128, BN = 256, kThreads = 256;
-constexpr uint32_t kAct = 16384, kCodes = 8192;
-constexpr uint32_t kSlot = kAct + kCodes;
-constexpr uint32_t kHdr = 4096, kSx = 4096;
-constexpr uint32_t kLds = 2 * kSlot + kHdr + kSx;
+constexpr uint32_t kAct = 16384, kSx = 4096;
+constexpr uint32_t kLds = 2 * kAct + kSx;
 static_assert(kLds <= 81920, "two workgroups per CU");
 
 // f16 of an f32, round to nearest even, as the low 16 bits
@@ -71,8 +77,9 @@ RFXQ_DEV void q4k_scales_mins(const u4_t hdr, float (&sc)[8], float (&mn)[8]) {
 }
 
 // Per super-block operands of one weight column: the constant-part A operand
-// (C_0..7 as f16 pairs) and the eight block multipliers f16(d*sc_b/16),
-// packed two per dword (block 2p low, 2p + 1 high).
+// (C_0..7 as f16 pairs) and the eight block multipliers, packed two per dword
+// (block 2p low, 2p + 1 high): f16(d*sc_b) for the low-nibble blocks (even
+// b), f16(d*sc_b/16) for the high-nibble ones (the codes' scales 1 and 16).
 RFXQ_DEV void q4k_sb_operands(const u4_t hdr, u4_t& cop, u4_t& dsc) {
     float sc[8], mn[8];
     q4k_scales_mins(hdr, sc, mn);
@@ -81,7 +88,7 @@ RFXQ_DEV void q4k_sb_operands(const u4_t hdr, u4_t& cop, u4_t& dsc) {
 #pragma unroll
     for (int b = 0; b < 8; b++) {
         c[b] = f16_rne(__builtin_fmaf(8.0f * d, sc[b], -(dmin * mn[b])));
-        s[b] = f16_rne(d * sc[b] * 0.0625f);
+        s[b] = f16_rne(d * sc[b] * ((b & 1) ? 0.0625f : 1.0f));
     }
 #pragma unroll
     for (int p = 0; p < 4; p++) {
@@ -97,25 +104,19 @@ RFXQ_DEV uint32_t splat16(uint32_t v) {
 }
 
 // Weight operand of one 16-k step: codes of block E (0: low nibbles, 1: high)
-// of the step's two quant dwords, as f16 pairs f16(16*(q - 8) * s) in the
-// activations' (q0, q2), (q1, q3) order. 16*(q - 8) is exact in f16, so the
-// multiply is the only rounding.
+// of the step's two quant dwords, as f16 pairs f16((q - 8) * s) in the
+// activations' (q0, q2), (q1, q3) order, s = f16(d*sc) (E = 0) or
+// f16(d*sc/16) (E = 1): the nibble is and-or'ed into the mantissa of an f16
+// 1024.0 where it already sits (bits 0-3: 1024 + q; bits 4-7: 1024 + 16q),
+// an exact add of -1032 (-1152) centres it, and one multiply rounds. `m` is
+// the nibble mask of E, `mg` the f16 pair (1024, 1024), `v0s`/`v1s` the
+// dwords shifted right by 8 (shared by both blocks); all in VGPRs so that
+// each code dword is one v_and_or_b32.
 template <int E>
-RFXQ_DEV u4_t q4k_codes_f16(uint32_t v0, uint32_t v1, uint32_t s) {
-    const uint32_t M = 0x00F000F0u, MG = 0x64006400u;
-    uint32_t w[4];
-    if (E == 0) {
-        w[0] = ((v0 << 4) & M) | MG;
-        w[1] = ((v0 >> 4) & M) | MG;
-        w[2] = ((v1 << 4) & M) | MG;
-        w[3] = ((v1 >> 4) & M) | MG;
-    } else {
-        w[0] = (v0 & M) | MG;
-        w[1] = ((v0 >> 8) & M) | MG;
-        w[2] = (v1 & M) | MG;
-        w[3] = ((v1 >> 8) & M) | MG;
-    }
-    const h2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
+RFXQ_DEV u4_t q4k_codes_f16(uint32_t v0, uint32_t v1, uint32_t v0s, uint32_t v1s, uint32_t s, uint32_t m,
+                            uint32_t mg) {
+    const uint32_t w[4] = {(v0 & m) | mg, (v0s & m) | mg, (v1 & m) | mg, (v1s & m) | mg};
+    const h2_t off = E ? h2_t{(half_t)-1152.0f, (half_t)-1152.0f} : h2_t{(half_t)-1032.0f, (half_t)-1032.0f};
     const h2_t sv = as_h2(s);
     u4_t r;
 #pragma unroll
@@ -157,48 +158,13 @@ RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t c_b
     }
 }
 
-// Asynchronous copies global -> LDS (buffer_load ... lds): lane l's 16 (4)
-// bytes land at lds + 16l (4l). Issued from inline asm so that the compiler
-// does not see LDS writes in flight: its own LDS reads then need no vmcnt
-// waits, and the ring is ordered by the explicit vmcnt waits and barriers
-// of the main loop. M0 (the LDS base) is saved and restored around the copy.
-typedef uint32_t sdesc_t __attribute__((ext_vector_type(4)));
-RFXQ_DEV void dma16(sdesc_t r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    uint32_t keep;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
-        : "=&s"(keep)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
-        : "memory");
-}
-RFXQ_DEV void dma4(sdesc_t r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    uint32_t keep;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dword %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
-        : "=&s"(keep)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
-        : "memory");
-}
-
-// raw buffer descriptor (base, stride 0, num_records = bytes) in SGPRs:
-// offsets at or past `bytes` read zeros
-RFXQ_DEV sdesc_t uniform_desc(const void* p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uintptr_t>(p);
-    return sdesc_t{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
-                   (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)),
-                   (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
-}
-
-RFXQ_DEV uint32_t bperm(uint32_t lane, uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(lane << 2), (int)v);
-}
-
-// an f16 value as f32 in a register, hidden from instruction selection (which
-// would otherwise fold the conversion back into every v_fma_mix_f32)
-RFXQ_DEV float f16_opaque(uint32_t bits16) {
-    float f = f16_bits_to_f32(bits16);
-    asm("" : "+v"(f));
-    return f;
+// Workgroup b of a g-workgroup launch as a tile index such that the tiles
+// each XCD runs are contiguous: workgroups go round-robin to the 8 XCDs, and
+// neighbouring tiles (the row tiles of one column tile, then the next column
+// tile) share weight and activation reads in that XCD's L2.
+RFXQ_DEV uint32_t xcd_tile(uint32_t b, uint32_t g) {
+    const uint32_t x = b & 7u, slot = b >> 3, q = g >> 3, r = g & 7u;
+    return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + slot;
 }
 
 RFXQ_DEV v16f_t mfma16(u4_t a, u4_t b, v16f_t c) {
@@ -208,94 +174,69 @@ RFXQ_DEV v16f_t mfma16(u4_t a, u4_t b, v16f_t c) {
 // ---------------------------------------------------------------- Q6_K
 //
 // A Q6_K super-block (ql[128], qh[64], scales[16] i8, d; src/dequant.rs:414-445)
-// has no constant part: w = d * sc * (q - 32), with one scale per 16 codes.
-// The scale goes into the weight operand, but sc*(q - 32) reaches 4096 in
-// magnitude and needs 12 significant bits, one more than f16 holds; split by
-// the code's low bit, q - 32 = (q & ~1) - 32 + (q & 1):
-//   hi = sc * ((q & ~1) - 32)   (even, |hi| <= 4096: exact in f16)
-//   lo = sc * (q & 1)           (|lo| <= 128)
-// Both operands are exact, so the four chained 32x32x16 f16 MFMAs of a
-// 32-block add exact products of f16 activations and the exact weights
-// sc*(q - 32) into the super-block accumulator t; per super-block y += d * t,
-// and the row scale 2^e at the end.
+// has no constant part: w = d * sc * (q - 32), one int8 scale per 16 codes.
+// The weight operand is f16((q - 32) * f16(d*sc)): the 6-bit code is and-or'ed
+// into the mantissa of an f16 1024.0 (low nibble from ql, two high bits from
+// qh), an exact add centres it, and one multiply rounds, as for Q4_K.
 //
-// A 64-k stage g = 2n + s of a super-block takes blocks A = 4n + s (low
-// nibbles of ql[64n + 32s + l], qh[32n + l] bits 2s..2s+1) and B = A + 2
-// (high nibbles, bits 2s+4..2s+5), l in [0, 32); lane half h holds positions
-// l in [16h, 16h + 16), whose scales are sc[8n + 2s + h] (A) and
-// sc[8n + 4 + 2s + h] (B). Blocks are 210 bytes, so a super-block starts at
-// a 2-byte offset when its index is odd (rows are 4-byte aligned: the host
-// requires an even super-block count per row): the ql and qh ranges are
-// copied as 9-dword windows from the aligned address below and realigned
-// with v_alignbyte after the LDS read.
+// A 64-k stage g = 2n + s of a super-block takes the 32-code groups A = s and
+// B = s + 2 of half n (elements 128n + 32s + l and 128n + 64 + 32s + l, l in
+// [0, 32)): low and high nibbles of ql[64n + 32s + l], bits 2s, 2s + 4 of
+// qh[32n + l]. Lane half h holds positions l in [16h, 16h + 16), whose scales
+// are sc[8n + 2s + h] (A) and sc[8n + 4 + 2s + h] (B). Blocks are 210 bytes,
+// so a super-block starts 0 or 2 bytes past a dword; its 16-byte pieces are
+// read with single unaligned buffer loads (the HSA unaligned access mode).
 
-// Q6_K kernel: 128x128 tiles; per LDS slot activations [128][64] f16 and the
-// code windows [128][72 B]; headers [128][20 B]
-constexpr uint32_t kBM6 = 128, kBN6 = 128;
-constexpr uint32_t kCodes6 = 128u * 18u * 4u;
-constexpr uint32_t kHdr6 = 128u * 5u * 4u;
+// (a & m) | c in one instruction (instruction selection would otherwise
+// merge two of them into an or3 of two ands)
+RFXQ_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+    return r;
+}
 
-// hi and lo operands of one 16-k step of block E (0: A, low nibbles; 1: B,
-// high nibbles) from the step's ql dwords l0, l1 and qh dwords q0, q1 (code
-// positions p..p+7): (q & ~1) << 4 and (q & 1) << 4 are placed in the
-// mantissa of an f16 1024.0, then (1024 + 16x) * (sc/16) + off gives
-// sc*(x - 32) with off = -96 sc (hi) and sc*x with off = -64 sc (lo), exact.
-// tab = (sc/16, -96 sc, -64 sc) as f16 pairs. Pairs follow the activations'
-// (p0, p2), (p1, p3) order.
-template <int E, int S>
-RFXQ_DEV void q6k_step_codes(uint32_t l0, uint32_t l1, uint32_t q0, uint32_t q1, const u4_t tab, u4_t& hi, u4_t& lo) {
-    const uint32_t MH = 0x00E000E0u, MQ = 0x03000300u, ML = 0x00100010u, MG = 0x64006400u;
-    uint32_t mh[4], ml[4];
-    const uint32_t ls[2] = {l0, l1}, qs[2] = {q0, q1};
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const uint32_t L = ls[u], Q = qs[u];
-        uint32_t m02, m13, h02, h13;
-        if (E == 0) {
-            m02 = L << 4;
-            m13 = L >> 4;
-            h02 = Q << (8 - 2 * S);
-            h13 = Q >> (2 * S);
-        } else {
-            m02 = L;
-            m13 = L >> 8;
-            h02 = Q << (4 - 2 * S);
-            h13 = Q >> (2 * S + 4);
-        }
-        mh[2 * u] = (m02 & MH) | (h02 & MQ) | MG;
-        mh[2 * u + 1] = (m13 & MH) | (h13 & MQ) | MG;
-        ml[2 * u] = (m02 & ML) | MG;
-        ml[2 * u + 1] = (m13 & ML) | MG;
-    }
-    const h2_t s = as_h2(tab.x), oh = as_h2(tab.y), ol = as_h2(tab.z);
+// Weight operand of one 16-k step of a stage's group A (E = 0) or B (E = 1)
+// from ql dwords l0, l1 (and l0s, l1s = the same >> 8) and qh dwords shifted
+// so that the group's two bits of bytes 0 and 2 (qa0, qa1) and of bytes 1
+// and 3 (qb0, qb1) sit at bits 4-5 (E = 0) or 8-9 (E = 1): the code goes into
+// the mantissa of an f16 1024.0 where its low nibble already sits (A: bits
+// 0-3, 1024 + q; B: bits 4-7, 1024 + 16q), an exact add of -1056 (-1536)
+// centres it, and one multiply by s (f16(d*sc), or f16(d*sc/16) for B)
+// rounds. Pairs follow the activations' (p0, p2), (p1, p3) order; the masks
+// and mg = the f16 pair (1024, 1024) are VGPRs so that each half is one
+// v_and_or_b32.
+template <int E>
+RFXQ_DEV u4_t q6k_codes_f16(uint32_t l0, uint32_t l1, uint32_t l0s, uint32_t l1s, uint32_t qa0, uint32_t qa1,
+                            uint32_t qb0, uint32_t qb1, uint32_t s, uint32_t ml, uint32_t mq, uint32_t mg) {
+    const uint32_t w[4] = {and_or(l0, ml, and_or(qa0, mq, mg)), and_or(l0s, ml, and_or(qb0, mq, mg)),
+                           and_or(l1, ml, and_or(qa1, mq, mg)), and_or(l1s, ml, and_or(qb1, mq, mg))};
+    const h2_t off = E ? h2_t{(half_t)-1536.0f, (half_t)-1536.0f} : h2_t{(half_t)-1056.0f, (half_t)-1056.0f};
+    const h2_t sv = as_h2(s);
+    u4_t r;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        hi[t] = h2_bits(__builtin_elementwise_fma(as_h2(mh[t]), s, oh));
-        lo[t] = h2_bits(__builtin_elementwise_fma(as_h2(ml[t]), s, ol));
+        h2_t c = as_h2(w[t]) + off;
+        asm("" : "+v"(c));  // keep the exact add and the rounding multiply apart (no fma)
+        r[t] = h2_bits(c * sv);
     }
+    return r;
 }
 
-// (sc/16, -96 sc, -64 sc) of a signed 8-bit scale, each as an f16 pair
-RFXQ_DEV u4_t q6k_tab(int sc) {
-    const float f = (float)sc;
-    const half_t a = (half_t)(f * 0.0625f), b = (half_t)(f * -96.0f), c = (half_t)(f * -64.0f);
-    const h2_t s = {a, a}, oh = {b, b}, ol = {c, c};
-    return u4_t{h2_bits(s), h2_bits(oh), h2_bits(ol), 0u};
-}
-
-// the weight operands of stage s of a half: [block][step] hi and lo
-template <int S>
-RFXQ_DEV void q6k_stage_operands(const uint32_t* V, const uint32_t* H, const u4_t tabA, const u4_t tabB,
-                                 u4_t (&hi)[2][2], u4_t (&lo)[2][2]) {
+// The eight block multipliers of lane half h of one column: f16(d * sc[2i + h])
+// for i = 0..7, divided by 16 for the B groups (i = 2, 3, 6, 7: codes placed
+// at 16q), packed two per dword (i = 2p low, 2p + 1 high); sc = the 16 int8
+// scales, d = the f16 bits of d.
+RFXQ_DEV u4_t q6k_multipliers(u4_t sc, uint32_t dbits, uint32_t h) {
+    const float d = f16_bits_to_f32(dbits);
+    uint32_t m[8];
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
-        q6k_step_codes<0, S>(V[2 * st], V[2 * st + 1], H[2 * st], H[2 * st + 1], tabA, hi[0][st], lo[0][st]);
-        q6k_step_codes<1, S>(V[2 * st], V[2 * st + 1], H[2 * st], H[2 * st + 1], tabB, hi[1][st], lo[1][st]);
+    for (int i = 0; i < 8; i++) {
+        const uint32_t byte = 2u * i + h;  // scale index; dword byte/4, byte byte%4
+        const int sv = (int)(int8_t)(sc[i >> 1] >> (8u * (byte & 3u)));
+        m[i] = f16_rne(d * (float)sv * ((i & 2) ? 0.0625f : 1.0f));
     }
+    return u4_t{pack16(m[0], m[1]), pack16(m[2], m[3]), pack16(m[4], m[5]), pack16(m[6], m[7])};
 }
-
-constexpr uint32_t kSlotQ6 = kAct + kCodes6;
-constexpr uint32_t kLdsQ6 = 3u * kSlotQ6 + kHdr6;
 
 }  // namespace mmqh
 
@@ -322,98 +263,107 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
     const uint32_t row_bytes = nsb * 144u;
     const uint32_t rec_bytes = nsb * 32u;
-    uint8_t* const hdr_lds = lds + 2u * kSlot;
-    uint8_t* const sx_lds = hdr_lds + kHdr;
+    uint8_t* const sx_lds = lds + 2u * kAct;
 
     // Weight columns past the matrix read past the buffer: zeros, no fault.
     // Activation rows are clamped or gathered (act_row): always in bounds.
     const rsrc_t r_act = make_rsrc(ds.xq, 0xFFFFFFFFu);
     const rsrc_t r_w = make_rsrc(ds.w, ds.n * row_bytes);
     const rsrc_t r_sx = make_rsrc(ds.xds, 0xFFFFFFFFu);
-    // Staged pieces (stage 0 of super-block 0). Activations: piece
-    // 256u + tid is chunk tid%8 of row 32u + tid/8 (LDS + 4096u); LDS chunk
-    // c of row r holds logical chunk c ^ ((r/2)%8). Quants: piece 256u + tid
-    // is half tid%2 of column 128u + tid/2 (LDS + 4096u), stored at half
-    // (tid%2) ^ ((column/8)%2). Headers: column tid. Sx: half tid%2 of row tid/2.
+    // Staged activations: piece 256u + tid is chunk tid%8 of row 32u + tid/8
+    // (LDS + 4096u); LDS chunk c of row r holds logical chunk c ^ ((r/2)%8).
+    // Sx: half tid%2 of row tid/2.
     const uint32_t ra = tid >> 3, ca = tid & 7u;
     uint32_t g_act[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + 16u * ca;
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
-    const uint32_t cq = tid >> 1, pq = tid & 1u;
-    const uint32_t g_cod = (n0 + cq) * row_bytes + 16u + 16u * pq;
-    const uint32_t l_cod = kAct + cq * 32u + 16u * (pq ^ ((cq >> 3) & 1u));
-    const uint32_t g_hdr = (n0 + tid) * row_bytes;
     const uint32_t g_sx = act_row(ds, m0 + (tid >> 1)) * rec_bytes + 16u * (tid & 1u);
+    // Weights go straight to registers (no other wave reads a wave's
+    // columns): lane (l32, h) of n-tile j loads, per stage, half h of the 32
+    // quant bytes of column 64w + 32j + l32, and that column's 16-byte
+    // header with the first stage of each super-block.
+    uint32_t col[2], g_q[2], g_h[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        col[j] = 64u * w + 32u * j + l32;
+        g_h[j] = (n0 + col[j]) * row_bytes;
+        g_q[j] = g_h[j] + 16u + 16u * h;
+    }
     const uint32_t nst = 4u * (sb1 - sb0);
 
-    // the staged loads of a stage in two halves: activations u = 2H, 2H + 1
-    // and quants u = H; the super-block headers and Sx records ride with
-    // half 0 of its first stage
-    u4_t sa[2], sq, shd, ssx;
     // Loads are issued unconditionally so that the compiler's wait counts stay
     // exact across the loop: past the last stage a lane reloads the last stage
-    // (in bounds; its copy in LDS is never read).
-    auto load_half = [&](uint32_t st, int H) {
+    // (in bounds; never used).
+    u4_t sa[4], ssx, qn[2], hn[2];
+    auto load_act = [&](uint32_t st, int H) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
         for (int u = 0; u < 2; u++)
-            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[2 * H + u], 512u * sb + 128u * g, 0);
-        sq = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_cod, 144u * sb + 32u * g + 128u * H * row_bytes, 0);
-        if (H == 0 && (st & 3u) == 0u) {
-            shd = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_hdr, 144u * sb, 0);
-            ssx = __builtin_amdgcn_raw_buffer_load_b128(r_sx, g_sx, 32u * sb, 0);
-        }
+            sa[2 * H + u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[2 * H + u], 512u * sb + 128u * g, 0);
+        if (H == 0 && (st & 3u) == 0u) ssx = __builtin_amdgcn_raw_buffer_load_b128(r_sx, g_sx, 32u * sb, 0);
     };
-    auto store_half = [&](uint32_t st, int H) {
-        uint8_t* S = lds + (st & 1u) * kSlot;
+    auto load_w = [&](uint32_t st) {
+        const uint32_t sl = min(st, nst - 1u);
+        const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
-        for (int u = 0; u < 2; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * (2u * H + u)) = sa[u];
-        *reinterpret_cast<u4_t*>(S + l_cod + 4096u * H) = sq;
-        if (H == 0 && (st & 3u) == 0u) {
-            reinterpret_cast<u4_t*>(hdr_lds)[tid] = shd;
-            reinterpret_cast<u4_t*>(sx_lds)[tid] = ssx;
-        }
+        for (int j = 0; j < 2; j++) qn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], 144u * sb + 32u * g, 0);
+        if ((st & 3u) == 0u)
+#pragma unroll
+            for (int j = 0; j < 2; j++) hn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_h[j], 144u * sb, 0);
+    };
+    auto store_act = [&](uint32_t st, int H) {
+        uint8_t* S = lds + (st & 1u) * kAct;
+#pragma unroll
+        for (int u = 0; u < 2; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * (2u * H + u)) = sa[2 * H + u];
+        if (H == 0 && (st & 3u) == 0u) reinterpret_cast<u4_t*>(sx_lds)[tid] = ssx;
     };
 
     v16f_t acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = v16f_t{};
     // LDS read offsets (16-byte units): activations of row l32 of row tile 0,
-    // logical chunk 4e + 2h + step; quants and header of column 64w + 32j + l32
+    // logical chunk 4e + 2h + step
     uint32_t a_act[2][2];
 #pragma unroll
     for (int e = 0; e < 2; e++)
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) a_act[e][s2] = l32 * 8u + ((4u * e + 2u * h + s2) ^ ((l32 >> 1) & 7u));
-    uint32_t a_codes[2], col[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        col[j] = 64u * w + 32u * j + l32;
-        a_codes[j] = kAct / 16u + 2u * col[j] + (h ^ ((col[j] >> 3) & 1u));
-    }
-    u4_t dsc[2] = {};
+    u4_t dsc[2] = {}, q[2] = {};
+    // code-extraction constants, kept in VGPRs (VOP3 takes no literal here)
+    uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mg = 0x64006400u;
+    asm("" : "+v"(mlo), "+v"(mhi), "+v"(mg));
 
     if (nst > 0u) {
-        load_half(0u, 0);
-        store_half(0u, 0);
-        load_half(0u, 1);
-        store_half(0u, 1);
+        load_w(0u);
+        load_act(0u, 0);
+        store_act(0u, 0);
+        load_act(0u, 1);
+        store_act(0u, 1);
     }
     __syncthreads();
+    MMQH_PROBE_BEGIN();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
         for (uint32_t g = 0; g < 4u; g++) {
             const uint32_t st = st0 + g;
-            load_half(st + 1u, 0);
-            const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kSlot);
+            u4_t hdr[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                q[j] = qn[j];
+                if (g == 0u) hdr[j] = hn[j];
+            }
+            load_w(st + 1u);
+            load_act(st + 1u, 0);
+            load_act(st + 1u, 1);
+            const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
             if (g == 0u) {
                 // super-block start: the columns' multipliers, and the
                 // constant part C_b * Sx_b into the accumulators
                 u4_t cop[2];
 #pragma unroll
-                for (int j = 0; j < 2; j++) q4k_sb_operands(reinterpret_cast<const u4_t*>(hdr_lds)[col[j]], cop[j], dsc[j]);
+                for (int j = 0; j < 2; j++) q4k_sb_operands(hdr[j], cop[j], dsc[j]);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const u4_t sxo = reinterpret_cast<const u4_t*>(sx_lds)[2u * (32u * i + l32) + h];
@@ -421,9 +371,7 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                     acc[i][1] = mfma16(cop[1], sxo, acc[i][1]);
                 }
             }
-            u4_t q[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) q[j] = S16[a_codes[j]];
+            MMQH_PROBE(0);
             uint32_t sm[2][2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
@@ -433,10 +381,16 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
             // four 16-k steps t = 2e + s2 (block 2g + e, positions 16s2..),
             // software pipelined: the operands of step t + 1 are read and built
             // while the eight MFMAs of step t run
+            uint32_t qs8[2][4];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) qs8[j][u] = q[j][u] >> 8;
             auto wop = [&](int t, int j) {
                 const int e = t >> 1, s2 = t & 1;
-                return e ? q4k_codes_f16<1>(q[j][2 * s2], q[j][2 * s2 + 1], sm[1][j])
-                         : q4k_codes_f16<0>(q[j][2 * s2], q[j][2 * s2 + 1], sm[0][j]);
+                const uint32_t a0 = q[j][2 * s2], a1 = q[j][2 * s2 + 1], b0 = qs8[j][2 * s2], b1 = qs8[j][2 * s2 + 1];
+                return e ? q4k_codes_f16<1>(a0, a1, b0, b1, sm[1][j], mhi, mg)
+                         : q4k_codes_f16<0>(a0, a1, b0, b1, sm[0][j], mlo, mg);
             };
             u4_t Xc[4], Wc[2];
 #pragma unroll
@@ -445,13 +399,6 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
             Wc[1] = wop(0, 1);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                if (t == 2) {
-                    // first half of stage st + 1 to LDS, second half's loads
-                    __builtin_amdgcn_sched_barrier(0);
-                    store_half(st + 1u, 0);
-                    load_half(st + 1u, 1);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
                 u4_t Xn[4], Wn[2];
                 if (t < 3) {
                     const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
@@ -486,10 +433,15 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            store_half(st + 1u, 1);
+            MMQH_PROBE(1);
+            store_act(st + 1u, 0);
+            store_act(st + 1u, 1);
+            MMQH_PROBE(2);
             __syncthreads();
+            MMQH_PROBE(3);
         }
     }
+    MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
@@ -505,13 +457,14 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmqh_q4k(MmqArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::kLds];
     if (blockDim.x != mmqh::kThreads) return;  // the tile assumes exactly kThreads lanes
-    const MmqDesc d = mmq_pick(args, blockIdx.x);
-    if (blockIdx.x - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
-    mmqh_q4k_tile(d, blockIdx.x - d.wg_begin, lds);
+    const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);
+    const MmqDesc d = mmq_pick(args, b);
+    if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
+    mmqh_q4k_tile(d, b - d.wg_begin, lds);
 }
 
-// One 128x128 tile (and one split-K range) of Y = X . W^T for Q6_K weights,
-// f16 activations.
+// One 128x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
+// the Q4_K tile's layout and pipeline, with the Q6_K weight operands.
 RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     using namespace mmqh;
     MmqDesc ds = dv;
@@ -527,152 +480,186 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     const uint32_t ks = t_local % ds.splits;
     const uint32_t rest = t_local / ds.splits;
     const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
-    const uint32_t m0 = tm * kBM6, n0 = tn * kBN6;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nsb = ds.k / 256u;
     const uint32_t sb0 = ks * ds.sb_per_split;
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
-    const uint32_t row_bytes = nsb * 210u;
+    const uint32_t row_bytes = nsb * 210u;  // a multiple of 4 (nsb is even)
 
-    const uint32_t L = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-    const uint32_t Lhdr = L + 3u * kSlotQ6;
-
-    const sdesc_t r_act = uniform_desc(ds.xq, 0xFFFFFFFFu);  // rows clamped or gathered (act_row)
-    const sdesc_t r_w = uniform_desc(ds.w, ds.n * row_bytes);
-    // activations: as the Q4_K kernel, but logical chunks 4-7 (block B) sit
-    // 128 bytes after chunks 0-3 (block A) in the f16 row
-    uint32_t o_act[4];
+    // The weights' buffer starts at the dword at or below ds.w (2-byte aligned);
+    // sh0 = the bytes between. Columns past the matrix read zeros.
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(ds.w);
+    const uint32_t sh0 = (uint32_t)(wa & 3u);
+    const rsrc_t r_act = make_rsrc(ds.xq, 0xFFFFFFFFu);
+    const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), ds.n * row_bytes + sh0);
+    const uint32_t ra = tid >> 3, ca = tid & 7u;
+    // activations: the Q4_K tile's staging, but the stage's logical chunks 4-7
+    // (group B) sit 128 bytes after chunks 0-3 (group A) in the f16 row
+    uint32_t g_act[4];
+    const uint32_t cofs = 16u * ca + (ca >= 4u ? 64u : 0u);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const uint32_t c = (lane & 7u) ^ (lane >> 4) ^ ((q & 1) ? 4u : 0u);
-        o_act[q] = act_row(ds, m0 + 32u * w + 8u * q + (lane >> 3)) * ds.ldq + 16u * c + (c >= 4u ? 64u : 0u);
-    }
-    // code windows: dword j of column c's window is copy lane 9c + j of the
-    // wave (five copies, the last on lanes 0-31); headers likewise 5 dwords
-    uint32_t o_c[5], o_h[3];
+    for (int u = 0; u < 4; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + cofs;
+    const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
+    // Weights straight to registers: lane (l32, h) of n-tile j loads, per
+    // stage, positions [16h, 16h + 16) of the ql and qh pieces of column
+    // 64w + 32j + l32 (five dwords each), and with the first stage of a
+    // super-block its scales and d.
+    uint32_t col[2], g_c[2];
 #pragma unroll
-    for (int q = 0; q < 5; q++) {
-        const uint32_t lp = 64u * q + lane;
-        o_c[q] = (n0 + 32u * w + lp / 9u) * row_bytes + 4u * (lp % 9u);
-    }
-#pragma unroll
-    for (int q = 0; q < 3; q++) {
-        const uint32_t lp = 64u * q + lane;
-        o_h[q] = (n0 + 32u * w + lp / 5u) * row_bytes + 4u * (lp % 5u);
+    for (int j = 0; j < 2; j++) {
+        col[j] = 64u * w + 32u * j + l32;
+        g_c[j] = (n0 + col[j]) * row_bytes + 16u * h;
     }
     const uint32_t nst = 4u * (sb1 - sb0);
-    // copies of stage st: 14 per wave, 17 when it opens a super-block
-    auto issue = [&](uint32_t st) {
-        const uint32_t sb = sb0 + (st >> 2), g = st & 3u, n = g >> 1, s = g & 1u, slot = st % 3u;
-        const uint32_t Ls = __builtin_amdgcn_readfirstlane(L + slot * kSlotQ6);
-        const uint32_t base = 210u * sb - 2u * (sb & 1u);  // 4-byte aligned
+
+    u4_t sa[4], qln[2], qhn[2], scn[2];
+    uint32_t dn[2];
+    auto load_act = [&](uint32_t st, int H) {
+        const uint32_t sl = min(st, nst - 1u);
+        const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
+        const uint32_t n = g >> 1, s = g & 1u;
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            dma16(r_act, Ls + 1024u * (4u * w + q), o_act[q], 512u * sb + 64u * (4u * n + s));
-        const uint32_t Lc = Ls + kAct + 2304u * w;
+        for (int u = 0; u < 2; u++)
+            sa[2 * H + u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[2 * H + u],
+                                                                  512u * sb + 256u * n + 64u * s, 0);
+    };
+    // 16-byte loads at 2-byte-aligned offsets (unaligned access mode)
+    auto load_w = [&](uint32_t st) {
+        const uint32_t sl = min(st, nst - 1u);
+        const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
+        const uint32_t n = g >> 1, s = g & 1u;
+        const uint32_t base = 210u * sb + sh0;
+        // the qh piece of half n serves both of its stages: loaded with s = 0
 #pragma unroll
-        for (int q = 0; q < 4; q++) dma4(r_w, Lc + 256u * q, o_c[q], base + 64u * n + 32u * s);
-        if (h == 0u) dma4(r_w, Lc + 1024u, o_c[4], base + 64u * n + 32u * s);
+        for (int j = 0; j < 2; j++) {
+            qln[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], base + 64u * n + 32u * s, 0);
+            if ((st & 1u) == 0u) qhn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], base + 128u + 32u * n, 0);
+        }
+        if ((st & 3u) == 0u) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) dma4(r_w, Lc + 1152u + 256u * q, o_c[q], base + 128u + 32u * n);
-        if (h == 0u) dma4(r_w, Lc + 1152u + 1024u, o_c[4], base + 128u + 32u * n);
-        if (g == 0u) {
-            const uint32_t Lh = Lhdr + 640u * w;
-            dma4(r_w, Lh, o_h[0], base + 192u);
-            dma4(r_w, Lh + 256u, o_h[1], base + 192u);
-            if (h == 0u) dma4(r_w, Lh + 512u, o_h[2], base + 192u);
+            for (int j = 0; j < 2; j++) {
+                scn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j] - 16u * h, base + 192u, 0);
+                dn[j] = __builtin_amdgcn_raw_buffer_load_b16(r_w, g_c[j] - 16u * h, base + 208u, 0);
+            }
         }
     };
-
-    v16f_t acc[4], t[4];
+    auto store_act = [&](uint32_t st, int H) {
+        uint8_t* S = lds + (st & 1u) * kAct;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        acc[i] = v16f_t{};
-        t[i] = v16f_t{};
-    }
+        for (int u = 0; u < 2; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * (2u * H + u)) = sa[2 * H + u];
+    };
+
+    v16f_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = v16f_t{};
     uint32_t a_act[2][2];
 #pragma unroll
     for (int e = 0; e < 2; e++)
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) a_act[e][s2] = l32 * 8u + ((4u * e + 2u * h + s2) ^ ((l32 >> 1) & 7u));
-    const uint32_t a_codes = (kAct + 2304u * w) / 4u + 9u * l32 + 4u * h;
-    uint32_t scw[4] = {0u, 0u, 0u, 0u}, dbits = 0u;
+    u4_t mult[2] = {}, L[2], Q[2];
+    uint32_t mla = 0x000F000Fu, mqa = 0x00300030u, mlb = 0x00F000F0u, mqb = 0x03000300u, mg = 0x64006400u;
+    asm("" : "+v"(mla), "+v"(mqa), "+v"(mlb), "+v"(mqb), "+v"(mg));
 
-    if (nst > 0u) issue(0u);
-    if (nst > 1u) issue(1u);
-    for (uint32_t st = 0; st < nst; st++) {
-        if (st + 1u < nst) {
-            if (((st + 1u) & 3u) == 0u) asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(14)" ::: "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (st + 2u < nst) issue(st + 2u);
-
-        const uint32_t sb = sb0 + (st >> 2), g = st & 3u, n = g >> 1, s = g & 1u;
-        const uint32_t sh = 2u * (sb & 1u);  // byte offset of the block in the windows
-        const uint8_t* S = lds + (st % 3u) * kSlotQ6;
-        const u4_t* S16 = reinterpret_cast<const u4_t*>(S);
-        if (g == 0u) {
-            const uint32_t* hp = reinterpret_cast<const uint32_t*>(lds + 3u * kSlotQ6 + 640u * w) + 5u * l32;
-            uint32_t hw[5];
+    if (nst > 0u) {
+        load_w(0u);
+        load_act(0u, 0);
+        load_act(0u, 1);
+        store_act(0u, 0);
+        store_act(0u, 1);
+    }
+    __syncthreads();
+    MMQH_PROBE_BEGIN();
+    for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
-            for (int j = 0; j < 5; j++) hw[j] = hp[j];
+        for (uint32_t g = 0; g < 4u; g++) {
+            const uint32_t st = st0 + g;
+            const uint32_t n = g >> 1, s = g & 1u;
 #pragma unroll
-            for (int j = 0; j < 4; j++) scw[j] = __builtin_amdgcn_alignbyte(hw[j + 1], hw[j], sh);
-            dbits = (hw[4] >> (8u * sh)) & 0xFFFFu;
-        }
-        const uint32_t* cp = reinterpret_cast<const uint32_t*>(S) + a_codes;
-        uint32_t V[4], H[4];
-        {
-            uint32_t c[5], e[5];
-#pragma unroll
-            for (int j = 0; j < 5; j++) {
-                c[j] = cp[j];
-                e[j] = cp[288 + j];
+            for (int j = 0; j < 2; j++) {
+                L[j] = qln[j];
+                if (s == 0u) Q[j] = qhn[j];
+                if (g == 0u) mult[j] = q6k_multipliers(scn[j], dn[j], h);
             }
+            load_w(st + 1u);
+            load_act(st + 1u, 0);
+            load_act(st + 1u, 1);
+            const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
+            MMQH_PROBE(0);
+            // groups A (e = 0) and B (e = 1): multipliers i = 4n + s + 2e
+            uint32_t sm[2][2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                V[j] = __builtin_amdgcn_alignbyte(c[j + 1], c[j], sh);
-                H[j] = __builtin_amdgcn_alignbyte(e[j + 1], e[j], sh);
+            for (int j = 0; j < 2; j++) {
+                sm[0][j] = s ? splat16<1>(mult[j][2 * n]) : splat16<0>(mult[j][2 * n]);
+                sm[1][j] = s ? splat16<1>(mult[j][2 * n + 1]) : splat16<0>(mult[j][2 * n + 1]);
             }
-        }
-        const uint32_t bsh = 8u * (2u * s + h);
-        const u4_t tabA = q6k_tab((int)(int8_t)(scw[2 * n] >> bsh));
-        const u4_t tabB = q6k_tab((int)(int8_t)(scw[2 * n + 1] >> bsh));
-        u4_t hi[2][2], lo[2][2];
-        if (s) q6k_stage_operands<1>(V, H, tabA, tabB, hi, lo);
-        else q6k_stage_operands<0>(V, H, tabA, tabB, hi, lo);
+            // shifted copies of the stage's code dwords (see q6k_codes_f16)
+            uint32_t Ls[2][4], Qa[2][4], Qb[2][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const u4_t* xp = S16 + 256u * i;
-            const u4_t xa0 = xp[a_act[0][0]], xa1 = xp[a_act[0][1]];
-            const u4_t xb0 = xp[a_act[1][0]], xb1 = xp[a_act[1][1]];
-            t[i] = mfma16(hi[0][0], xa0, t[i]);
-            t[i] = mfma16(lo[0][0], xa0, t[i]);
-            t[i] = mfma16(hi[0][1], xa1, t[i]);
-            t[i] = mfma16(lo[0][1], xa1, t[i]);
-            t[i] = mfma16(hi[1][0], xb0, t[i]);
-            t[i] = mfma16(lo[1][0], xb0, t[i]);
-            t[i] = mfma16(hi[1][1], xb1, t[i]);
-            t[i] = mfma16(lo[1][1], xb1, t[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (g == 3u) {
-            uint32_t dd[16];
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) dd[r] = bperm(8u * (r >> 2) + 4u * h + (r & 3), dbits);
+                for (int u = 0; u < 4; u++) {
+                    Ls[j][u] = L[j][u] >> 8;
+                    Qa[j][u] = s ? Q[j][u] << 2 : Q[j][u] << 4;
+                    Qb[j][u] = s ? Q[j][u] >> 6 : Q[j][u] >> 4;
+                }
+            auto wop = [&](int t, int j) {
+                const int e = t >> 1, u = 2 * (t & 1);
+                if (e == 0)
+                    return q6k_codes_f16<0>(L[j][u], L[j][u + 1], Ls[j][u], Ls[j][u + 1], Qa[j][u], Qa[j][u + 1],
+                                            Qb[j][u], Qb[j][u + 1], sm[0][j], mla, mqa, mg);
+                return q6k_codes_f16<1>(L[j][u], L[j][u + 1], Ls[j][u], Ls[j][u + 1], Qa[j][u], Qa[j][u + 1],
+                                        Qb[j][u], Qb[j][u + 1], sm[1][j], mlb, mqb, mg);
+            };
+            u4_t Xc[4], Wc[2];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float d = f16_opaque(dd[r]);
+            for (int i = 0; i < 4; i++) Xc[i] = S16[256u * i + a_act[0][0]];
+            Wc[0] = wop(0, 0);
+            Wc[1] = wop(0, 1);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                u4_t Xn[4], Wn[2];
+                if (t < 3) {
+                    const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
+                    Wn[0] = wop(t + 1, 0);
+                    Wn[1] = wop(t + 1, 1);
+                }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    acc[i][r] = __builtin_fmaf(t[i][r], d, acc[i][r]);
-                    t[i][r] = 0.0f;
+                    acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
+                    acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
+                }
+                if (t < 3) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) Xc[i] = Xn[i];
+                    Wc[0] = Wn[0];
+                    Wc[1] = Wn[1];
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+            MMQH_PROBE(1);
+            store_act(st + 1u, 0);
+            store_act(st + 1u, 1);
+            MMQH_PROBE(2);
+            __syncthreads();
+            MMQH_PROBE(3);
         }
     }
+    MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
@@ -680,13 +667,16 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     for (int i = 0; i < 4; i++) {
         const uint32_t row = m0 + 32u * i + l32;
         const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
-        store_tile(ds, y, row, n0 + 32u * w, h, acc[i], scale, vec);
+#pragma unroll
+        for (int j = 0; j < 2; j++) store_tile(ds, y, row, n0 + 64u * w + 32u * j, h, acc[i][j], scale, vec);
     }
 }
 
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmqh_q6k(MmqArgs args) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::kLdsQ6];
-    const MmqDesc d = mmq_pick(args, blockIdx.x);
-    if (blockIdx.x - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
-    mmqh_q6k_tile(d, blockIdx.x - d.wg_begin, lds);
+    __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::kLds];
+    if (blockDim.x != mmqh::kThreads) return;  // the tile assumes exactly kThreads lanes
+    const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);
+    const MmqDesc d = mmq_pick(args, b);
+    if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
+    mmqh_q6k_tile(d, b - d.wg_begin, lds);
 }

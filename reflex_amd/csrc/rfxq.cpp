@@ -729,7 +729,7 @@ bool f16_kernel(const rfxq_weight* w, uint32_t rows) {
 }
 
 // weight columns per workgroup tile (rows: kMmqBM, or 64 for the int8 *_m64 kernels)
-uint32_t tile_bn(uint32_t ty, bool f16) { return f16 && ty == RFXQ_TYPE_Q4_K ? 256u : 128u; }
+uint32_t tile_bn(uint32_t ty, bool f16) { (void)ty; return f16 ? 256u : 128u; }
 
 // How a GEMM of `rows` rows runs (Model::gemm's choice between the fused GEMV,
 // the MMA kernel and its split-K, kernels.rs:628-713 quant_mma_splits /

@@ -148,10 +148,10 @@ def test_policy_tiles_and_splits(rq):
         assert (p["splits"], p["sb_per_split"]) == (3, 6)
     with rq.options(quant_mma_splits=100):   # at most one split per super-block
         assert pol(Q4K, 4096, 4096, 512)["splits"] == 16
-    # Q6_K tiles are 128 x 128: down at 8B has 4 x 32 tiles, enough for 256 CUs
+    # Q6_K tiles are 128 x 256 too: down at 8B has 4 x 16 tiles -> 8 splits of 7 super-blocks
     p = pol(Q6K, 14336, 4096, 512, 256)
-    assert (p["tile_m"], p["tile_n"], p["splits"]) == (128, 128, 1)
-    # v_proj at 8B: 4 x 8 tiles -> 16 splits, capped at nsb / 2 = 8
+    assert (p["tile_m"], p["tile_n"], p["splits"], p["sb_per_split"]) == (128, 256, 8, 7)
+    # v_proj at 8B: 4 x 4 tiles -> 32 splits, capped at nsb / 2 = 8
     assert pol(Q6K, 4096, 1024, 512, 256)["splits"] == 8
 
 
