@@ -73,7 +73,7 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall", "-Wextra", "-Wno-unused-parameter",
-        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
+        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *os.environ.get("RFXQ_EXTRA_HOST_FLAGS", "").split(),
         os.path.join(CSRC, "rfxq.cpp"), embed_o, scratch_o,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp,
     ], verbose)

@@ -32,6 +32,13 @@
 #pragma once
 #include "common.hpp"
 
+// Phase probes: empty in the library; a timing harness defines them.
+#ifndef GEMV_PROBE
+#define GEMV_PROBE_BEGIN()
+#define GEMV_PROBE(i)
+#define GEMV_PROBE_END()
+#endif
+
 struct GemvDesc {
     const uint8_t* w;  // raw blocks, row-major [n][k / QK]
     const float* x;    // [k] f32
@@ -50,25 +57,28 @@ struct GemvArgs {
 
 // ---------------------------------------------------------------- prologue
 
-// x -> LDS f16 (pair-permuted; Q4_K high-nibble runs scaled by 1/16) and the
-// per-16 sums of the stored f16 values (computed with the same dot2 op).
-// The first 4096 elements are loaded into registers by gemv_x_load before the
-// weight loads are issued, so their latency overlaps; the barriers wait on LDS
-// only, weight loads issued before stay in flight.
+// x -> LDS f16 (pair-permuted; the runs of high-nibble codes scaled by 1/16:
+// elements with bit `hi` of their index set, hi = 32 for Q4_K, 64 for Q6_K, 0
+// for none) and the per-16 sums of the stored f16 values (computed with the
+// same dot2 op). x (at most kGemvMaxK elements, 16 per lane) is loaded into
+// registers by gemv_x_load before the weight loads are issued, all at once,
+// so staging costs one L2 round trip; the barriers wait on LDS only, weight
+// loads issued before stay in flight.
+constexpr uint32_t kGemvMaxK = 16384;
 struct XRegs {
-    float4 v[4];
+    float4 v[kGemvMaxK / 1024u];
 };
 
 RFXQ_DEV void gemv_x_load(const float* __restrict__ x, uint32_t k, XRegs& xr, uint32_t tid) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (uint32_t i = 0; i < kGemvMaxK / 1024u; i++) {
         const uint32_t e = 4u * tid + 1024u * i;
         if (e < k) xr.v[i] = ldf4(x + e);
     }
 }
 
-RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, bool prescale_hi, float scale) {
-    const float sc = (prescale_hi && (e & 32u)) ? 0.0625f * scale : scale;
+RFXQ_DEV void gemv_x_put(uint32_t* lds_x, uint32_t e, float4 v, uint32_t hi, float scale) {
+    const float sc = (e & hi) ? 0.0625f * scale : scale;
     const h2_t a = {(half_t)(v.x * sc), (half_t)(v.z * sc)};
     const h2_t b = {(half_t)(v.y * sc), (half_t)(v.w * sc)};
     lds_st64(lds_addr(lds_x) + 2u * e, u2_t{h2_bits(a), h2_bits(b)});
@@ -98,33 +108,15 @@ RFXQ_DEV void gemv_x_sums(const uint32_t* lds_x, float* lds_s, uint32_t k, uint3
 // staged again multiplied by an exact power of two 2^-s and row results are
 // multiplied by 2^s when stored; otherwise it is 1 and nothing changes.
 // lds_p (the row results, free while staging) carries the waves' maxima.
-RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool prescale_hi, const XRegs& xr,
+RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, uint32_t hi, const XRegs& xr,
                             uint32_t* lds_x, float* lds_s, float* lds_p, uint32_t tid) {
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (uint32_t i = 0; i < kGemvMaxK / 1024u; i++) {
         const uint32_t e = 4u * tid + 1024u * i;
         if (e < k) {
-            gemv_x_put(lds_x, e, xr.v[i], prescale_hi, 1.0f);
+            gemv_x_put(lds_x, e, xr.v[i], hi, 1.0f);
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xr.v[i].x), fabsf(xr.v[i].y)), fmaxf(fabsf(xr.v[i].z), fabsf(xr.v[i].w))));
-        }
-    }
-    // the rest in batches of 8 loads in flight (one L2 round trip per 8 KB
-    // of x rather than one per 1 KB)
-    for (uint32_t b = 4096u; b < k; b += 8192u) {
-        float4 t[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t e = b + 4u * tid + 1024u * i;
-            if (e < k) t[i] = ldf4(x + e);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t e = b + 4u * tid + 1024u * i;
-            if (e < k) {
-                gemv_x_put(lds_x, e, t[i], prescale_hi, 1.0f);
-                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t[i].x), fabsf(t[i].y)), fmaxf(fabsf(t[i].z), fabsf(t[i].w))));
-            }
         }
     }
 #pragma unroll
@@ -143,7 +135,7 @@ RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, bool presca
         (void)frexpf(amax, &ex);  // amax < 2^ex
         const float scale = ldexpf(1.0f, 14 - ex);
         inv = ldexpf(1.0f, ex - 14);
-        for (uint32_t e = 4u * tid; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), prescale_hi, scale);
+        for (uint32_t e = 4u * tid; e < k; e += 1024u) gemv_x_put(lds_x, e, ldf4(x + e), hi, scale);
         lds_barrier();
         gemv_x_sums(lds_x, lds_s, k, tid);
         lds_barrier();
@@ -168,6 +160,7 @@ RFXQ_DEV uint32_t u4_at(const uint4* a, int j) {
 
 struct Q4K {
     static constexpr uint32_t QK = 256, BB = 144, UPB = 4;  // units per block
+    static constexpr uint32_t XHI = 32;    // x of high-nibble runs staged / 16
     static constexpr bool ALIGNED = true;  // blocks (and rows) start 16-byte aligned
     static constexpr int NJ = 3;           // 1 KB copy instructions per item (64 x 36 B)
     struct Raw {
@@ -266,6 +259,7 @@ RFXQ_DEV u4_t seg_align(const Seg& s, uint32_t sh) {
 
 struct Q6K {
     static constexpr uint32_t QK = 256, BB = 210, UPB = 4;
+    static constexpr uint32_t XHI = 64;   // x of the high-nibble runs (64..127 of each 128) staged / 16
     static constexpr bool ALIGNED = false;  // blocks are 2-byte aligned
     static constexpr int NJ = 4;            // 64 x 52.5 B plus per-row alignment slack
     struct Raw {
@@ -327,6 +321,10 @@ struct Q6K {
             x.s[t] = __builtin_bit_cast(float, lds_ld32(lds_addr(lds_s) + 4u * (o / 16u + 2u * t)));
         }
     }
+    // runs 0, 1 (low nibbles of ql) as 1024 + q with the qh bits at 4-5;
+    // runs 2, 3 (high nibbles) as 1024 + 16q with the qh bits at 8-9, against
+    // x staged / 16: each pair is two v_and_or_b32 and one dot2, the shifted
+    // qh words shared by a low and a high run
     static RFXQ_DEV float dot(const Raw& r, uint32_t unit, const XV& x, uint32_t MG) {
 #pragma clang fp contract(off)
         const uint32_t g = unit & 3u, n = g >> 1, hs = g & 1u, sh = r.sh;
@@ -341,30 +339,41 @@ struct Q6K {
         const int sc3 = (int)(int8_t)(W1 >> (8u * hs + 16u));
         const uint32_t A[4] = {a.x, a.y, a.z, a.w}, C[4] = {c.x, c.y, c.z, c.w}, H[4] = {h.x, h.y, h.z, h.w};
         float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
-        const uint32_t M4 = 0x000F000Fu, M2 = 0x00300030u;
+        uint32_t ml = 0x000F000Fu, mq = 0x00300030u, mlh = 0x00F000F0u, mqh = 0x03000300u;
+        asm volatile("" : "+v"(ml), "+v"(mq), "+v"(mlh), "+v"(mqh));
+        auto ao = [](uint32_t v, uint32_t m, uint32_t c2) {
+            uint32_t o;
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(o) : "v"(v), "v"(m), "v"(c2));
+            return o;
+        };
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t av = A[j], cv = C[j], hv = H[j];
-            r0 = dot2((av & M4) | ((hv << 4) & M2) | MG, u4_at(x.r[0], 2 * j), r0);
-            r0 = dot2(((av >> 8) & M4) | ((hv >> 4) & M2) | MG, u4_at(x.r[0], 2 * j + 1), r0);
-            r1 = dot2((cv & M4) | ((hv << 2) & M2) | MG, u4_at(x.r[1], 2 * j), r1);
-            r1 = dot2(((cv >> 8) & M4) | ((hv >> 6) & M2) | MG, u4_at(x.r[1], 2 * j + 1), r1);
-            r2 = dot2(((av >> 4) & M4) | (hv & M2) | MG, u4_at(x.r[2], 2 * j), r2);
-            r2 = dot2(((av >> 12) & M4) | ((hv >> 8) & M2) | MG, u4_at(x.r[2], 2 * j + 1), r2);
-            r3 = dot2(((cv >> 4) & M4) | ((hv >> 2) & M2) | MG, u4_at(x.r[3], 2 * j), r3);
-            r3 = dot2(((cv >> 12) & M4) | ((hv >> 10) & M2) | MG, u4_at(x.r[3], 2 * j + 1), r3);
+            const uint32_t a8 = av >> 8, c8 = cv >> 8;
+            const uint32_t h4l = hv << 4, h4r = hv >> 4, h2l = hv << 2, h6r = hv >> 6;
+            r0 = dot2(ao(av, ml, ao(h4l, mq, MG)), u4_at(x.r[0], 2 * j), r0);
+            r0 = dot2(ao(a8, ml, ao(h4r, mq, MG)), u4_at(x.r[0], 2 * j + 1), r0);
+            r1 = dot2(ao(cv, ml, ao(h2l, mq, MG)), u4_at(x.r[1], 2 * j), r1);
+            r1 = dot2(ao(c8, ml, ao(h6r, mq, MG)), u4_at(x.r[1], 2 * j + 1), r1);
+            r2 = dot2(ao(av, mlh, ao(h4l, mqh, MG)), u4_at(x.r[2], 2 * j), r2);
+            r2 = dot2(ao(a8, mlh, ao(h4r, mqh, MG)), u4_at(x.r[2], 2 * j + 1), r2);
+            r3 = dot2(ao(cv, mlh, ao(h2l, mqh, MG)), u4_at(x.r[3], 2 * j), r3);
+            r3 = dot2(ao(c8, mlh, ao(h6r, mqh, MG)), u4_at(x.r[3], 2 * j + 1), r3);
         }
+        // runs 0, 1: sum (1024 + q) x - 1056 sum x; runs 2, 3: sum (64 + q) x -
+        // 96 sum x = r - 1536 sum(x / 16), the staged sums being of x / 16
         const float ds0 = d * (float)sc0, ds1 = d * (float)sc1, ds2 = d * (float)sc2, ds3 = d * (float)sc3;
         float acc = fmaf(ds0, r0, -((1056.0f * ds0) * x.s[0]));
         acc += fmaf(ds1, r1, -((1056.0f * ds1) * x.s[1]));
-        acc += fmaf(ds2, r2, -((1056.0f * ds2) * x.s[2]));
-        acc += fmaf(ds3, r3, -((1056.0f * ds3) * x.s[3]));
+        acc += fmaf(ds2, r2, -((1536.0f * ds2) * x.s[2]));
+        acc += fmaf(ds3, r3, -((1536.0f * ds3) * x.s[3]));
         return acc;
     }
 };
 
 struct Q80 {
     static constexpr uint32_t QK = 32, BB = 34, UPB = 1;
+    static constexpr uint32_t XHI = 0;
     static constexpr bool ALIGNED = false;  // blocks are 2-byte aligned
     static constexpr int NJ = 3;            // 64 x 34 B plus per-row alignment slack
     struct Raw {
@@ -434,9 +443,19 @@ struct Q80 {
 // slot is its own array, so the compiler's wait counting knows which copy a
 // read depends on and waits for exactly that one.
 constexpr uint32_t kSlotBytes = 4096;
-constexpr int kRing = 2;
+#ifndef RFXQ_GEMV_RING
+#define RFXQ_GEMV_RING 2
+#endif
+constexpr int kRing = RFXQ_GEMV_RING;
 __shared__ __attribute__((aligned(16))) uint8_t gemv_ring0[4][kSlotBytes];
 __shared__ __attribute__((aligned(16))) uint8_t gemv_ring1[4][kSlotBytes];
+#if RFXQ_GEMV_RING > 2
+__shared__ __attribute__((aligned(16))) uint8_t gemv_ring2[4][kSlotBytes];
+#endif
+#if RFXQ_GEMV_RING > 3
+__shared__ __attribute__((aligned(16))) uint8_t gemv_ring3[4][kSlotBytes];
+#endif
+
 
 // Offset for copies past a wave's last item: beyond any weight buffer's range
 // (the host keeps weights below it), so the copy writes zeros and fetches
@@ -499,12 +518,27 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
         pc[j] = 16u * (p - r * ppr);
     }
     const uint32_t uo = sub * ppr * 16u + T::unit_off(li);  // this lane's unit in a slot
-    uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave]};
+    uint8_t* const ring[kRing] = {gemv_ring0[wave], gemv_ring1[wave]
+#if RFXQ_GEMV_RING > 2
+                                  , gemv_ring2[wave]
+#endif
+#if RFXQ_GEMV_RING > 3
+                                  , gemv_ring3[wave]
+#endif
+    };
 
     // next item to copy: pass lu, row iteration lit; S = buffer offset of the
     // item's first row chunk (scalar)
     const uint32_t S0 = wsh + base0 * row_bytes;
     uint32_t lu = n_it ? 0u : U, lit = 0, lS = S0;
+    auto advance = [&](uint32_t& u, uint32_t& it, uint32_t& S) {
+        S += row_step;
+        if (++it == n_it) {
+            it = 0;
+            u++;
+            S = S0 + u * chunk;
+        }
+    };
     uint32_t slotS[kRing];
     auto issue = [&](int t) {
         const bool valid = lu < U;
@@ -516,12 +550,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             g += pc[j];
             dma16_stream(wr, ring[t] + 1024 * j, valid && pv[j] ? g : kPastEnd);
         }
-        lS += row_step;
-        if (++lit == n_it) {
-            lit = 0;
-            lu++;
-            lS = S0 + lu * chunk;
-        }
+        advance(lu, lit, lS);
     };
 
     // Stores share vmcnt with the copies and may complete out of order with
@@ -529,12 +558,14 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
     // (the previous segment's are drained here), and results go to LDS and
     // are stored after the last wait.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    GEMV_PROBE_BEGIN();
     XRegs xr;
     gemv_x_load(dsc.x, k, xr, tid);
 #pragma unroll
     for (int t = 0; t < kRing; t++) issue(t);
     if (restage) lds_barrier();  // every wave is done with the previous segment's x
-    const float y_scale = gemv_stage_x(dsc.x, k, T::QK == 256u && T::BB == 144u, xr, lds_x, lds_s, lds_p, tid);
+    const float y_scale = gemv_stage_x(dsc.x, k, T::XHI, xr, lds_x, lds_s, lds_p, tid);
+    GEMV_PROBE(0);
 
     // f16 1024.0 in both halves, kept in a VGPR: gfx9 VOP3 takes at most one
     // SGPR/constant, so (v & mask) | magic is one v_and_or_b32 only this way
@@ -570,12 +601,15 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             }
         }
     }
+    GEMV_PROBE(1);
     // no copy may land in LDS after the workgroup is gone (or in the next
     // segment's reads)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     for (uint32_t i = tid; i < row_end - row_begin; i += 256u)
         bst4f(yr, (row_begin + i) * 4u, __builtin_bit_cast(float, lds_ld32(out0 + 4u * i)) * y_scale);
+    GEMV_PROBE(2);
+    GEMV_PROBE_END();
 }
 
 template <typename T>
@@ -624,7 +658,7 @@ RFXQ_DEV GemvDesc gemv_uniform(const GemvDesc* p) {
 
 // LDS: [part_floats] row results of the current segment, then x as f16
 // (k * 2 bytes) and the per-16 x sums (k / 4 bytes).
-extern "C" __global__ __launch_bounds__(256) void rfxq_gemv(GemvArgs args) {
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rfxq_gemv(GemvArgs args) {
     extern __shared__ uint32_t lds[];
     uint32_t d0, it0, d1, it1;
     if (args.ranges) {

@@ -78,9 +78,9 @@ RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t*
 // ---------------------------------------------------------------- f16 activations
 //
 // The input stage of the f16-activation prefill kernels (mmqh.hpp): one wave
-// per row. Pass 1 finds max |x| of the row; e = ilogb(max) - 8 (clamped to
+// per row. It finds max |x| of the row; e = ilogb(max) - 8 (clamped to
 // [-120, 120]; 0 for an all-zero or non-finite maximum) so that the scaled
-// row's largest value lies in [256, 512). Pass 2 writes
+// row's largest value lies in [256, 512), then writes
 //   xh  [rows][k] f16 = RNE(x * 2^-e), groups of four stored (x0, x2), (x1, x3)
 //   xsx [rows][k/256][16] f16: per 32-block b of the super-block, the sum of
 //       the block's 32 f16 values (f32: lane partials ((h0+h1)+h2)+h3 over 8
@@ -88,43 +88,72 @@ RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t*
 //       lo[b] = f16(S - hi)
 //   xrs [rows] f32 = 2^e
 // and, optionally, the source values themselves to yout (f32 [rows][k]).
+// row exponent of the f16 layout from the row's max |x|
+RFXQ_DEV int act_f16_exp(float mx) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    return (mx > 0.0f && mx <= 3.4028235e38f) ? min(max(ilogbf(mx) - 8, -120), 120) : 0;
+}
+
+RFXQ_DEV float absmax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
+
+// the f16 layout of one row's four values at column c (lane's chunk)
+RFXQ_DEV void act_f16_chunk(float4 v, uint32_t lane, uint32_t c, uint64_t ro, uint32_t r, uint32_t nsb, float scale,
+                            uint16_t* __restrict__ xh, uint16_t* __restrict__ xsx, float* __restrict__ yout) {
+    if (yout) *reinterpret_cast<float4*>(yout + ro + c) = v;
+    const half_t h0 = (half_t)(v.x * scale), h1 = (half_t)(v.y * scale);
+    const half_t h2 = (half_t)(v.z * scale), h3 = (half_t)(v.w * scale);
+    uint2 hv;
+    hv.x = h2_bits(h2_t{h0, h2});
+    hv.y = h2_bits(h2_t{h1, h3});
+    *reinterpret_cast<uint2*>(xh + ro + c) = hv;
+    float s = (((float)h0 + (float)h1) + (float)h2) + (float)h3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    if ((lane & 7u) == 0u) {
+        const uint32_t blk = c / 32u;
+        const half_t hi = (half_t)s;
+        const half_t lo = (half_t)(s - (float)hi);
+        uint16_t* rec = xsx + ((uint64_t)r * nsb + blk / 8u) * 16u;
+        rec[blk & 7u] = __builtin_bit_cast(uint16_t, hi);
+        rec[8u + (blk & 7u)] = __builtin_bit_cast(uint16_t, lo);
+    }
+}
+
+// Rows of up to kActRegK values are read once, into registers; longer rows
+// are read twice (the maximum, then the layout).
+constexpr uint32_t kActRegK = 4096;
+
 template <class Src>
 RFXQ_DEV void act_f16_row(const Src& src, uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
                           uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
     const uint32_t lane = threadIdx.x & 63u;
-    float mx = 0.0f;
-    for (uint32_t c = 4u * lane; c < k; c += 256u) {
-        const float4 v = src.load(r, c);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.4028235e38f) e = min(max(ilogbf(mx) - 8, -120), 120);
-    const float scale = ldexpf(1.0f, -e);
     const uint64_t ro = (uint64_t)r * k;
     const uint32_t nsb = k / 256u;
-    for (uint32_t c = 4u * lane; c < k; c += 256u) {
-        const float4 v = src.load(r, c);
-        if (yout) *reinterpret_cast<float4*>(yout + ro + c) = v;
-        const half_t h0 = (half_t)(v.x * scale), h1 = (half_t)(v.y * scale);
-        const half_t h2 = (half_t)(v.z * scale), h3 = (half_t)(v.w * scale);
-        uint2 hv;
-        hv.x = h2_bits(h2_t{h0, h2});
-        hv.y = h2_bits(h2_t{h1, h3});
-        *reinterpret_cast<uint2*>(xh + ro + c) = hv;
-        float s = (((float)h0 + (float)h1) + (float)h2) + (float)h3;
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        if ((lane & 7u) == 0u) {
-            const uint32_t blk = c / 32u;
-            const half_t hi = (half_t)s;
-            const half_t lo = (half_t)(s - (float)hi);
-            uint16_t* rec = xsx + ((uint64_t)r * nsb + blk / 8u) * 16u;
-            rec[blk & 7u] = __builtin_bit_cast(uint16_t, hi);
-            rec[8u + (blk & 7u)] = __builtin_bit_cast(uint16_t, lo);
-        }
+    int e;
+    if (k <= kActRegK) {
+        constexpr uint32_t NC = kActRegK / 256u;
+        float4 v[NC];
+        float mx = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++)
+            if (i < nsb) v[i] = src.load(r, 4u * lane + 256u * i);
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++)
+            if (i < nsb) mx = fmaxf(mx, absmax4(v[i]));
+        e = act_f16_exp(mx);
+        const float scale = ldexpf(1.0f, -e);
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++)
+            if (i < nsb) act_f16_chunk(v[i], lane, 4u * lane + 256u * i, ro, r, nsb, scale, xh, xsx, yout);
+    } else {
+        float mx = 0.0f;
+        for (uint32_t c = 4u * lane; c < k; c += 256u) mx = fmaxf(mx, absmax4(src.load(r, c)));
+        e = act_f16_exp(mx);
+        const float scale = ldexpf(1.0f, -e);
+        for (uint32_t c = 4u * lane; c < k; c += 256u)
+            act_f16_chunk(src.load(r, c), lane, c, ro, r, nsb, scale, xh, xsx, yout);
     }
     if (lane == 0u) xrs[r] = ldexpf(1.0f, e);
 }

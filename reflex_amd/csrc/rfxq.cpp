@@ -78,6 +78,11 @@ struct GemvDesc {
     uint32_t pad[4];
 };
 constexpr uint32_t kGemvInline = 4;
+#ifndef RFXQ_GEMV_RING
+#define RFXQ_GEMV_RING 2
+#endif
+// the GEMV kernel's static LDS: per wave RFXQ_GEMV_RING slots of 4 KB
+constexpr uint32_t kGemvRingLds = RFXQ_GEMV_RING * 16384u;
 struct GemvRange {
     uint32_t d0, it0, d1, it1;
 };
@@ -565,7 +570,7 @@ uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) {
     uint64_t g = (total_bytes + kb * 1024u - 1u) / (kb * 1024u);
     g = std::max<uint64_t>(g, 2u * (uint32_t)c->cus);
     // LDS per workgroup: the 32 KB weight ring, x and its sums, and up to 4 KB of row results
-    const uint32_t occ = std::min<uint32_t>(4u, (160u * 1024u) / (32768u + kmax * 2u + kmax / 4u + 4096u));
+    const uint32_t occ = std::min<uint32_t>(4u, (160u * 1024u) / (kGemvRingLds + kmax * 2u + kmax / 4u + 4096u));
     const uint64_t slots = (uint64_t)std::max(1, c->cus) * std::max(1u, occ);
     if (g > slots) {
         const uint64_t waves = (total_bytes + slots * 512u * 1024u - 1u) / (slots * 512u * 1024u);
