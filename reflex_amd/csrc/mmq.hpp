@@ -536,7 +536,15 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float
                                                                     uint32_t splits) {
     for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) {
         float s = ws[i];
-        for (uint32_t z = 1; z < splits; z++) s += ws[(uint64_t)z * n + i];
+        // eight loads in flight per round trip, added in split order
+        for (uint32_t z0 = 1; z0 < splits; z0 += 8u) {
+            float v[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; u++) v[u] = z0 + u < splits ? ws[(uint64_t)(z0 + u) * n + i] : 0.0f;
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; u++)
+                if (z0 + u < splits) s += v[u];
+        }
         y[i] = s;
     }
 }

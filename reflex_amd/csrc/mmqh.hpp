@@ -55,10 +55,18 @@
 
 namespace mmqh {
 
-constexpr uint32_t BM = 128, BN = 256, kThreads = 256;
-constexpr uint32_t kAct = 16384, kSx = 4096;
-constexpr uint32_t kLds = 2 * kAct + kSx;
-static_assert(kLds <= 81920, "two workgroups per CU");
+// MT = 32-row tiles per wave (4: 128-row workgroup tiles; 1: 32-row tiles,
+// the fused few-row form and small expert groups: weights read once per 32
+// rows)
+constexpr uint32_t BN = 256, kThreads = 256;
+template <int MT>
+struct Tile {
+    static constexpr uint32_t BM = 32u * MT;
+    static constexpr uint32_t kAct = BM * 128u;  // activation stage: BM rows x 64 f16
+    static constexpr uint32_t kSx = BM * 32u;    // Q4_K: the super-block's Sx records of BM rows
+    static constexpr uint32_t kLds = 2u * kAct + kSx;
+};
+static_assert(Tile<4>::kLds <= 81920, "two workgroups per CU");
 
 // f16 of an f32, round to nearest even, as the low 16 bits
 RFXQ_DEV uint32_t f16_rne(float v) { return __builtin_bit_cast(uint16_t, (half_t)v); }
@@ -241,9 +249,11 @@ RFXQ_DEV u4_t q6k_multipliers(u4_t sc, uint32_t dbits, uint32_t h) {
 }  // namespace mmqh
 
 
-// One 128x256 tile (and one split-K range) of Y = X . W^T for Q4_K weights.
+// One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q4_K weights.
+template <int MT>
 RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     using namespace mmqh;
+    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
     MmqDesc ds = dv;
     {
         uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
@@ -272,11 +282,11 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     const rsrc_t r_sx = make_rsrc(ds.xds, 0xFFFFFFFFu);
     // Staged activations: piece 256u + tid is chunk tid%8 of row 32u + tid/8
     // (LDS + 4096u); LDS chunk c of row r holds logical chunk c ^ ((r/2)%8).
-    // Sx: half tid%2 of row tid/2.
+    // Sx: half tid%2 of row tid/2 (threads below 2 BM).
     const uint32_t ra = tid >> 3, ca = tid & 7u;
-    uint32_t g_act[4];
+    uint32_t g_act[MT];
 #pragma unroll
-    for (int u = 0; u < 4; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + 16u * ca;
+    for (int u = 0; u < MT; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + 16u * ca;
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
     const uint32_t g_sx = act_row(ds, m0 + (tid >> 1)) * rec_bytes + 16u * (tid & 1u);
     // Weights go straight to registers (no other wave reads a wave's
@@ -295,14 +305,15 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     // Loads are issued unconditionally so that the compiler's wait counts stay
     // exact across the loop: past the last stage a lane reloads the last stage
     // (in bounds; never used).
-    u4_t sa[4], ssx, qn[2], hn[2];
-    auto load_act = [&](uint32_t st, int H) {
+    const bool sx_lane = tid < 2u * BM;
+    u4_t sa[MT], ssx, qn[2], hn[2];
+    auto load_act = [&](uint32_t st) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-            sa[2 * H + u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[2 * H + u], 512u * sb + 128u * g, 0);
-        if (H == 0 && (st & 3u) == 0u) ssx = __builtin_amdgcn_raw_buffer_load_b128(r_sx, g_sx, 32u * sb, 0);
+        for (int u = 0; u < MT; u++)
+            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 128u * g, 0);
+        if ((st & 3u) == 0u && sx_lane) ssx = __builtin_amdgcn_raw_buffer_load_b128(r_sx, g_sx, 32u * sb, 0);
     };
     auto load_w = [&](uint32_t st) {
         const uint32_t sl = min(st, nst - 1u);
@@ -313,16 +324,16 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 #pragma unroll
             for (int j = 0; j < 2; j++) hn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_h[j], 144u * sb, 0);
     };
-    auto store_act = [&](uint32_t st, int H) {
+    auto store_act = [&](uint32_t st) {
         uint8_t* S = lds + (st & 1u) * kAct;
 #pragma unroll
-        for (int u = 0; u < 2; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * (2u * H + u)) = sa[2 * H + u];
-        if (H == 0 && (st & 3u) == 0u) reinterpret_cast<u4_t*>(sx_lds)[tid] = ssx;
+        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
+        if ((st & 3u) == 0u && sx_lane) reinterpret_cast<u4_t*>(sx_lds)[tid] = ssx;
     };
 
-    v16f_t acc[4][2];
+    v16f_t acc[MT][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = v16f_t{};
+    for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v16f_t{};
     // LDS read offsets (16-byte units): activations of row l32 of row tile 0,
     // logical chunk 4e + 2h + step
     uint32_t a_act[2][2];
@@ -337,10 +348,8 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 
     if (nst > 0u) {
         load_w(0u);
-        load_act(0u, 0);
-        store_act(0u, 0);
-        load_act(0u, 1);
-        store_act(0u, 1);
+        load_act(0u);
+        store_act(0u);
     }
     __syncthreads();
     MMQH_PROBE_BEGIN();
@@ -355,8 +364,7 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                 if (g == 0u) hdr[j] = hn[j];
             }
             load_w(st + 1u);
-            load_act(st + 1u, 0);
-            load_act(st + 1u, 1);
+            load_act(st + 1u);
             const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
             if (g == 0u) {
                 // super-block start: the columns' multipliers, and the
@@ -365,7 +373,7 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 #pragma unroll
                 for (int j = 0; j < 2; j++) q4k_sb_operands(hdr[j], cop[j], dsc[j]);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < MT; i++) {
                     const u4_t sxo = reinterpret_cast<const u4_t*>(sx_lds)[2u * (32u * i + l32) + h];
                     acc[i][0] = mfma16(cop[0], sxo, acc[i][0]);
                     acc[i][1] = mfma16(cop[1], sxo, acc[i][1]);
@@ -392,50 +400,49 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                 return e ? q4k_codes_f16<1>(a0, a1, b0, b1, sm[1][j], mhi, mg)
                          : q4k_codes_f16<0>(a0, a1, b0, b1, sm[0][j], mlo, mg);
             };
-            u4_t Xc[4], Wc[2];
+            u4_t Xc[MT], Wc[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) Xc[i] = S16[256u * i + a_act[0][0]];
+            for (int i = 0; i < MT; i++) Xc[i] = S16[256u * i + a_act[0][0]];
             Wc[0] = wop(0, 0);
             Wc[1] = wop(0, 1);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                u4_t Xn[4], Wn[2];
+                u4_t Xn[MT], Wn[2];
                 if (t < 3) {
                     const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
+                    for (int i = 0; i < MT; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
                     Wn[0] = wop(t + 1, 0);
                     Wn[1] = wop(t + 1, 1);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < MT; i++) {
                     acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
                     acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
                 }
                 if (t < 3) {
-                    // interleave: per MFMA one LDS read (first four) and a few VALU ops
+                    // interleave: per MFMA one LDS read (first MT) and a few VALU ops
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
+                    for (int u = 0; u < MT; u++) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
+                    for (int u = 0; u < MT; u++) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) Xc[i] = Xn[i];
+                    for (int i = 0; i < MT; i++) Xc[i] = Xn[i];
                     Wc[0] = Wn[0];
                     Wc[1] = Wn[1];
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
             MMQH_PROBE(1);
-            store_act(st + 1u, 0);
-            store_act(st + 1u, 1);
+            store_act(st + 1u);
             MMQH_PROBE(2);
             __syncthreads();
             MMQH_PROBE(3);
@@ -446,7 +453,7 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < MT; i++) {
         const uint32_t row = m0 + 32u * i + l32;
         const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
 #pragma unroll
@@ -454,19 +461,24 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmqh_q4k(MmqArgs args) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::kLds];
-    if (blockDim.x != mmqh::kThreads) return;  // the tile assumes exactly kThreads lanes
-    const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);
-    const MmqDesc d = mmq_pick(args, b);
-    if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
-    mmqh_q4k_tile(d, b - d.wg_begin, lds);
-}
+#define RFXQ_MMQH_ENTRY(NAME, TILE, MT, WPE)                                                                \
+    extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
+        __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::Tile<MT>::kLds];                            \
+        if (blockDim.x != mmqh::kThreads) return; /* the tile assumes exactly kThreads lanes */               \
+        const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);                                           \
+        const MmqDesc d = mmq_pick(args, b);                                                                 \
+        if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;                                     \
+        TILE<MT>(d, b - d.wg_begin, lds);                                                                     \
+    }
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k, mmqh_q4k_tile, 4, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m32, mmqh_q4k_tile, 1, 4)
 
-// One 128x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
+// One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
 // the Q4_K tile's layout and pipeline, with the Q6_K weight operands.
+template <int MT>
 RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     using namespace mmqh;
+    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
     MmqDesc ds = dv;
     {
         uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
@@ -495,10 +507,10 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     const uint32_t ra = tid >> 3, ca = tid & 7u;
     // activations: the Q4_K tile's staging, but the stage's logical chunks 4-7
     // (group B) sit 128 bytes after chunks 0-3 (group A) in the f16 row
-    uint32_t g_act[4];
+    uint32_t g_act[MT];
     const uint32_t cofs = 16u * ca + (ca >= 4u ? 64u : 0u);
 #pragma unroll
-    for (int u = 0; u < 4; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + cofs;
+    for (int u = 0; u < MT; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + cofs;
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
     // Weights straight to registers: lane (l32, h) of n-tile j loads, per
     // stage, positions [16h, 16h + 16) of the ql and qh pieces of column
@@ -512,16 +524,15 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
     const uint32_t nst = 4u * (sb1 - sb0);
 
-    u4_t sa[4], qln[2], qhn[2], scn[2];
+    u4_t sa[MT], qln[2], qhn[2], scn[2];
     uint32_t dn[2];
-    auto load_act = [&](uint32_t st, int H) {
+    auto load_act = [&](uint32_t st) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
         const uint32_t n = g >> 1, s = g & 1u;
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-            sa[2 * H + u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[2 * H + u],
-                                                                  512u * sb + 256u * n + 64u * s, 0);
+        for (int u = 0; u < MT; u++)
+            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 256u * n + 64u * s, 0);
     };
     // 16-byte loads at 2-byte-aligned offsets (unaligned access mode)
     auto load_w = [&](uint32_t st) {
@@ -543,15 +554,15 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
             }
         }
     };
-    auto store_act = [&](uint32_t st, int H) {
+    auto store_act = [&](uint32_t st) {
         uint8_t* S = lds + (st & 1u) * kAct;
 #pragma unroll
-        for (int u = 0; u < 2; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * (2u * H + u)) = sa[2 * H + u];
+        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
     };
 
-    v16f_t acc[4][2];
+    v16f_t acc[MT][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = v16f_t{};
+    for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v16f_t{};
     uint32_t a_act[2][2];
 #pragma unroll
     for (int e = 0; e < 2; e++)
@@ -563,10 +574,8 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 
     if (nst > 0u) {
         load_w(0u);
-        load_act(0u, 0);
-        load_act(0u, 1);
-        store_act(0u, 0);
-        store_act(0u, 1);
+        load_act(0u);
+        store_act(0u);
     }
     __syncthreads();
     MMQH_PROBE_BEGIN();
@@ -582,8 +591,7 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                 if (g == 0u) mult[j] = q6k_multipliers(scn[j], dn[j], h);
             }
             load_w(st + 1u);
-            load_act(st + 1u, 0);
-            load_act(st + 1u, 1);
+            load_act(st + 1u);
             const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
             MMQH_PROBE(0);
             // groups A (e = 0) and B (e = 1): multipliers i = 4n + s + 2e
@@ -611,49 +619,48 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
                 return q6k_codes_f16<1>(L[j][u], L[j][u + 1], Ls[j][u], Ls[j][u + 1], Qa[j][u], Qa[j][u + 1],
                                         Qb[j][u], Qb[j][u + 1], sm[1][j], mlb, mqb, mg);
             };
-            u4_t Xc[4], Wc[2];
+            u4_t Xc[MT], Wc[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) Xc[i] = S16[256u * i + a_act[0][0]];
+            for (int i = 0; i < MT; i++) Xc[i] = S16[256u * i + a_act[0][0]];
             Wc[0] = wop(0, 0);
             Wc[1] = wop(0, 1);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                u4_t Xn[4], Wn[2];
+                u4_t Xn[MT], Wn[2];
                 if (t < 3) {
                     const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
+                    for (int i = 0; i < MT; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
                     Wn[0] = wop(t + 1, 0);
                     Wn[1] = wop(t + 1, 1);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < MT; i++) {
                     acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
                     acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
                 }
                 if (t < 3) {
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
+                    for (int u = 0; u < MT; u++) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
+                    for (int u = 0; u < MT; u++) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) Xc[i] = Xn[i];
+                    for (int i = 0; i < MT; i++) Xc[i] = Xn[i];
                     Wc[0] = Wn[0];
                     Wc[1] = Wn[1];
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
             MMQH_PROBE(1);
-            store_act(st + 1u, 0);
-            store_act(st + 1u, 1);
+            store_act(st + 1u);
             MMQH_PROBE(2);
             __syncthreads();
             MMQH_PROBE(3);
@@ -664,7 +671,7 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < MT; i++) {
         const uint32_t row = m0 + 32u * i + l32;
         const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
 #pragma unroll
@@ -672,11 +679,5 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rfxq_mmqh_q6k(MmqArgs args) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::kLds];
-    if (blockDim.x != mmqh::kThreads) return;  // the tile assumes exactly kThreads lanes
-    const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);
-    const MmqDesc d = mmq_pick(args, b);
-    if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;
-    mmqh_q6k_tile(d, b - d.wg_begin, lds);
-}
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, mmqh_q6k_tile, 4, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m32, mmqh_q6k_tile, 1, 3)

@@ -158,13 +158,78 @@ RFXQ_DEV void act_f16_row(const Src& src, uint32_t r, uint32_t k, uint16_t* __re
     if (lane == 0u) xrs[r] = ldexpf(1.0f, e);
 }
 
+// One row by the whole 256-thread workgroup: thread t takes the four values
+// at 4t + 1024i, held in registers up to 16384 values (longer rows are read
+// twice); the row maximum
+// combines the four waves through LDS. Same layouts and arithmetic as
+// act_f16_row (the block sums are formed by the same 8 lanes in the same
+// order), so the result does not depend on which form wrote it.
+template <class Src>
+RFXQ_DEV void act_f16_row_wg(const Src& src, uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
+                             uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
+    __shared__ float wmax[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint64_t ro = (uint64_t)r * k;
+    const uint32_t nsb = k / 256u;
+    constexpr uint32_t NC = 16;  // rows up to 16384 values stay in registers
+    float4 v[NC];
+    float mx = 0.0f;
+    const bool reg = k <= NC * 1024u;
+    if (reg) {
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++) {
+            const uint32_t c = 4u * tid + 1024u * i;
+            if (c < k) v[i] = src.load(r, c);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++)
+            if (4u * tid + 1024u * i < k) mx = fmaxf(mx, absmax4(v[i]));
+    } else {
+        for (uint32_t c = 4u * tid; c < k; c += 1024u) mx = fmaxf(mx, absmax4(src.load(r, c)));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0u) wmax[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    __syncthreads();  // wmax is reused by the next row
+    const int e = act_f16_exp(mx);
+    const float scale = ldexpf(1.0f, -e);
+    if (reg) {
+#pragma unroll
+        for (uint32_t i = 0; i < NC; i++) {
+            const uint32_t c = 4u * tid + 1024u * i;
+            if (c < k) act_f16_chunk(v[i], lane, c, ro, r, nsb, scale, xh, xsx, yout);
+        }
+    } else {
+        for (uint32_t c = 4u * tid; c < k; c += 1024u) act_f16_chunk(src.load(r, c), lane, c, ro, r, nsb, scale, xh, xsx, yout);
+    }
+    if (tid == 0u) xrs[r] = ldexpf(1.0f, e);
+}
+
+// Rows per workgroup of the f16 activation kernels: a row per wave (4 per
+// workgroup) for many short rows, a whole workgroup per row otherwise (few
+// rows, or rows too long for one wave's registers). The host sizes grids by
+// the same rule.
+RFXQ_DEV bool act_wave_rows(uint32_t rows, uint32_t k) { return k <= kActRegK && rows >= 128u; }
+
+template <class Src>
+RFXQ_DEV void act_f16_rows(const Src& src, uint32_t rows, uint32_t k, uint32_t b, uint32_t nb,
+                           uint16_t* __restrict__ xh, uint16_t* __restrict__ xsx, float* __restrict__ xrs,
+                           float* __restrict__ yout) {
+    if (act_wave_rows(rows, k)) {
+        for (uint32_t r = b * 4u + (threadIdx.x >> 6); r < rows; r += nb * 4u)
+            act_f16_row(src, r, k, xh, xsx, xrs, yout);
+    } else {
+        for (uint32_t r = b; r < rows; r += nb) act_f16_row_wg(src, r, k, xh, xsx, xrs, yout);
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16(const float* __restrict__ x, uint32_t ldx,
                                                               const int32_t* __restrict__ src_rows, uint32_t rows,
                                                               uint32_t k, uint16_t* __restrict__ xh,
                                                               uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
-    const QuantSrcPlain src{x, ldx, src_rows};
-    for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4u)
-        act_f16_row(src, r, k, xh, xsx, xrs, nullptr);
+    act_f16_rows(QuantSrcPlain{x, ldx, src_rows}, rows, k, blockIdx.x, gridDim.x, xh, xsx, xrs, nullptr);
 }
 
 // Several activations in one launch (grouped GEMMs): workgroups
@@ -186,9 +251,8 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_multi(const ActF1
         else hi = mid - 1u;
     }
     const ActF16Desc d = table[lo];
-    const QuantSrcPlain src{d.x, d.k, nullptr};
-    for (uint32_t r = (blockIdx.x - d.wg_begin) * 4u + (threadIdx.x >> 6); r < d.rows; r += d.wgs * 4u)
-        act_f16_row(src, r, d.k, d.xh, d.xsx, d.xrs, nullptr);
+    act_f16_rows(QuantSrcPlain{d.x, d.k, nullptr}, d.rows, d.k, blockIdx.x - d.wg_begin, d.wgs, d.xh, d.xsx, d.xrs,
+                 nullptr);
 }
 
 extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,
@@ -333,7 +397,5 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_silu_and_mul_q8_1(const f
     if (xq)
         quant_q8_1_rows(src, rows, k, xq, k, xds, y, ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6,
                         ((uint64_t)gridDim.x * blockDim.x) >> 6);
-    if (xh)
-        for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4u)
-            act_f16_row(src, r, k, xh, xsx, xrs, xq ? nullptr : y);
+    if (xh) act_f16_rows(src, rows, k, blockIdx.x, gridDim.x, xh, xsx, xrs, xq ? nullptr : y);
 }

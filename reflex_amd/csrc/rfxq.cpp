@@ -131,7 +131,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmqh[2] = {}, act_f16 = nullptr, act_f16_multi = nullptr;
+    hipFunction_t mmqh[2][2] = {}, act_f16 = nullptr, act_f16_multi = nullptr;  // [type][128-row, 32-row tiles]
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
@@ -194,8 +194,10 @@ int load_ctx(int device, Ctx** out) {
         {&c->dots[0], "rfxq_mmq_dots_q4k"},
         {&c->dots[1], "rfxq_mmq_dots_q6k"},
         {&c->dots[2], "rfxq_mmq_dots_q8_0"},
-        {&c->mmqh[0], "rfxq_mmqh_q4k"},
-        {&c->mmqh[1], "rfxq_mmqh_q6k"},
+        {&c->mmqh[0][0], "rfxq_mmqh_q4k"},
+        {&c->mmqh[1][0], "rfxq_mmqh_q6k"},
+        {&c->mmqh[0][1], "rfxq_mmqh_q4k_m32"},
+        {&c->mmqh[1][1], "rfxq_mmqh_q6k_m32"},
         {&c->act_f16, "rfxq_act_f16"},
         {&c->act_f16_multi, "rfxq_act_f16_multi"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
@@ -733,47 +735,55 @@ bool f16_kernel(const rfxq_weight* w, uint32_t rows) {
     return mmq_f16() && f16_capable(w->ggml_type, w->in_features, w->out_features, rows);
 }
 
-// weight columns per workgroup tile (rows: kMmqBM, or 64 for the int8 *_m64 kernels)
-uint32_t tile_bn(uint32_t ty, bool f16) { (void)ty; return f16 ? 256u : 128u; }
+// weight columns per workgroup tile: 256 on the f16 kernels, 128 on the int8 ones
+uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 
 // How a GEMM of `rows` rows runs (Model::gemm's choice between the fused GEMV,
 // the MMA kernel and its split-K, kernels.rs:628-713 quant_mma_splits /
 // block_rows / max_rows and :2144-2169, re-derived for MI355X):
 // - one GEMV per row (PATH_GEMV_ROWS) for a single row, with the MMA path off
-//   (REFLEX_QUANT_MMA=0), above REFLEX_QUANT_MMA_MAX_ROWS, up to
-//   REFLEX_QUANT_FUSED_MAX_ROWS rows (default 16: a 128-row tile would be
-//   mostly idle), and for Q8_0 in f16 mode (no f16-activation Q8_0 kernel; the
-//   int8 format's error floor exceeds the north star's bound) or with
-//   in_features not a multiple of 256;
+//   (REFLEX_QUANT_MMA=0), above REFLEX_QUANT_MMA_MAX_ROWS, for Q8_0 in f16
+//   mode (no f16-activation Q8_0 kernel; the int8 format's error floor
+//   exceeds the north star's bound), with in_features not a multiple of 256,
+//   and up to REFLEX_QUANT_FUSED_MAX_ROWS rows (default 16) on the int8 path,
+//   up to kGemvRowsMax of them on the f16 path (a GEMV per row re-reads the
+//   weights, cheaper than the few-row tiles' launch pair below 5 rows);
 // - otherwise the f16-activation kernels (PATH_MMQ_F16: Q4_K, and Q6_K with an
-//   even super-block count per row) or the int8 kernels (PATH_MMQ_INT8; 64-row
-//   tiles with REFLEX_QUANT_MMA_TILE=64);
+//   even super-block count per row): 32-row tiles up to 32 rows (the fused
+//   few-row form: each weight read once for all rows), 128-row tiles above,
+//   or the int8 kernels (PATH_MMQ_INT8; 64-row tiles with
+//   REFLEX_QUANT_MMA_TILE=64);
 // - split-K: none once the tiles cover half the CUs (each CU holds two
 //   workgroups; a split costs a partials round trip and a reduce launch),
 //   else enough splits for about two workgroups per CU, each of at least two
-//   super-blocks; REFLEX_QUANT_MMA_SPLITS forces the count.
+//   super-blocks (one with 32-row tiles); REFLEX_QUANT_MMA_SPLITS forces the
+//   count.
 enum : uint32_t { PATH_GEMV_ROWS = RFXQ_PATH_GEMV_ROWS, PATH_MMQ_INT8 = RFXQ_PATH_MMQ_INT8, PATH_MMQ_F16 = RFXQ_PATH_MMQ_F16 };
+constexpr uint32_t kGemvRowsMax = 4;
 
 
 rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o) {
     rfxq_gemm_policy p;
     std::memset(&p, 0, sizeof p);
     p.splits = 1;
+    const bool f16 = o.mmq_f16 && k % 256u == 0 && f16_capable(ty, k, n, rows);
     const bool gemv = rows <= 1 || !o.quant_mma || (o.quant_mma_max_rows && rows > o.quant_mma_max_rows) ||
-                      rows <= o.fused_max_rows || k % 256u != 0 || (ty == RFXQ_TYPE_Q8_0 && o.mmq_f16);
+                      (rows <= o.fused_max_rows && (!f16 || rows <= kGemvRowsMax)) || k % 256u != 0 ||
+                      (ty == RFXQ_TYPE_Q8_0 && o.mmq_f16);
     if (gemv) {
         p.path = PATH_GEMV_ROWS;
         return p;
     }
-    const bool f16 = o.mmq_f16 && f16_capable(ty, k, n, rows);
     p.path = f16 ? PATH_MMQ_F16 : PATH_MMQ_INT8;
-    p.tile_m = !f16 && o.quant_mma_tile == 64 ? 64u : kMmqBM;
-    p.tile_n = tile_bn(ty, f16);
+    p.tile_m = f16 ? (rows <= 32u ? 32u : kMmqBM) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
+    p.tile_n = tile_bn(f16);
     const uint32_t nsb = k / 256u;
     const uint32_t tiles = ((rows + p.tile_m - 1u) / p.tile_m) * ((n + p.tile_n - 1u) / p.tile_n);
     uint32_t splits = 1;
     if (o.quant_mma_splits) splits = o.quant_mma_splits;
-    else if (2u * tiles < std::max(cus, 1u)) splits = std::min((2u * cus + tiles - 1u) / tiles, std::max(1u, nsb / 2u));
+    else if (2u * tiles < std::max(cus, 1u))
+        // 32-row tiles stream weights (few rows): splits down to one super-block
+        splits = std::min((2u * cus + tiles - 1u) / tiles, std::max(1u, p.tile_m == 32u ? nsb : nsb / 2u));
     splits = std::min(std::max(1u, splits), nsb);
     p.sb_per_split = (nsb + splits - 1u) / splits;
     p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
@@ -848,6 +858,13 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
 }
 
 // f16 layout of x (rfxq_act_f16): one wave per row
+// workgroups of an f16 activation launch: a row per wave (4 per workgroup)
+// for at least 128 rows of at most 4096 values, else a row per workgroup
+// (the kernels' act_wave_rows rule)
+uint32_t act_f16_grid(uint32_t rows, uint32_t k) {
+    return k <= 4096u && rows >= 128u ? std::min<uint32_t>((rows + 3u) / 4u, 4096u) : std::min<uint32_t>(rows, 16384u);
+}
+
 int launch_act_f16(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
                    uint8_t* base, const ActLayout& L, hipStream_t stream) {
     struct {
@@ -860,8 +877,7 @@ int launch_act_f16(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows
         float* xrs;
     } a = {x, ldx, 0, src_rows, rows, k, reinterpret_cast<uint16_t*>(base + L.xh),
            reinterpret_cast<uint16_t*>(base + L.xsx), reinterpret_cast<float*>(base + L.xrs)};
-    const uint32_t grid = std::min<uint32_t>((rows + 3u) / 4u, 4096u);
-    return launch(c->act_f16, grid, 0, stream, &a, sizeof a, "rfxq_act_f16 launch");
+    return launch(c->act_f16, act_f16_grid(rows, k), 0, stream, &a, sizeof a, "rfxq_act_f16 launch");
 }
 
 // the activation layouts of L at `base` from x
@@ -876,17 +892,18 @@ int launch_act(Ctx* c, const float* x, uint32_t rows, uint32_t k, uint8_t* base,
     return RFXQ_OK;
 }
 
-// f16: Q4_K / Q6_K descriptors on rfxq_mmqh_q4k / _q6k (f16 activation layout)
-// m64: the descriptors are tiled by 64 rows (rfxq_mmq_*_m64)
+// f16: Q4_K / Q6_K descriptors on rfxq_mmqh_q4k / _q6k (f16 activation
+// layout; tile_m 32: the *_m32 kernels); int8: tile_m 64 takes rfxq_mmq_*_m64
 int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
-               bool dots, hipStream_t stream, bool f16 = false, bool m64 = false) {
+               bool dots, hipStream_t stream, bool f16 = false, uint32_t tile_m = kMmqBM) {
+    const bool m64 = !f16 && tile_m == 64u;
     MmqArgs a;
     std::memset(&a, 0, sizeof a);
     a.ndesc = count;
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && !dots && !m64 && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)];
+    if (f16 && !dots && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : 0];
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch", kMmqThreads);
 }
 
@@ -952,7 +969,7 @@ int gemm_run(Ctx* c, const GemmPlan& p, const uint8_t* act, const ActLayout& L, 
     d.splits = p.pol.splits;
     d.sb_per_split = p.pol.sb_per_split;
     const uint32_t wgs = p.tiles_m * p.tiles_n * p.pol.splits;
-    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, p.f16, p.pol.tile_m == 64u))
+    if (int rc = launch_mmq(c, w->ggml_type, &d, 1, nullptr, wgs, false, stream, p.f16, p.pol.tile_m))
         return rc;
     if (p.pol.splits > 1)
         if (int rc = launch_reduce(c, part, y, (uint64_t)rows * n, p.pol.splits, stream)) return rc;
@@ -988,7 +1005,8 @@ int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
 // and each MMQ kernel runs as one launch over all of its GEMMs. Each GEMM
 // takes the single-GEMM policy's path (gemm_policy); GEMMs on the GEMV path
 // run as one GEMV per row in one table-driven launch.
-constexpr uint32_t kGroupKernels = 9;  // type_index + 3 * variant (0: int8, 1: int8 64-row, 2: f16)
+// type_index + 3 * variant (0: int8, 1: int8 64-row, 2: f16, 3: f16 32-row)
+constexpr uint32_t kGroupKernels = 12;
 struct GemmGroup {
     struct Act {
         const float* x;
@@ -1017,7 +1035,11 @@ struct GemmGroup {
 };
 
 bool group_f16(uint32_t g) { return g >= 6u; }
-bool group_m64(uint32_t g) { return g >= 3u && g < 6u; }
+uint32_t group_tile_m(uint32_t g) {
+    const uint32_t v = g / 3u;
+    return v == 1u ? 64u : v == 3u ? 32u : kMmqBM;
+}
+uint32_t group_variant(bool f16, uint32_t tile_m) { return f16 ? (tile_m == 32u ? 3u : 2u) : (tile_m == 64u ? 1u : 0u); }
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
@@ -1038,7 +1060,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             continue;
         }
         const bool f16 = pol.path == PATH_MMQ_F16;
-        item_kernel[i] = type_index(it.w->ggml_type) + 3u * (f16 ? 2u : pol.tile_m == 64u ? 1u : 0u);
+        item_kernel[i] = type_index(it.w->ggml_type) + 3u * group_variant(f16, pol.tile_m);
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
@@ -1074,7 +1096,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         d.k = k;
         d.type = it.w->ggml_type;
         d.ldy = d.n;
-        const uint32_t bm = group_m64(t) ? 64u : kMmqBM, bn = tile_bn(d.type, group_f16(t));
+        const uint32_t bm = group_tile_m(t), bn = tile_bn(group_f16(t));
         d.tiles_m = (rows + bm - 1u) / bm;
         d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
@@ -1095,7 +1117,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         for (uint32_t i = 0; i < v.size(); i++) {
             MmqDesc& d = v[i];
             const uint32_t nsb = d.k / 256u;
-            const uint32_t s = std::min(want, forced ? nsb : std::max(1u, nsb / 2u));
+            const uint32_t s = std::min(want, forced || group_tile_m(t) == 32u ? nsb : std::max(1u, nsb / 2u));
             d.sb_per_split = (nsb + s - 1u) / s;
             d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
             if (d.splits > 1u) {
@@ -1116,7 +1138,7 @@ int launch_group_kernel(Ctx* c, const GemmGroup& g, uint32_t t, const MmqDesc* t
     const auto& v = g.descs[t];
     if (v.empty()) return RFXQ_OK;
     return launch_mmq(c, v[0].type, v.data(), (uint32_t)v.size(), table, g.wgs[t], false, stream, group_f16(t),
-                      group_m64(t));
+                      group_tile_m(t));
 }
 
 // the split-K reduces of kernel t
@@ -1572,7 +1594,7 @@ int rfxq_gemm_batch(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, 
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n * d[j].splits;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_m64(t)))
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_tile_m(t)))
                 return rc;
         }
         if (int rc = run_group_reduces(c, g, t, stream)) return rc;
@@ -1712,8 +1734,8 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         const rfxq_gemm_q8_1_item& it = items[i];
         const uint32_t k = it.w->in_features;
         const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, it.w->out_features, rows);
-        const bool m64 = !f16 && o.quant_mma_tile == 64u;
-        const uint32_t t = type_index(it.w->ggml_type) + 3u * (f16 ? 2u : m64 ? 1u : 0u);
+        const uint32_t tile_m = f16 ? (rows <= 32u ? 32u : kMmqBM) : o.quant_mma_tile == 64u ? 64u : kMmqBM;
+        const uint32_t t = type_index(it.w->ggml_type) + 3u * group_variant(f16, tile_m);
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;
@@ -1724,7 +1746,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         d.k = k;
         d.type = it.w->ggml_type;
         d.ldy = d.n;
-        const uint32_t bm = m64 ? 64u : kMmqBM, bn = tile_bn(d.type, f16);
+        const uint32_t bm = tile_m, bn = tile_bn(f16);
         d.tiles_m = (rows + bm - 1u) / bm;
         d.tiles_n = (d.n + bn - 1u) / bn;
         d.splits = 1;
@@ -1742,7 +1764,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
                 d[j].wg_begin = wg;
                 wg += d[j].tiles_m * d[j].tiles_n;
             }
-            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_m64(t)))
+            if (int rc = launch_mmq(c, d[0].type, d, cnt, nullptr, wg, false, stream, group_f16(t), group_tile_m(t)))
                 return rc;
         }
     }
@@ -1794,7 +1816,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
                 plan->qgrid += wgs;
             }
             if (a.need_h) {
-                const uint32_t wgs = std::min<uint32_t>((rows + 3u) / 4u, 4096u);
+                const uint32_t wgs = act_f16_grid(rows, a.k);
                 hq.push_back(ActF16Desc{a.x, reinterpret_cast<uint16_t*>(ab + a.L.xh),
                                         reinterpret_cast<uint16_t*>(ab + a.L.xsx), reinterpret_cast<float*>(ab + a.L.xrs),
                                         rows, a.k, plan->hgrid, wgs});
@@ -2113,12 +2135,12 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     float* d_cw = reinterpret_cast<float*>(B + o_cw);
     MmqDesc* d_desc = reinterpret_cast<MmqDesc*>(B + o_desc);
 
-    // descriptor tables: [gate+up descs][down descs]; on the int8 kernels
-    // experts averaging at most 48 routed rows take 64-row tiles
+    // descriptor tables: [gate+up descs][down descs]; experts averaging at
+    // most 48 routed rows take 32-row (f16) or 64-row (int8) tiles
     uint32_t used = 0;
     for (uint32_t e = 0; e < expert_count; e++) used += off[e + 1] > off[e];
-    const bool m64 = !f16 && used && P <= 48u * used;
-    const uint32_t bm = m64 ? 64u : kMmqBM;
+    const bool small = used && P <= 48u * used;
+    const uint32_t bm = small ? (f16 ? 32u : 64u) : kMmqBM;
     std::vector<MmqDesc> descs;
     uint32_t wg_gu = 0;
     // act: the activation layouts (rows gathered through rws, or starting at row r0)
@@ -2145,7 +2167,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         d.type = ew.ggml_type;
         d.ldy = n;
         d.tiles_m = (m + bm - 1u) / bm;
-        const uint32_t bn = tile_bn(d.type, f16);
+        const uint32_t bn = tile_bn(f16);
         d.tiles_n = (n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = d.k / 256u;
@@ -2179,14 +2201,14 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
 
     if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
     if (n_gu) {
-        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, m64))
+        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, bm))
             return rc;
     }
     if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
     if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
     if (n_dn) {
         if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
-                                f16, m64))
+                                f16, bm))
             return rc;
     }
     {
@@ -2318,9 +2340,10 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     MmqDesc* d_gu = reinterpret_cast<MmqDesc*>(B + o_dgu);
     MmqDesc* d_dn = reinterpret_cast<MmqDesc*>(B + o_ddn);
 
-    // int8 kernels: 64-row tiles when the experts would average at most 48 rows
-    const bool m64 = !f16 && P <= 48u * std::min(expert_count, P);
-    const uint32_t bm = m64 ? 64u : kMmqBM;
+    // 32-row (f16) or 64-row (int8) tiles when the experts would average at
+    // most 48 rows
+    const bool small = P <= 48u * std::min(expert_count, P);
+    const uint32_t bm = small ? (f16 ? 32u : 64u) : kMmqBM;
     MoePlanArgs pa;
     std::memset(&pa, 0, sizeof pa);
     pa.idx = d_idx;
@@ -2339,7 +2362,7 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         d->k = k;
         d->type = w0->ggml_type;
         d->ldy = n;
-        const uint32_t bn = tile_bn(d->type, f16);
+        const uint32_t bn = tile_bn(f16);
         d->tiles_n = (n + bn - 1u) / bn;
         d->splits = 1;
         d->sb_per_split = k / 256u;
@@ -2395,12 +2418,12 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
         const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
         if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
-                                2u * tiles_bound * pa.tg.tiles_n, false, stream, f16, m64))
+                                2u * tiles_bound * pa.tg.tiles_n, false, stream, f16, bm))
             return rc;
         if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
         if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
         if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
-                                stream, f16, m64))
+                                stream, f16, bm))
             return rc;
     }
     struct {
