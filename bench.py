@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_K GEMV GB/s & M=512 prefill TOPS (% of MI355X peak), Qwen3-0.6B shapes"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X published
+F16_PEAK_TOPS = 2500.0   # dense f16 MFMA, MI355X published (the prefill kernels' arithmetic)
 
 
 def log(*a):
@@ -332,8 +333,8 @@ def moe_leg(rq, synth, torch, np, dev, timed):
         logits = synth.normals(synth.seed_for(5, 0, 4), tokens * E).reshape(tokens, E)
         y = torch.empty(tokens * H, device=dev)
         used = len({e for t in range(tokens) for e, _ in rq.route_top_k(logits[t], K)})
-        steps = 20 if tokens > 1 else 100
-        ms = timed(lambda i: rq.moe_ffn_grouped(x, tokens, H, logits, E, K, True, 1.0, gate, up, down, y), steps, 3)
+        steps = 30 if tokens > 1 else 100
+        ms = timed(lambda i: rq.moe_ffn_grouped(x, tokens, H, logits, E, K, True, 1.0, gate, up, down, y), steps, 10)
         wbytes = used * per_expert
         ops = tokens * K * 2 * 3 * F * H
         gbs = wbytes / (ms * 1e-3) / 1e9
@@ -345,7 +346,7 @@ def moe_leg(rq, synth, torch, np, dev, timed):
         # the same step with routing on the device (logits in device memory)
         lg = torch.from_numpy(logits).to(dev)
         ms_d = timed(lambda i: rq.moe_ffn_grouped_device(x, tokens, H, lg, E, K, True, 1.0, gate, up, down, y),
-                     steps, 3)
+                     steps, 10)
         gbs_d = wbytes / (ms_d * 1e-3) / 1e9
         out[tag + "_device_routing"] = {"ms_per_step": round(ms_d, 4), "gbs": round(gbs_d, 1),
                                         "frac_hbm_peak": round(gbs_d / HBM_PEAK_GBS, 4)}
@@ -387,11 +388,43 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
         ms = timed(lambda i: plan.run(), steps, 2)
         tops = ops / (ms * 1e-3) / 1e12
         out[tag] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                    "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1), "dtype": "f16-exact int8 dots (Q4_K, Q6_K)" if os.environ.get("REFLEX_MMQ_F16", "1") != "0" else "int8",
+                    "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1),
+                    "dtype": "f16 MFMA, f32 accumulate" if rq.get_options()["mmq_f16"] else "int8 MFMA (Q8_1)",
+                    "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4),
                     "gemms_per_step": len(items)}
         print(f"prefill {tag}: {ms:.3f} ms/step  {tops:.0f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)",
               file=sys.stderr, flush=True)
         del plan, items, keep
+    # config 4's tied LM head at M=512 (one GEMM, 151936 x 1024 Q6_K) and the
+    # few-row GEMMs of short prompts (the reference's fused-path measurements:
+    # 12 and 29 rows) over one Qwen3-0.6B layer set, weights read once per step
+    name, ty, n, k = synth.LM_HEAD
+    w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(4, 0, 50)), k, n, device=dev)
+    x = torch.randn(512 * k, device=dev, generator=gen)
+    y = torch.empty(512 * n, device=dev)
+    plan = rq.GemmPlan([(x, w, y)], 512)
+    ms = timed(lambda i: plan.run(), 10, 2)
+    ops = 2 * 512 * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+    out["qwen3_8b_lm_head_m512"] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                    "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4), "ms_per_step": round(ms, 3)}
+    print(f"prefill lm_head M=512: {ms:.3f} ms  {tops:.0f} TOPS", file=sys.stderr, flush=True)
+    del plan, w, x, y
+    layer = synth.QWEN3_06B_LAYER
+    ws = [rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(3, 0, pi)), k, n, device=dev)
+          for pi, (_, ty, n, k) in enumerate(layer)]
+    wbytes = sum(synth.weight_bytes(ty, n, k) for _, ty, n, k in layer)
+    for rows in (12, 29):
+        items = [(torch.randn(rows * k, device=dev, generator=gen), w, torch.empty(rows * n, device=dev))
+                 for w, (_, ty, n, k) in zip(ws, layer)]
+        plan = rq.GemmPlan(items, rows)
+        ms = timed(lambda i: plan.run(), 50, 10)
+        out[f"qwen3_06b_layer_rows{rows}"] = {"us_per_step": round(ms * 1e3, 1),
+                                             "weight_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1)}
+        print(f"prefill 0.6B layer, {rows} rows: {ms * 1e3:.1f} us  ({wbytes / (ms * 1e-3) / 1e9:.0f} GB/s of weights)",
+              file=sys.stderr, flush=True)
+        del plan, items
+    del ws
     # fused activation producers at the 8B shapes (rmsnorm before q/k/v and
     # gate/up, SiLU·up before down): one launch writes the quantized layouts
     rows, hid, ffn = 512, 4096, 14336

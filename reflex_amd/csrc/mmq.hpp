@@ -548,3 +548,36 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce(const float
         y[i] = s;
     }
 }
+
+// Several split-K reduces in one launch: item i takes workgroups
+// [wg_begin, next item's wg_begin) and sums its splits as rfxq_splitk_reduce.
+struct ReduceItem {
+    const float* ws;
+    float* y;
+    uint32_t n, splits, wg_begin, wgs;
+};
+#define REDUCE_INLINE 32
+struct ReduceArgs {
+    uint32_t count, pad;
+    ReduceItem items[REDUCE_INLINE];
+};
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_splitk_reduce_multi(ReduceArgs a) {
+    uint32_t it = 0;
+    for (uint32_t j = 1; j < a.count; j++)
+        if (a.items[j].wg_begin <= blockIdx.x) it = j;
+    const ReduceItem r = a.items[it];
+    const uint64_t n = r.n;
+    for (uint64_t i = (uint64_t)(blockIdx.x - r.wg_begin) * 256u + threadIdx.x; i < n; i += (uint64_t)r.wgs * 256u) {
+        float s = r.ws[i];
+        for (uint32_t z0 = 1; z0 < r.splits; z0 += 8u) {
+            float v[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; u++) v[u] = z0 + u < r.splits ? r.ws[(uint64_t)(z0 + u) * n + i] : 0.0f;
+#pragma unroll
+            for (uint32_t u = 0; u < 8u; u++)
+                if (z0 + u < r.splits) s += v[u];
+        }
+        r.y[i] = s;
+    }
+}

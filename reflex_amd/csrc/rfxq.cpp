@@ -113,6 +113,18 @@ struct MmqArgs {
     MmqDesc inl[kMmqInline];
 };
 static_assert(sizeof(MmqDesc) == 104, "MmqDesc layout");
+// rfxq_splitk_reduce_multi's arguments (mmq.hpp)
+struct ReduceItem {
+    const float* ws;
+    float* y;
+    uint32_t n, splits, wg_begin, wgs;
+};
+constexpr uint32_t REDUCE_INLINE = 32;
+struct ReduceArgs {
+    uint32_t count, pad;
+    ReduceItem items[REDUCE_INLINE];
+};
+static_assert(sizeof(ReduceItem) == 32 && sizeof(ReduceArgs) == 8 + 32 * 32, "ReduceArgs layout");
 
 constexpr uint32_t kMmqBM = 128, kMmqBN = 128;
 
@@ -129,7 +141,7 @@ struct Ctx {
     int device = -1;
     int cus = 256;
     hipModule_t mod = nullptr;
-    hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr;
+    hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr, reduce_multi = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
     hipFunction_t mmqh[2][2] = {}, act_f16 = nullptr, act_f16_multi = nullptr;  // [type][128-row, 32-row tiles]
     hipFunction_t deq[3][2] = {};
@@ -185,6 +197,7 @@ int load_ctx(int device, Ctx** out) {
         {&c->quant_multi, "rfxq_quantize_q8_1_multi"},
         {&c->quant, "rfxq_quantize_q8_1"},
         {&c->reduce, "rfxq_splitk_reduce"},
+        {&c->reduce_multi, "rfxq_splitk_reduce_multi"},
         {&c->mmq[0], "rfxq_mmq_q4k"},
         {&c->mmq[1], "rfxq_mmq_q6k"},
         {&c->mmq[2], "rfxq_mmq_q8_0"},
@@ -1143,10 +1156,26 @@ int launch_group_kernel(Ctx* c, const GemmGroup& g, uint32_t t, const MmqDesc* t
 
 // the split-K reduces of kernel t
 int run_group_reduces(Ctx* c, const GemmGroup& g, uint32_t t, hipStream_t stream) {
-    for (const auto& r : g.reduces)
-        if (r.t == t)
-            if (int rc = launch_reduce(c, r.part, r.y, r.n, r.splits, stream)) return rc;
-    return RFXQ_OK;
+    // all of kernel t's reduces in launches of up to REDUCE_INLINE items
+    ReduceArgs a;
+    std::memset(&a, 0, sizeof a);
+    uint32_t wg = 0;
+    auto flush = [&]() -> int {
+        if (a.count == 0) return RFXQ_OK;
+        const int rc = launch(c->reduce_multi, wg, 0, stream, &a, sizeof a, "rfxq_splitk_reduce_multi launch");
+        std::memset(&a, 0, sizeof a);
+        wg = 0;
+        return rc;
+    };
+    for (const auto& r : g.reduces) {
+        if (r.t != t) continue;
+        const uint32_t wgs = (uint32_t)std::min<uint64_t>((r.n + 255u) / 256u, 2048u);
+        a.items[a.count++] = ReduceItem{r.part, r.y, (uint32_t)r.n, r.splits, wg, wgs};
+        wg += wgs;
+        if (a.count == REDUCE_INLINE)
+            if (int rc = flush()) return rc;
+    }
+    return flush();
 }
 
 // workspace offsets -> addresses

@@ -185,6 +185,16 @@ def test_gemm_prefill_8b_sampled_rows(rq, orc, name, ty, n, k):
     _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x, rows)
 
 
+@pytest.mark.parametrize("rows", [5, 12, 29])
+@pytest.mark.parametrize("name,ty,n,k", [c for c in synth.QWEN3_8B_LAYER if c[0] in ("q_proj", "down_proj")],
+                         ids=["q_proj", "down_proj"])
+def test_gemm_few_rows_8b(rq, orc, rows, name, ty, n, k):
+    """The few-row path (32-row tiles, every row checked) at the 8B shapes."""
+    seed = synth.seed_for(4, 3, rows)
+    x = synth.activations(rows * k, seed + 1000).reshape(rows, k)
+    _check_gemm(rq, orc, ty, rows, n, k, synth.weights(ty, n, k, seed), x)
+
+
 def test_gemm_prefill_lm_head_m512(rq, orc):
     """BASELINE config 4's tied LM head, 151936 x 1024 Q6_K, at M = 512: 12 sampled
     rows against the reference over all 151936 columns."""
@@ -196,7 +206,7 @@ def test_gemm_prefill_lm_head_m512(rq, orc):
 
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
-@pytest.mark.parametrize("m", [2, 7, 33, 129, 513])
+@pytest.mark.parametrize("m", [2, 5, 7, 12, 29, 32, 33, 129, 513])
 def test_gemm_row_counts(rq, orc, ty, m):
     n, k = 200, 1024
     w_np = orc.synthetic(ty, k, n, 60 + m)
