@@ -384,8 +384,9 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
                 items.append((xs[g], w, y))
         plan = rq.GemmPlan(items, 512)
         ops = sum(2 * 512 * n * k for _, _, n, k in layer) * nl
-        steps = 10 if nl > 1 else 20
-        ms = timed(lambda i: plan.run(), steps, 2)
+        # warm-up long enough for the clocks to settle (~30 ms of load)
+        steps, warm = (20, 40) if nl > 1 else (40, 80)
+        ms = timed(lambda i: plan.run(), steps, warm)
         tops = ops / (ms * 1e-3) / 1e12
         out[tag] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                     "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1),
@@ -403,7 +404,7 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
     x = torch.randn(512 * k, device=dev, generator=gen)
     y = torch.empty(512 * n, device=dev)
     plan = rq.GemmPlan([(x, w, y)], 512)
-    ms = timed(lambda i: plan.run(), 10, 2)
+    ms = timed(lambda i: plan.run(), 20, 60)
     ops = 2 * 512 * n * k
     tops = ops / (ms * 1e-3) / 1e12
     out["qwen3_8b_lm_head_m512"] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),

@@ -229,7 +229,19 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16(const float* __re
                                                               const int32_t* __restrict__ src_rows, uint32_t rows,
                                                               uint32_t k, uint16_t* __restrict__ xh,
                                                               uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
-    act_f16_rows(QuantSrcPlain{x, ldx, src_rows}, rows, k, blockIdx.x, gridDim.x, xh, xsx, xrs, nullptr);
+    const QuantSrcPlain src{x, ldx, src_rows};
+    for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4u)
+        act_f16_row(src, r, k, xh, xsx, xrs, nullptr);
+}
+
+// the same with a row per workgroup (few or long rows; a kernel of its own:
+// its registers would otherwise limit the row-per-wave kernel's occupancy)
+extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_wg(const float* __restrict__ x, uint32_t ldx,
+                                                                 const int32_t* __restrict__ src_rows, uint32_t rows,
+                                                                 uint32_t k, uint16_t* __restrict__ xh,
+                                                                 uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
+    const QuantSrcPlain src{x, ldx, src_rows};
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) act_f16_row_wg(src, r, k, xh, xsx, xrs, nullptr);
 }
 
 // Several activations in one launch (grouped GEMMs): workgroups
@@ -242,17 +254,29 @@ struct ActF16Desc {
     uint32_t rows, k, wg_begin, wgs;
 };
 
-extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_multi(const ActF16Desc* __restrict__ table,
-                                                                    uint32_t ndesc) {
+RFXQ_DEV const ActF16Desc& act_f16_pick(const ActF16Desc* __restrict__ table, uint32_t ndesc) {
     uint32_t lo = 0, hi = ndesc - 1u;
     while (lo < hi) {
         const uint32_t mid = (lo + hi + 1u) >> 1;
         if (table[mid].wg_begin <= blockIdx.x) lo = mid;
         else hi = mid - 1u;
     }
-    const ActF16Desc d = table[lo];
-    act_f16_rows(QuantSrcPlain{d.x, d.k, nullptr}, d.rows, d.k, blockIdx.x - d.wg_begin, d.wgs, d.xh, d.xsx, d.xrs,
-                 nullptr);
+    return table[lo];
+}
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_multi(const ActF16Desc* __restrict__ table,
+                                                                    uint32_t ndesc) {
+    const ActF16Desc d = act_f16_pick(table, ndesc);
+    const QuantSrcPlain src{d.x, d.k, nullptr};
+    for (uint32_t r = (blockIdx.x - d.wg_begin) * 4u + (threadIdx.x >> 6); r < d.rows; r += d.wgs * 4u)
+        act_f16_row(src, r, d.k, d.xh, d.xsx, d.xrs, nullptr);
+}
+
+extern "C" __global__ __launch_bounds__(256) void rfxq_act_f16_multi_wg(const ActF16Desc* __restrict__ table,
+                                                                       uint32_t ndesc) {
+    const ActF16Desc d = act_f16_pick(table, ndesc);
+    const QuantSrcPlain src{d.x, d.k, nullptr};
+    for (uint32_t r = blockIdx.x - d.wg_begin; r < d.rows; r += d.wgs) act_f16_row_wg(src, r, d.k, d.xh, d.xsx, d.xrs, nullptr);
 }
 
 extern "C" __global__ __launch_bounds__(256) void rfxq_quantize_q8_1(const float* __restrict__ x, uint32_t ldx,

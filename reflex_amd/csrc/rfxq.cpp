@@ -143,7 +143,8 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr, reduce_multi = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmqh[2][2] = {}, act_f16 = nullptr, act_f16_multi = nullptr;  // [type][128-row, 32-row tiles]
+    hipFunction_t mmqh[2][2] = {};  // [type][128-row, 32-row tiles]
+    hipFunction_t act_f16 = nullptr, act_f16_multi = nullptr, act_f16_wg = nullptr, act_f16_multi_wg = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
@@ -213,6 +214,8 @@ int load_ctx(int device, Ctx** out) {
         {&c->mmqh[1][1], "rfxq_mmqh_q6k_m32"},
         {&c->act_f16, "rfxq_act_f16"},
         {&c->act_f16_multi, "rfxq_act_f16_multi"},
+        {&c->act_f16_wg, "rfxq_act_f16_wg"},
+        {&c->act_f16_multi_wg, "rfxq_act_f16_multi_wg"},
         {&c->deq[0][0], "rfxq_dequant_q4k_f32"},
         {&c->deq[0][1], "rfxq_dequant_q4k_f16"},
         {&c->deq[1][0], "rfxq_dequant_q6k_f32"},
@@ -871,11 +874,13 @@ int launch_quant(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, 
 }
 
 // f16 layout of x (rfxq_act_f16): one wave per row
-// workgroups of an f16 activation launch: a row per wave (4 per workgroup)
-// for at least 128 rows of at most 4096 values, else a row per workgroup
-// (the kernels' act_wave_rows rule)
-uint32_t act_f16_grid(uint32_t rows, uint32_t k) {
-    return k <= 4096u && rows >= 128u ? std::min<uint32_t>((rows + 3u) / 4u, 4096u) : std::min<uint32_t>(rows, 16384u);
+// f16 activation kernels: a row per wave (rfxq_act_f16[_multi], 4 rows per
+// workgroup) for at least 128 rows of at most 4096 values, else a row per
+// workgroup (rfxq_act_f16[_multi]_wg: few rows, or rows too long for one
+// wave's registers)
+bool act_f16_wave(uint32_t rows, uint32_t k) { return k <= 4096u && rows >= 128u; }
+uint32_t act_f16_grid(uint32_t rows, bool wave) {
+    return wave ? std::min<uint32_t>((rows + 3u) / 4u, 4096u) : std::min<uint32_t>(rows, 16384u);
 }
 
 int launch_act_f16(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows, uint32_t rows, uint32_t k,
@@ -890,7 +895,9 @@ int launch_act_f16(Ctx* c, const float* x, uint32_t ldx, const int32_t* src_rows
         float* xrs;
     } a = {x, ldx, 0, src_rows, rows, k, reinterpret_cast<uint16_t*>(base + L.xh),
            reinterpret_cast<uint16_t*>(base + L.xsx), reinterpret_cast<float*>(base + L.xrs)};
-    return launch(c->act_f16, act_f16_grid(rows, k), 0, stream, &a, sizeof a, "rfxq_act_f16 launch");
+    const bool wave = act_f16_wave(rows, k);
+    return launch(wave ? c->act_f16 : c->act_f16_wg, act_f16_grid(rows, wave), 0, stream, &a, sizeof a,
+                  "rfxq_act_f16 launch");
 }
 
 // the activation layouts of L at `base` from x
@@ -1283,6 +1290,7 @@ struct rfxq_gemm_plan {
     uint32_t nq = 0, qgrid = 0;
     ActF16Desc* htable = nullptr;  // f16 layouts: one rfxq_act_f16_multi launch
     uint32_t nh = 0, hgrid = 0;
+    bool hwave = true;  // htable runs on rfxq_act_f16_multi (else _multi_wg)
     rfxq_gemv_plan* q8 = nullptr;  // GEMMs on the GEMV path, one item per row
 };
 
@@ -1836,6 +1844,9 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
         // one launch per layout kind for all activations
         std::vector<QuantDesc> q;
         std::vector<ActF16Desc> hq;
+        plan->hwave = true;  // one kernel for all f16 layouts: row per wave only if every activation allows it
+        for (const auto& a : plan->g.acts)
+            if (a.need_h && !act_f16_wave(rows, a.k)) plan->hwave = false;
         for (const auto& a : plan->g.acts) {
             uint8_t* ab = base + a.off;
             if (a.need_i8) {
@@ -1845,7 +1856,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
                 plan->qgrid += wgs;
             }
             if (a.need_h) {
-                const uint32_t wgs = act_f16_grid(rows, a.k);
+                const uint32_t wgs = act_f16_grid(rows, plan->hwave);
                 hq.push_back(ActF16Desc{a.x, reinterpret_cast<uint16_t*>(ab + a.L.xh),
                                         reinterpret_cast<uint16_t*>(ab + a.L.xsx), reinterpret_cast<float*>(ab + a.L.xrs),
                                         rows, a.k, plan->hgrid, wgs});
@@ -1894,7 +1905,8 @@ int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {
             const ActF16Desc* table;
             uint32_t ndesc, pad;
         } ha = {plan->htable, plan->nh, 0};
-        if (int rc = launch(c->act_f16_multi, plan->hgrid, 0, stream, &ha, sizeof ha, "rfxq_act_f16_multi launch"))
+        if (int rc = launch(plan->hwave ? c->act_f16_multi : c->act_f16_multi_wg, plan->hgrid, 0, stream, &ha, sizeof ha,
+                            "rfxq_act_f16_multi launch"))
             return rc;
     }
     for (uint32_t t = 0; t < kGroupKernels; t++) {
