@@ -37,6 +37,7 @@
 #define GEMV_PROBE_BEGIN()
 #define GEMV_PROBE(i)
 #define GEMV_PROBE_END()
+#define GEMV_PROBE_WAIT()
 #endif
 
 struct GemvDesc {
@@ -584,6 +585,7 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
                 // most those of the other kRing - 1 slots are outstanding
                 // (stores issued since only make this wait longer)
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * NJ) : "memory");
+                GEMV_PROBE_WAIT();
                 const typename T::Raw rr = T::fetch(ring[t], uo + sh, unit);
                 issue(t);  // the slot's reads are done (fetch waits for them): refill it during the math
                 float acc = T::dot(rr, unit, xv, magic);

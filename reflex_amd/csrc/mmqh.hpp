@@ -23,24 +23,25 @@
 // Sx lo). Everything accumulates in one f32 accumulator in the matrix core:
 // no per-block or per-super-block epilogue on the VALU.
 //
-// Q4_K tile: 128 activation rows x 256 weight columns per 256-thread
-// workgroup (two per CU); wave w owns weight columns [64w, +64) against all
-// 128 rows: eight 32x32 MFMA tiles, A = weights, B = activations (lane l holds
-// activation row l%32 of its tile and 16 weight columns), so each activation
-// operand read from LDS feeds two MFMAs and each converted weight operand
-// four. Data moves in 64-k stages through a 2-slot LDS ring: activations
-// [128][64] f16 (16 KB, 16-byte chunks XOR-swizzled by row/2) and weight
-// quants [256][32 B] (8 KB, halves swizzled by column/8), plus the super-block
-// headers [256][16 B] and Sx records [128][32 B] with the first stage of a
-// super-block (56 KB). Every lane loads its share of stage s + 1 into
-// registers with plain buffer loads while stage s computes, in two halves
-// written to the other slot at mid-stage and at its end; one barrier per
-// stage. (The LDS-DMA path, buffer_load ... lds, measured slower here: it
-// throttles the MFMA stream of the same CU.) Activation rows are gathered
-// through MmqDesc::rows when set (MoE expert groups).
-//
-// Q6_K tile: 128 x 128 per 256-thread workgroup with a 3-slot LDS-DMA ring
-// (see the Q6_K section below).
+// Tiles: (32 MT) activation rows x 256 weight columns per 256-thread
+// workgroup, MT = 4 (128-row tiles, two workgroups per CU) or MT = 1 (32-row
+// tiles: few-row GEMMs and small expert groups). Wave w owns weight columns
+// [64w, +64) against all rows: 2 MT 32x32 MFMA tiles, A = weights,
+// B = activations (lane l holds activation row l%32 of its tile and 16
+// weight columns), so each activation operand read from LDS feeds two MFMAs
+// and each converted weight operand MT. Data moves in 64-k stages:
+//   - weights go straight to registers: no other wave reads a wave's columns,
+//     so each lane loads its own 16-byte pieces of the stage one stage ahead
+//     (plain buffer loads) and converts them there;
+//   - activations [BM][64] f16 (16-byte chunks XOR-swizzled by row/2) and,
+//     with the first stage of a super-block, the Sx records [BM][32 B] pass
+//     through a 2-slot LDS ring: every lane loads its share of stage s + 1
+//     into registers while stage s computes and writes it to the other slot;
+//     one barrier per stage.
+// (The LDS-DMA path, buffer_load ... lds, measured slower here: it throttles
+// the MFMA stream of the same CU.) Activation rows are gathered through
+// MmqDesc::rows when set (MoE expert groups). The Q6_K tile (below) has the
+// same layout and pipeline with its own weight operands.
 #pragma once
 #include "common.hpp"
 #include "mmq.hpp"

@@ -221,6 +221,44 @@ def test_gemv_maximum_in_features(rq, orc, ty):
         rq.gemv(torch.zeros(k2, device=DEV), w)
 
 
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+@pytest.mark.parametrize("n,k", [(5, 4352), (33, 8448), (130, 12288), (3, 16128)])
+def test_gemv_long_rows(rq, orc, ty, n, k):
+    """Rows longer than 4096 run as several passes per lane: K = 4352 has 68
+    units per row (4 lanes per row, 17 passes), K = 8448 Q8_0 264; few rows
+    leave waves without rows."""
+    w = orc.synthetic(ty, k, n, 300 + n)
+    x = orc.activations(k, 301 + n)
+    _check_gemv(rq, orc, ty, n, k, w, x, tol=5e-4)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+def test_gemv_long_rows_beyond_f16_range(rq, orc, ty):
+    """Several-pass rows with |x| beyond 2^15: the staged x is scaled."""
+    n, k = 300, 8192
+    x = synth.activations(k, 79) * np.float32(2e5)
+    _check_gemv(rq, orc, ty, n, k, orc.synthetic(ty, k, n, 78), x)
+
+
+def test_gemv_mixed_row_lengths_match_single_calls(rq, orc):
+    """A launch mixing K = 3072..14336 (one-pass and several-pass rows, x
+    staged at the launch's widest size) equals single calls bit for bit."""
+    shapes = [(Q4K, 4096, 4096), (Q6K, 1024, 4096), (Q4K, 1024, 3072), (Q6K, 4096, 14336), (Q8_0, 512, 8192)]
+    items, singles = [], []
+    for i, (ty, n, k) in enumerate(shapes):
+        w = _weight(rq, ty, orc.synthetic(ty, k, n, 400 + i), n, k)
+        x = _dev(synth.activations(k, 410 + i))
+        singles.append(rq.gemv(x, w).cpu().numpy())
+        items.append((x, w, torch.full((n,), float("nan"), device=DEV)))
+    plan = rq.GemvPlan(items)
+    plan.run()
+    for (_, _, y), ref in zip(items, singles):
+        assert np.array_equal(y.cpu().numpy(), ref)
+    rq.gemv_batch(items[:4])
+    for (_, _, y), ref in zip(items[:4], singles[:4]):
+        assert np.array_equal(y.cpu().numpy(), ref)
+
+
 def test_gemv_plan_several_waves_of_workgroups(rq):
     """A plan beyond 512 KB per resident workgroup (9 x 33 MB at K = 14336,
     two workgroups per CU) runs as whole waves of workgroups; every output

@@ -397,3 +397,122 @@ def test_rmsnorm_closed_form(orc):
         got = orc.rmsnorm(x, w, 2, k, eps)
         inv = np.float32(1.0) / np.sqrt(np.float32(c * c) + np.float32(eps))
         assert np.array_equal(got, np.stack([(x[0] * inv) * w] * 2))
+
+
+# ------------------------------------------------------------ SiLU * up
+
+def test_silu_and_mul_against_f64_and_limits(orc):
+    """silu_and_mul.cu:7-23, g / (1 + e^-g) * u in f32 (three roundings plus
+    expf's): within 3 ulps of the f64 value (below 1e-35 in magnitude, where
+    expf(-g) overflows to inf, within 1e-35); exact zeros at g = 0 and u = 0;
+    g * u at large g (e^-g below half an ulp of 1); a vanishing negative tail
+    at very negative g; odd symmetry silu(-g) = silu(g) - g checked to
+    rounding. A sign error in the exponent, a dropped factor or a swapped
+    operand fails one of these."""
+    rng = np.random.default_rng(11)
+    g = np.concatenate([rng.standard_normal(4000) * 4, rng.uniform(-90, 90, 1000)]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    out = orc.silu_and_mul(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(out - want) <= 3 * ulp + 1e-35)
+    z = orc.silu_and_mul(np.zeros(3, np.float32), np.array([1, -2, 3], np.float32))
+    assert np.all(z == 0)
+    assert np.all(orc.silu_and_mul(g, np.zeros_like(u)) == 0)
+    big = np.array([20.0, 40.0, 88.0], np.float32)
+    assert np.array_equal(orc.silu_and_mul(big, np.full(3, 3.0, np.float32)), big * np.float32(3.0))
+    neg = orc.silu_and_mul(np.array([-90.0, -200.0], np.float32), np.ones(2, np.float32))
+    assert np.all(np.abs(neg) < 1e-35) and np.all(neg <= 0)
+    a = orc.silu_and_mul(g, np.ones_like(g)).astype(np.float64)
+    b = orc.silu_and_mul(-g, np.ones_like(g)).astype(np.float64)
+    assert np.all(np.abs((a - b) - g64) <= 8 * np.spacing(np.abs(g)).astype(np.float64) + 1e-30)
+
+
+# ------------------------------------------------------------ f16 activation format
+
+def test_act_f16_invariants(orc):
+    """The f16 activation layout (no reference counterpart beyond the f16
+    cast of convert.cu:91): the row scale is a power of two placing the row
+    maximum in [256, 512); decoding the stored f16 values times the scale
+    gives x back to f16 rounding; the stored order within each group of four
+    is (x0, x2, x1, x3) (checked on exactly representable values); block sums
+    hi + lo equal the exact sum of the block's 32 f16 values where that sum is
+    exact in f32, and agree to f32 rounding elsewhere; an all-zero row has
+    scale 1 and zeros."""
+    rng = np.random.default_rng(5)
+    rows, k = 6, 512
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[1] *= np.float32(3e5)
+    x[2] *= np.float32(1e-6)
+    x[3] = 0
+    x[4] = (np.arange(k) - 250).astype(np.float32)   # max 261: scale 1, exact
+    xh, xsx, xrs = orc.act_f16(x)
+    for r in (0, 1, 2, 4):
+        s = float(xrs[r])
+        assert s == 2.0 ** round(np.log2(s))
+        mx = np.max(np.abs(x[r])) / s
+        assert 256 <= mx < 512
+    assert xrs[3] == 1 and np.all(xh[3] == 0)
+    h = xh.view(np.float16).astype(np.float64).reshape(rows, k // 4, 4)[:, :, [0, 2, 1, 3]].reshape(rows, k)
+    dec = h * xrs[:, None].astype(np.float64)
+    assert np.all(np.abs(dec - x) <= np.abs(x) * 2.0 ** -11 + 1e-30)
+    # stored order on exact integers: stored[4i + 1] = x[4i + 2], stored[4i + 2] = x[4i + 1]
+    st = xh[4].view(np.float16).astype(np.float64).reshape(k // 4, 4)
+    xi = x[4].astype(np.float64).reshape(k // 4, 4)
+    assert np.array_equal(st, xi[:, [0, 2, 1, 3]])
+    sx = xsx.view(np.float16).astype(np.float64)
+    tot = (sx[..., :8] + sx[..., 8:]).reshape(rows, k // 32)
+    exact = h.reshape(rows, k // 32, 32).sum(axis=2)
+    assert np.array_equal(tot[4], exact[4])
+    assert np.all(np.abs(tot - exact) <= np.abs(exact) * 2.0 ** -20 + 1e-3 * 2.0 ** -10)
+
+
+# ------------------------------------------------------------ f16-operand GEMM model
+
+def _q6k_block(d, sc, q):
+    """One Q6_K block: ql[128], qh[64], scales[16] (int8), d f16 from 256 six-bit codes
+    in element order (dequant.rs:414-445 layout)."""
+    blk = bytearray(210)
+    for h in range(2):
+        for l in range(32):
+            q0, q1, q2, q3 = (q[128 * h + l + 32 * j] for j in range(4))
+            blk[64 * h + l] = (q0 & 15) | ((q2 & 15) << 4)
+            blk[64 * h + 32 + l] = (q1 & 15) | ((q3 & 15) << 4)
+            blk[128 + 32 * h + l] = (q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6)
+    blk[192:208] = np.asarray(sc, np.int8).tobytes()
+    blk[208:210] = bytes(f16b(d))
+    return bytes(blk)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
+def test_mmqh_model_reference_exact_case(orc, ty):
+    """Where every f16 rounding of the f16-operand model is exact (integer
+    activations with row maxima in [256, 512): scale 1; power-of-two d and
+    dmin with small scales: exact weight operands and constant parts), the
+    model equals dequant + f64 matmul bit for bit; a dropped constant part,
+    a wrong nibble or qh bit order, or a missing x16 on the high-nibble codes
+    breaks the equality."""
+    rng = np.random.default_rng(8)
+    n, k, rows = 5, 512, 3
+    nsb = k // 256
+    blocks = []
+    for _ in range(n * nsb):
+        if ty == Q4K:
+            sc = rng.integers(0, 64, 8).tolist()
+            m = rng.integers(0, 64, 8).tolist()
+            blocks.append(_q4k_block(2.0 ** -4, 2.0 ** -5, sc, m, rng.integers(0, 16, 256).tolist(),
+                                     rng.integers(0, 16, 256).tolist()))
+        else:
+            blocks.append(_q6k_block(2.0 ** -6, rng.integers(-15, 16, 16), rng.integers(0, 64, 256).tolist()))
+    w = np.frombuffer(b"".join(blocks), np.uint8).copy()
+    x = rng.integers(-300, 301, (rows, k)).astype(np.float32)
+    x[:, 7] = 300
+    got = orc.mmqh_model_reference(ty, w, n, k, x)
+    want = orc.reference_gemm(ty, w, n, k, x)
+    assert np.array_equal(got, want)
+    # and on random data the model stays within f16 rounding of the reference
+    w2 = orc.synthetic(ty, k, 64, 9)
+    x2 = rng.standard_normal((4, k)).astype(np.float32)
+    e = orc.rel_err_row_l2(orc.mmqh_model_reference(ty, w2, 64, k, x2), orc.reference_gemm(ty, w2, 64, k, x2))
+    assert e < 1e-3
