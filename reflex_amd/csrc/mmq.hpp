@@ -491,6 +491,12 @@ RFXQ_DEV void mmq_tile(const MmqDesc& ds, uint32_t t_local, float* lds_da, float
 // below it (descriptors with no tiles share the next one's wg_begin and are
 // skipped). A workgroup past the last descriptor's tiles (launch grids that
 // are upper bounds, for tables built on the device) returns at once.
+// Workgroups the descriptors of a launch use (the last one's end)
+RFXQ_DEV uint32_t mmq_tile_count(const MmqArgs& a) {
+    const MmqDesc* l = (a.ndesc <= MMQ_INLINE ? a.inl : a.table) + (a.ndesc - 1u);
+    return __builtin_amdgcn_readfirstlane(l->wg_begin + l->tiles_m * l->tiles_n * l->splits);
+}
+
 RFXQ_DEV MmqDesc mmq_pick(const MmqArgs& a, uint32_t wg) {
     if (a.ndesc <= MMQ_INLINE) {
         MmqDesc d = a.inl[0];

@@ -462,17 +462,23 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
 }
 
+// The tiles of a launch are spread over the XCDs by their real count: a grid
+// sized by an upper bound (device-written MoE tables) would otherwise leave
+// the XCDs that own the tail of the tile range without work.
 #define RFXQ_MMQH_ENTRY(NAME, TILE, MT, WPE)                                                                \
     extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
         __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::Tile<MT>::kLds];                            \
         if (blockDim.x != mmqh::kThreads) return; /* the tile assumes exactly kThreads lanes */               \
-        const uint32_t b = mmqh::xcd_tile(blockIdx.x, gridDim.x);                                           \
+        const uint32_t tiles = min(gridDim.x, mmq_tile_count(args));                                        \
+        if (blockIdx.x >= tiles) return;                                                                     \
+        const uint32_t b = mmqh::xcd_tile(blockIdx.x, tiles);                                               \
         const MmqDesc d = mmq_pick(args, b);                                                                 \
         if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;                                     \
         TILE<MT>(d, b - d.wg_begin, lds);                                                                     \
     }
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k, mmqh_q4k_tile, 4, 2)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m32, mmqh_q4k_tile, 1, 4)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m64, mmqh_q4k_tile, 2, 3)
 
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
 // the Q4_K tile's layout and pipeline, with the Q6_K weight operands.
@@ -682,3 +688,4 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, mmqh_q6k_tile, 4, 2)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m32, mmqh_q6k_tile, 1, 3)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m64, mmqh_q6k_tile, 2, 2)

@@ -143,7 +143,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr, reduce_multi = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmqh[2][2] = {};  // [type][128-row, 32-row tiles]
+    hipFunction_t mmqh[2][3] = {};  // [type][128-row, 32-row, 64-row tiles]
     hipFunction_t act_f16 = nullptr, act_f16_multi = nullptr, act_f16_wg = nullptr, act_f16_multi_wg = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
@@ -212,6 +212,8 @@ int load_ctx(int device, Ctx** out) {
         {&c->mmqh[1][0], "rfxq_mmqh_q6k"},
         {&c->mmqh[0][1], "rfxq_mmqh_q4k_m32"},
         {&c->mmqh[1][1], "rfxq_mmqh_q6k_m32"},
+        {&c->mmqh[0][2], "rfxq_mmqh_q4k_m64"},
+        {&c->mmqh[1][2], "rfxq_mmqh_q6k_m64"},
         {&c->act_f16, "rfxq_act_f16"},
         {&c->act_f16_multi, "rfxq_act_f16_multi"},
         {&c->act_f16_wg, "rfxq_act_f16_wg"},
@@ -766,7 +768,8 @@ uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 //   weights, cheaper than the few-row tiles' launch pair below 5 rows);
 // - otherwise the f16-activation kernels (PATH_MMQ_F16: Q4_K, and Q6_K with an
 //   even super-block count per row): 32-row tiles up to 32 rows (the fused
-//   few-row form: each weight read once for all rows), 128-row tiles above,
+//   few-row form: each weight read once for all rows), 64-row tiles up to
+//   64, 128-row tiles above,
 //   or the int8 kernels (PATH_MMQ_INT8; 64-row tiles with
 //   REFLEX_QUANT_MMA_TILE=64);
 // - split-K: none once the tiles cover half the CUs (each CU holds two
@@ -777,6 +780,24 @@ uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 enum : uint32_t { PATH_GEMV_ROWS = RFXQ_PATH_GEMV_ROWS, PATH_MMQ_INT8 = RFXQ_PATH_MMQ_INT8, PATH_MMQ_F16 = RFXQ_PATH_MMQ_F16 };
 constexpr uint32_t kGemvRowsMax = 4;
 
+
+// Row tile of the f16 kernels for a GEMM (or an expert group averaging
+// `rows`): weights are read once per tile, so the smallest tile that holds
+// the rows (32 or 64 rows: weight-stream bound, more workgroups per CU), 128
+// above
+uint32_t f16_tile_m(uint32_t rows) { return rows <= 32u ? 32u : rows <= 64u ? 64u : kMmqBM; }
+
+// Row tile of a grouped MoE launch, `pairs` routed rows over `experts`
+// groups: f16 kernels 32-row tiles up to 12 rows per expert on average,
+// 64-row up to 64 (config 5 at 32 rows on average: 229 us per layer against
+// 255 us with 32-row and 266 us with 128-row tiles: fewer experts read twice),
+// 128 above; int8 kernels 64-row tiles up to 48.
+uint32_t moe_tile_m(uint32_t pairs, uint32_t experts, bool f16) {
+    if (!experts) return kMmqBM;
+    const uint32_t avg = (pairs + experts - 1u) / experts;
+    if (f16) return avg <= 12u ? 32u : avg <= 64u ? 64u : kMmqBM;
+    return avg <= 48u ? 64u : kMmqBM;
+}
 
 rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o) {
     rfxq_gemm_policy p;
@@ -791,7 +812,7 @@ rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows,
         return p;
     }
     p.path = f16 ? PATH_MMQ_F16 : PATH_MMQ_INT8;
-    p.tile_m = f16 ? (rows <= 32u ? 32u : kMmqBM) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
+    p.tile_m = f16 ? f16_tile_m(rows) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
     p.tile_n = tile_bn(f16);
     const uint32_t nsb = k / 256u;
     const uint32_t tiles = ((rows + p.tile_m - 1u) / p.tile_m) * ((n + p.tile_n - 1u) / p.tile_n);
@@ -923,7 +944,7 @@ int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const 
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && !dots && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : 0];
+    if (f16 && !dots && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : tile_m == 64u ? 2 : 0];
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch", kMmqThreads);
 }
 
@@ -1025,8 +1046,9 @@ int check_act(const void* act, uint32_t rows, uint32_t k, const char* what) {
 // and each MMQ kernel runs as one launch over all of its GEMMs. Each GEMM
 // takes the single-GEMM policy's path (gemm_policy); GEMMs on the GEMV path
 // run as one GEMV per row in one table-driven launch.
-// type_index + 3 * variant (0: int8, 1: int8 64-row, 2: f16, 3: f16 32-row)
-constexpr uint32_t kGroupKernels = 12;
+// type_index + 3 * variant (0: int8, 1: int8 64-row, 2: f16, 3: f16 32-row,
+// 4: f16 64-row)
+constexpr uint32_t kGroupKernels = 15;
 struct GemmGroup {
     struct Act {
         const float* x;
@@ -1057,9 +1079,9 @@ struct GemmGroup {
 bool group_f16(uint32_t g) { return g >= 6u; }
 uint32_t group_tile_m(uint32_t g) {
     const uint32_t v = g / 3u;
-    return v == 1u ? 64u : v == 3u ? 32u : kMmqBM;
+    return v == 1u || v == 4u ? 64u : v == 3u ? 32u : kMmqBM;
 }
-uint32_t group_variant(bool f16, uint32_t tile_m) { return f16 ? (tile_m == 32u ? 3u : 2u) : (tile_m == 64u ? 1u : 0u); }
+uint32_t group_variant(bool f16, uint32_t tile_m) { return f16 ? (tile_m == 32u ? 3u : tile_m == 64u ? 4u : 2u) : (tile_m == 64u ? 1u : 0u); }
 
 int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
@@ -2176,12 +2198,11 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     float* d_cw = reinterpret_cast<float*>(B + o_cw);
     MmqDesc* d_desc = reinterpret_cast<MmqDesc*>(B + o_desc);
 
-    // descriptor tables: [gate+up descs][down descs]; experts averaging at
-    // most 48 routed rows take 32-row (f16) or 64-row (int8) tiles
+    // descriptor tables: [gate+up descs][down descs]; the row tile by the
+    // used experts' average row count
     uint32_t used = 0;
     for (uint32_t e = 0; e < expert_count; e++) used += off[e + 1] > off[e];
-    const bool small = used && P <= 48u * used;
-    const uint32_t bm = small ? (f16 ? 32u : 64u) : kMmqBM;
+    const uint32_t bm = moe_tile_m(P, used, f16);
     std::vector<MmqDesc> descs;
     uint32_t wg_gu = 0;
     // act: the activation layouts (rows gathered through rws, or starting at row r0)
@@ -2381,10 +2402,8 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     MmqDesc* d_gu = reinterpret_cast<MmqDesc*>(B + o_dgu);
     MmqDesc* d_dn = reinterpret_cast<MmqDesc*>(B + o_ddn);
 
-    // 32-row (f16) or 64-row (int8) tiles when the experts would average at
-    // most 48 rows
-    const bool small = P <= 48u * std::min(expert_count, P);
-    const uint32_t bm = small ? (f16 ? 32u : 64u) : kMmqBM;
+    // the row tile by the average rows of the experts the pairs can reach
+    const uint32_t bm = moe_tile_m(P, std::min(expert_count, P), f16);
     MoePlanArgs pa;
     std::memset(&pa, 0, sizeof pa);
     pa.idx = d_idx;

@@ -185,11 +185,11 @@ def test_gemm_prefill_8b_sampled_rows(rq, orc, name, ty, n, k):
     _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x, rows)
 
 
-@pytest.mark.parametrize("rows", [5, 12, 29])
+@pytest.mark.parametrize("rows", [5, 12, 29, 48])
 @pytest.mark.parametrize("name,ty,n,k", [c for c in synth.QWEN3_8B_LAYER if c[0] in ("q_proj", "down_proj")],
                          ids=["q_proj", "down_proj"])
 def test_gemm_few_rows_8b(rq, orc, rows, name, ty, n, k):
-    """The few-row path (32-row tiles, every row checked) at the 8B shapes."""
+    """The few-row paths (32- and 64-row tiles, every row checked) at the 8B shapes."""
     seed = synth.seed_for(4, 3, rows)
     x = synth.activations(rows * k, seed + 1000).reshape(rows, k)
     _check_gemm(rq, orc, ty, rows, n, k, synth.weights(ty, n, k, seed), x)
@@ -206,8 +206,10 @@ def test_gemm_prefill_lm_head_m512(rq, orc):
 
 
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
-@pytest.mark.parametrize("m", [2, 5, 7, 12, 29, 32, 33, 129, 513])
+@pytest.mark.parametrize("m", [2, 5, 7, 12, 29, 32, 33, 48, 64, 65, 129, 513])
 def test_gemm_row_counts(rq, orc, ty, m):
+    """Every tile height: GEMV rows (2), 32-row (5..32), 64-row (33..64) and
+    128-row tiles (65 up), ragged counts of each."""
     n, k = 200, 1024
     w_np = orc.synthetic(ty, k, n, 60 + m)
     x = synth.activations(m * k, 61 + m).reshape(m, k)

@@ -101,12 +101,12 @@ def test_policy_paths(rq):
     G, I8, F16 = rq.PATH_GEMV_ROWS, rq.PATH_MMQ_INT8, rq.PATH_MMQ_F16
     pol = rq.gemm_policy
     # one row, and up to 4 rows (within fused_max_rows): GEMVs; 5..32 rows:
-    # 32 x 256 tiles (the fused few-row form), above: 128 x 256 tiles
+    # 32 x 256 tiles (the fused few-row form), 33..64: 64 x 256, above: 128 x 256
     assert pol(Q4K, 1024, 2048, 1)["path"] == G
     assert pol(Q4K, 1024, 2048, 4)["path"] == G
     p = pol(Q4K, 1024, 2048, 5)
     assert (p["path"], p["tile_m"], p["tile_n"]) == (F16, 32, 256)
-    assert (pol(Q4K, 1024, 2048, 32)["tile_m"], pol(Q4K, 1024, 2048, 33)["tile_m"]) == (32, 128)
+    assert [pol(Q4K, 1024, 2048, m)["tile_m"] for m in (32, 33, 64, 65)] == [32, 64, 64, 128]
     with rq.options(fused_max_rows=2):
         assert pol(Q4K, 1024, 2048, 3)["path"] == F16
     with rq.options(mmq_f16=0):   # the int8 path keeps GEMVs up to fused_max_rows
@@ -161,6 +161,9 @@ def test_policy_tiles_and_splits(rq):
     assert (p["splits"], p["sb_per_split"]) == (16, 1)
     p = pol(Q6K, 14336, 4096, 12, 256)   # 16 tiles -> 32 splits of ceil(56 / 32) = 2 -> 28
     assert (p["splits"], p["sb_per_split"]) == (28, 2)
+    # 64-row tiles: splits capped at nsb / 2 like the 128-row ones
+    p = pol(Q4K, 4096, 4096, 48, 256)    # 16 tiles -> 32 wanted, capped at 16 / 2
+    assert (p["tile_m"], p["splits"], p["sb_per_split"]) == (64, 8, 2)
     # Q6_K tiles are 128 x 256 too: down at 8B has 4 x 16 tiles -> 8 splits of 7 super-blocks
     p = pol(Q6K, 14336, 4096, 512, 256)
     assert (p["tile_m"], p["tile_n"], p["splits"], p["sb_per_split"]) == (128, 256, 8, 7)
