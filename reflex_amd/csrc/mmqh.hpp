@@ -252,23 +252,11 @@ RFXQ_DEV u4_t q6k_multipliers(u4_t sc, uint32_t dbits, uint32_t h) {
 
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q4_K weights.
 template <int MT>
-RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
+RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
     using namespace mmqh;
     constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
-    MmqDesc ds = dv;
-    {
-        uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
-#pragma unroll
-        for (uint32_t i = 0; i < sizeof(MmqDesc) / 4u; i++) p[i] = __builtin_amdgcn_readfirstlane(p[i]);
-        t_local = __builtin_amdgcn_readfirstlane(t_local);
-    }
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-    const uint32_t ks = t_local % ds.splits;
-    const uint32_t rest = t_local / ds.splits;
-    const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nsb = ds.k / 256u;
     const uint32_t sb0 = ks * ds.sb_per_split;
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
@@ -462,6 +450,41 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
 }
 
+template <int MT>
+RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds);
+
+// One (32 MT)x256 tile (and one split-K range): the descriptor made uniform,
+// the tile decoded, and the rows computed by the body of as many 32-row tiles
+// as the tile has rows (a ragged last tile, or an expert group of 33 rows in
+// a 64-row tile, runs no MFMAs on absent rows).
+template <int MT, int TY>
+RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
+    MmqDesc ds = dv;
+    {
+        uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
+#pragma unroll
+        for (uint32_t i = 0; i < sizeof(MmqDesc) / 4u; i++) p[i] = __builtin_amdgcn_readfirstlane(p[i]);
+        t_local = __builtin_amdgcn_readfirstlane(t_local);
+    }
+    const uint32_t ks = t_local % ds.splits;
+    const uint32_t rest = t_local / ds.splits;
+    const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
+    const uint32_t m0 = tm * 32u * MT, n0 = tn * mmqh::BN;
+    const uint32_t sub = min((uint32_t)MT, (ds.m - m0 + 31u) / 32u);  // 32-row tiles with rows
+    auto run = [&](auto mt) {
+        constexpr int M = decltype(mt)::value;
+        if constexpr (TY == TY_Q4K) mmqh_q4k_rows<M>(ds, m0, n0, ks, lds);
+        else mmqh_q6k_rows<M>(ds, m0, n0, ks, lds);
+    };
+    if constexpr (MT >= 4) {
+        if (sub >= 4u) return run(std::integral_constant<int, 4>{});
+        if (sub == 3u) return run(std::integral_constant<int, 3>{});
+    }
+    if constexpr (MT >= 2)
+        if (sub >= 2u) return run(std::integral_constant<int, 2>{});
+    run(std::integral_constant<int, 1>{});
+}
+
 // The tiles of a launch are spread over the XCDs by their real count: a grid
 // sized by an upper bound (device-written MoE tables) would otherwise leave
 // the XCDs that own the tail of the tile range without work.
@@ -474,32 +497,20 @@ RFXQ_DEV void mmqh_q4k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
         const uint32_t b = mmqh::xcd_tile(blockIdx.x, tiles);                                               \
         const MmqDesc d = mmq_pick(args, b);                                                                 \
         if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;                                     \
-        TILE<MT>(d, b - d.wg_begin, lds);                                                                     \
+        mmqh_tile<MT, TILE>(d, b - d.wg_begin, lds);                                                          \
     }
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k, mmqh_q4k_tile, 4, 2)
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m32, mmqh_q4k_tile, 1, 4)
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m64, mmqh_q4k_tile, 2, 3)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k, TY_Q4K, 4, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m32, TY_Q4K, 1, 4)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m64, TY_Q4K, 2, 3)
 
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
 // the Q4_K tile's layout and pipeline, with the Q6_K weight operands.
 template <int MT>
-RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
+RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
     using namespace mmqh;
     constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
-    MmqDesc ds = dv;
-    {
-        uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
-#pragma unroll
-        for (uint32_t i = 0; i < sizeof(MmqDesc) / 4u; i++) p[i] = __builtin_amdgcn_readfirstlane(p[i]);
-        t_local = __builtin_amdgcn_readfirstlane(t_local);
-    }
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-    const uint32_t ks = t_local % ds.splits;
-    const uint32_t rest = t_local / ds.splits;
-    const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nsb = ds.k / 256u;
     const uint32_t sb0 = ks * ds.sb_per_split;
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
@@ -686,6 +697,6 @@ RFXQ_DEV void mmqh_q6k_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     }
 }
 
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, mmqh_q6k_tile, 4, 2)
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m32, mmqh_q6k_tile, 1, 3)
-RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m64, mmqh_q6k_tile, 2, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, TY_Q6K, 4, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m32, TY_Q6K, 1, 3)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m64, TY_Q6K, 2, 2)

@@ -933,6 +933,35 @@ int launch_act(Ctx* c, const float* x, uint32_t rows, uint32_t k, uint8_t* base,
     return RFXQ_OK;
 }
 
+// SiLU(gate) * up of rows x k written straight into the layouts of L at
+// `base` (rfxq_silu_and_mul_q8_1 without its f32 output): one launch instead
+// of rfxq_silu_and_mul and the layout pass, the same values
+int launch_silu_act(Ctx* c, const float* gate, const float* up, uint32_t rows, uint32_t k, uint8_t* base,
+                    const ActLayout& L, bool i8, bool h, hipStream_t stream) {
+    struct {
+        const float* gate;
+        const float* up;
+        uint32_t rows, k;
+        int8_t* xq;
+        uint32_t* xds;
+        uint16_t* xh;
+        uint16_t* xsx;
+        float* xrs;
+        float* y;
+    } a = {gate,
+           up,
+           rows,
+           k,
+           i8 ? reinterpret_cast<int8_t*>(base + L.xq) : nullptr,
+           i8 ? reinterpret_cast<uint32_t*>(base + L.xds) : nullptr,
+           h ? reinterpret_cast<uint16_t*>(base + L.xh) : nullptr,
+           h ? reinterpret_cast<uint16_t*>(base + L.xsx) : nullptr,
+           h ? reinterpret_cast<float*>(base + L.xrs) : nullptr,
+           nullptr};
+    const uint32_t grid = i8 ? quant_grid((uint64_t)rows * (k / 32u)) : act_f16_grid(rows, act_f16_wave(rows, k));
+    return launch(c->silu_q, grid, 0, stream, &a, sizeof a, "rfxq_silu_and_mul_q8_1 launch");
+}
+
 // f16: Q4_K / Q6_K descriptors on rfxq_mmqh_q4k / _q6k (f16 activation
 // layout; tile_m 32: the *_m32 kernels); int8: tile_m 64 takes rfxq_mmq_*_m64
 int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
@@ -2266,8 +2295,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, bm))
             return rc;
     }
-    if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-    if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
+    if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
     if (n_dn) {
         if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
                                 f16, bm))
@@ -2480,8 +2508,7 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
                                 2u * tiles_bound * pa.tg.tiles_n, false, stream, f16, bm))
             return rc;
-        if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
-        if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
+        if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
         if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
                                 stream, f16, bm))
             return rc;
