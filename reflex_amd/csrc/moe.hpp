@@ -187,8 +187,8 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __
 }
 
 // Grouping and descriptor tables, one workgroup of 1024 threads: the pairs
-// (token t, slot j) sorted by (expert, t*k + j) with a bitonic sort of the
-// keys expert*P2 + pair in LDS; then
+// (token t, slot j) in the order (expert, t*k + j) by a stable counting sort;
+// then
 //   pair_row[q]       token of the pair at sorted position q (MMQ row gather)
 //   comb_idx/comb_w   per token, its pairs' positions and weights in
 //                     increasing expert order (the combine's order)
@@ -207,7 +207,7 @@ struct MoePlanArgs {
     MmqDesc tg, tu, td;         // templates (m, rows, wg_begin filled per expert)
     uint64_t w_stride_gu;       // bytes between experts in gate / up
     uint64_t w_stride_dn;       // ... in down
-    uint32_t tokens, k, E, P2;  // P2: power of two >= tokens * k
+    uint32_t tokens, k, E, pad;
     uint32_t bm, ffn, hidden, f16;  // f16: descriptors read the f16 activation layout
     // GEMV form (few tokens; gemv_gu NULL: not written): per sorted pair q,
     // gemv_gu[2q], [2q+1] = gate, up of its token's row, gemv_dn[q] = down of
@@ -223,31 +223,38 @@ struct MoePlanArgs {
 };
 
 extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) {
-    __shared__ uint32_t key[kPlanMaxPairs];
+    __shared__ uint16_t pe[kPlanMaxPairs];                        // expert of each pair
+    __shared__ __attribute__((aligned(16))) float pw[kPlanMaxPairs];  // its weight (first: routing scratch)
+    static_assert(4u * kRouteLds <= kPlanMaxPairs, "routing scratch inside pw");
     __shared__ uint32_t start[kRouteMaxE + 1], cnt[kRouteMaxE];
-    const uint32_t tid = threadIdx.x, P = a.tokens * a.k, P2 = a.P2;
+    const uint32_t tid = threadIdx.x, P = a.tokens * a.k;
     if (a.logits) {
-        __shared__ __attribute__((aligned(16))) float sp[4][kRouteLds];
+        float (*sp)[kRouteLds] = reinterpret_cast<float (*)[kRouteLds]>(pw);
         if (tid < 256u)
             for (uint32_t t = tid >> 6; t < a.tokens; t += 4u)
                 moe_route_token(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
                                 const_cast<float*>(a.wts), sp[tid >> 6]);
         __syncthreads();  // (a workgroup barrier orders the global writes for the reads below)
     }
-    // Stable counting sort of the pairs by expert into key[0, P) (values
-    // expert * P2 + pair): a histogram, its exclusive scan (base), then the
-    // pairs in chunks of 1024, one per thread: a lane's rank among the
+    // Stable counting sort of the pairs by expert: the pairs' experts and
+    // weights read once into LDS; a histogram and its exclusive scan give each
+    // expert's first position; then, chunk by chunk, a pair's rank among the
     // lanes of its wave with the same expert comes from ballots over the
-    // expert's bits, the waves before it from per-wave counts in LDS.
+    // expert's bits and the waves before it from per-wave counts in LDS.
+    // The pair's sorted position q is written where it is used: its row
+    // gather (pair_row[q]), its combine slot (the rank of its expert among
+    // its token's experts) and, in the GEMV form, its descriptors.
     __shared__ uint32_t base[kRouteMaxE];
     __shared__ uint16_t wcnt[16][kRouteMaxE];
     const uint32_t E = a.E, lane = tid & 63u, wave = tid >> 6;
-    for (uint32_t e = tid; e < E; e += 1024u) {
-        cnt[e] = 0u;
-        base[e] = 0u;
+    for (uint32_t e = tid; e < E; e += 1024u) base[e] = 0u;
+#pragma unroll 4
+    for (uint32_t i = tid; i < P; i += 1024u) {
+        pe[i] = (uint16_t)min((uint32_t)a.idx[i], E - 1u);
+        pw[i] = a.wts[i];
     }
     __syncthreads();
-    for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[min((uint32_t)a.idx[i], E - 1u)], 1u);
+    for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[pe[i]], 1u);
     __syncthreads();
     const uint32_t hist = tid < E ? base[tid] : 0u;
     for (uint32_t off = 1; off < E; off <<= 1) {
@@ -256,13 +263,17 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         if (tid < E) base[tid] += o;
         __syncthreads();
     }
-    if (tid < E) base[tid] -= hist;  // inclusive -> exclusive
+    if (tid < E) {
+        base[tid] -= hist;  // inclusive -> exclusive
+        start[tid] = base[tid];
+        cnt[tid] = hist;
+    }
     for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
         for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
         __syncthreads();
         const uint32_t i = c0 + tid;
         const bool valid = i < P;
-        const uint32_t e = valid ? min((uint32_t)a.idx[i], E - 1u) : 0u;
+        const uint32_t e = valid ? (uint32_t)pe[i] : 0u;
         uint64_t same = __ballot(valid);
 #pragma unroll
         for (uint32_t bit = 0; bit < 10u; bit++) {  // E <= 1024
@@ -273,9 +284,36 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         if (valid && rank == 0u) wcnt[wave][e] = (uint16_t)__popcll(same);
         __syncthreads();
         if (valid) {
-            uint32_t pos = base[e] + rank;
-            for (uint32_t w = 0; w < wave; w++) pos += wcnt[w][e];
-            key[pos] = e * P2 + i;
+            uint32_t q = base[e] + rank;
+            for (uint32_t w = 0; w < wave; w++) q += wcnt[w][e];
+            const uint32_t t = i / a.k;
+            a.pair_row[q] = (int32_t)t;
+            uint32_t slot = 0;
+            for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)pe[t * a.k + j] < e;
+            a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
+            a.comb_w[(uint64_t)t * a.k + slot] = pw[i];
+            if (a.gemv_gu) {
+                GemvDesc* dg = a.gemv_gu + 2u * q;
+                GemvDesc* du = dg + 1;
+                GemvDesc* dd = a.gemv_dn + q;
+                const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.vg);
+                const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.vu);
+                const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.vd);
+#pragma unroll
+                for (uint32_t f = 0; f < sizeof(GemvDesc) / 4u; f++) {
+                    reinterpret_cast<uint32_t*>(dg)[f] = tg[f];
+                    reinterpret_cast<uint32_t*>(du)[f] = tu[f];
+                    reinterpret_cast<uint32_t*>(dd)[f] = td[f];
+                }
+                dg->w = a.vg.w + (uint64_t)e * a.w_stride_gu;
+                du->w = a.vu.w + (uint64_t)e * a.w_stride_gu;
+                dd->w = a.vd.w + (uint64_t)e * a.w_stride_dn;
+                dg->x = du->x = a.vg.x + (uint64_t)t * a.hidden;
+                dg->y = a.vg.y + (uint64_t)q * a.ffn;
+                du->y = a.vu.y + (uint64_t)q * a.ffn;
+                dd->x = a.vd.x + (uint64_t)q * a.ffn;
+                dd->y = a.vd.y + (uint64_t)q * a.hidden;
+            }
         }
         __syncthreads();
         if (tid < E) {
@@ -285,41 +323,6 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         }
         __syncthreads();  // (the next chunk clears wcnt)
     }
-    // per sorted position: gather row, combine slot, expert bounds
-    for (uint32_t q = tid; q < P; q += 1024u) {
-        const uint32_t pair = key[q] % P2, e = key[q] / P2;
-        const uint32_t t = pair / a.k;
-        a.pair_row[q] = (int32_t)t;
-        uint32_t slot = 0;
-#pragma unroll 8
-        for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)a.idx[(uint64_t)t * a.k + j] < e;
-        a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
-        a.comb_w[(uint64_t)t * a.k + slot] = a.wts[pair];
-        if (a.gemv_gu) {
-            GemvDesc* dg = a.gemv_gu + 2u * q;
-            GemvDesc* du = dg + 1;
-            GemvDesc* dd = a.gemv_dn + q;
-            const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.vg);
-            const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.vu);
-            const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.vd);
-#pragma unroll
-            for (uint32_t i = 0; i < sizeof(GemvDesc) / 4u; i++) {
-                reinterpret_cast<uint32_t*>(dg)[i] = tg[i];
-                reinterpret_cast<uint32_t*>(du)[i] = tu[i];
-                reinterpret_cast<uint32_t*>(dd)[i] = td[i];
-            }
-            dg->w = a.vg.w + (uint64_t)e * a.w_stride_gu;
-            du->w = a.vu.w + (uint64_t)e * a.w_stride_gu;
-            dd->w = a.vd.w + (uint64_t)e * a.w_stride_dn;
-            dg->x = du->x = a.vg.x + (uint64_t)t * a.hidden;
-            dg->y = a.vg.y + (uint64_t)q * a.ffn;
-            du->y = a.vu.y + (uint64_t)q * a.ffn;
-            dd->x = a.vd.x + (uint64_t)q * a.ffn;
-            dd->y = a.vd.y + (uint64_t)q * a.hidden;
-        }
-        if (q == 0u || key[q - 1u] / P2 != e) start[e] = q;
-        if (q + 1u == P || key[q + 1u] / P2 != e) cnt[e] = q + 1u;  // end, made a count below
-    }
     __syncthreads();
     // per expert (one thread each): rows, tiles; workgroup offsets by an
     // inclusive scan over the experts (Hillis-Steele in LDS)
@@ -327,7 +330,7 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     const uint32_t tn_f = a.tg.tiles_n, tn_h = a.td.tiles_n;  // column tiles of gate / up and of down
     uint32_t m = 0, tm = 0;
     if (tid < a.E) {
-        m = cnt[tid] ? cnt[tid] - start[tid] : 0u;
+        m = cnt[tid];
         tm = (m + a.bm - 1u) / a.bm;
         scan_gu[tid] = 2u * tm * tn_f;
         scan_dn[tid] = tm * tn_h;

@@ -2349,7 +2349,7 @@ struct MoePlanArgs {
     MmqDesc* descs_dn;
     MmqDesc tg, tu, td;
     uint64_t w_stride_gu, w_stride_dn;
-    uint32_t tokens, k, E, P2;
+    uint32_t tokens, k, E, pad;
     uint32_t bm, ffn, hidden, f16;
     GemvDesc* gemv_gu;
     GemvDesc* gemv_dn;
@@ -2464,9 +2464,6 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     pa.tokens = rows;
     pa.k = top_k;
     pa.E = expert_count;
-    uint32_t p2 = 2;
-    while (p2 < P) p2 <<= 1;
-    pa.P2 = p2;
     pa.bm = bm;
     pa.ffn = ffn;
     pa.hidden = hidden;
