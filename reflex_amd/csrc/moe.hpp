@@ -48,12 +48,37 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_silu_and_mul(const float*
 }
 
 // out[t,:] = sum_j w[t,j] * pair_out[idx[t,j],:] for j in 0..k (pairs sorted
-// by expert), evaluated as fma(w, v, acc) from acc = 0.
+// by expert), evaluated as fma(w, v, acc) from acc = 0. With `vec` (hidden a
+// multiple of 4, 16-byte aligned rows) a workgroup takes whole tokens, four
+// columns per lane, the k rows' loads issued together; else one element per
+// lane. Same operations in the same order either way.
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_combine(const float* __restrict__ pair_out,
                                                                   const int32_t* __restrict__ idx,
                                                                   const float* __restrict__ w,
                                                                   float* __restrict__ out, uint32_t tokens,
-                                                                  uint32_t k, uint32_t hidden) {
+                                                                  uint32_t k, uint32_t hidden, uint32_t vec) {
+    if (vec) {
+        for (uint32_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+            const uint64_t tk = (uint64_t)t * k;
+            for (uint32_t c = 4u * threadIdx.x; c < hidden; c += 1024u) {
+                float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+                for (uint32_t j = 0; j < k; j++) {
+                    const int32_t p = idx[tk + j];
+                    if (p >= 0) {
+                        const float wj = w[tk + j];
+                        const float4 v = *reinterpret_cast<const float4*>(pair_out + (uint64_t)p * hidden + c);
+                        acc.x = fmaf(wj, v.x, acc.x);
+                        acc.y = fmaf(wj, v.y, acc.y);
+                        acc.z = fmaf(wj, v.z, acc.z);
+                        acc.w = fmaf(wj, v.w, acc.w);
+                    }
+                }
+                *reinterpret_cast<float4*>(out + (uint64_t)t * hidden + c) = acc;
+            }
+        }
+        return;
+    }
     const uint64_t total = (uint64_t)tokens * hidden;
     for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256u) {
         const uint64_t t = i / hidden, c = i % hidden;
