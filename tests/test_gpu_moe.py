@@ -269,6 +269,39 @@ def test_moe_ffn_grouped_device_in_graph(rq, orc):
         torch.randn(1024, device=DEV).sum().item()
 
 
+def test_moe_graph_replays_after_workspace_growth(rq, orc):
+    """A captured call keeps its workspace: a later, larger eager call grows
+    the library's per-device workspace (the old one is retired, not freed),
+    and the graph captured before still replays to the eager result."""
+    tokens, experts, hidden, ffn, k = 2, 32, 1024, 512, 4
+    y_d, _, _, ws, x, logits = _moe_device_case(rq, orc, tokens, experts, hidden, ffn, k, 970)
+    lg = _dev(logits)
+    out = torch.empty(tokens * hidden, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+    torch.cuda.synchronize()
+    # a prefill far larger than any other call of the suite (~200 MB of workspace)
+    bt, be, bh, bf, bk = 2048, 16, 2048, 2048, 4
+    gw = synth.weights(Q4K, be * bf, bh, 980)
+    dw = synth.weights(Q4K, be * bh, bf, 981)
+    W = lambda a, i, o: rq.Weight(rq.GgmlType.Q4K, _dev(a), [i, o, be])  # noqa: E731
+    big = (W(gw, bh, bf), W(gw, bh, bf), W(dw, bf, bh))
+    bx = _dev(synth.activations(bt * bh, 982))
+    blg = _dev(synth.normals(983, bt * be))
+    bout = torch.empty(bt * bh, device=DEV)
+    rq.moe_ffn_grouped_device(bx, bt, bh, blg, be, bk, True, 1.0, *big, bout)
+    torch.cuda.synchronize()
+    assert torch.isfinite(bout).all()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(tokens, hidden), y_d)
+
+
 def test_moe_ffn_grouped_device_errors(rq):
     experts, hidden, ffn = 2, 256, 256
     W = lambda n, i, o: rq.Weight(rq.GgmlType.Q4K, torch.zeros(n, dtype=torch.uint8, device=DEV), [i, o, experts])  # noqa: E731
