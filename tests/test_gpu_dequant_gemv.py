@@ -306,3 +306,26 @@ def test_gemv_gather_errors(rq):
         rq.gemv_gather(x, w, [3, 256])
     with pytest.raises(rq.ReflexError, match="x.len"):
         rq.gemv_gather(x[:256], w, [1])
+
+
+def test_gemv_large_plans_interleaved_repeat(rq):
+    """Two plans of tens of MB (one descriptor of 32768 rows; the 8B q, k,
+    gate and down shapes), run interleaved three times, each run equal to the
+    single calls bit for bit: a plan keeps no state between runs."""
+    def big_plan(shapes, seed):
+        items, singles = [], []
+        for i, (ty, n, k) in enumerate(shapes):
+            w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, seed + i), k, n, device=DEV)
+            x = _dev(synth.activations(k, seed + 50 + i))
+            singles.append(rq.gemv(x, w).cpu().numpy())
+            items.append((x, w, torch.empty(n, device=DEV)))
+        return rq.GemvPlan(items), items, singles
+    a = big_plan([(Q6K, 32768, 1024)], 600)
+    b = big_plan([(Q4K, 4096, 4096), (Q6K, 1024, 4096), (Q4K, 14336, 4096), (Q6K, 4096, 14336)], 700)
+    for rep in range(3):
+        for plan, items, singles in (a, b):
+            for _, _, y in items:
+                y.fill_(float("nan"))
+            plan.run()
+            for (_, _, y), ref in zip(items, singles):
+                assert np.array_equal(y.cpu().numpy(), ref), f"run {rep}"

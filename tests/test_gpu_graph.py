@@ -85,3 +85,22 @@ def test_gemm_plan_in_graph(rq):
             plan.run()
     torch.cuda.synchronize()
     _replays(g, [y for _, _, y in items], want, _other_work)
+
+
+def test_gemv_large_plan_twice_in_graph(rq):
+    """A 62 MB plan captured twice in one graph, and run eagerly between the
+    replays, replays to the eager bits."""
+    shapes = [(Q6K, 32768, 1024), (Q4K, 14336, 4096)]
+    items = [(_x(k, 200 + i), _w(rq, ty, n, k, 210 + i), torch.empty(n, device=DEV)) for i, (ty, n, k) in enumerate(shapes)]
+    plan = rq.GemvPlan(items)
+    plan.run()
+    torch.cuda.synchronize()
+    want = [y.clone() for _, _, y in items]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            plan.run()
+            plan.run()
+    torch.cuda.synchronize()
+    _replays(g, [y for _, _, y in items], want, lambda: (plan.run(), _other_work()))
