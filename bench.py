@@ -333,8 +333,11 @@ def moe_leg(rq, synth, torch, np, dev, timed):
         logits = synth.normals(synth.seed_for(5, 0, 4), tokens * E).reshape(tokens, E)
         y = torch.empty(tokens * H, device=dev)
         used = len({e for t in range(tokens) for e, _ in rq.route_top_k(logits[t], K)})
-        steps = 30 if tokens > 1 else 100
-        ms = timed(lambda i: rq.moe_ffn_grouped(x, tokens, H, logits, E, K, True, 1.0, gate, up, down, y), steps, 10)
+        # warm-up of ~20 ms or more: the first few dozen prefill calls of a
+        # process issue up to twice as slowly on the host (measured: 394 us per
+        # call in the second batch of 30, then 196 us from the third on)
+        steps, warm = (30, 150) if tokens > 1 else (100, 500)
+        ms = timed(lambda i: rq.moe_ffn_grouped(x, tokens, H, logits, E, K, True, 1.0, gate, up, down, y), steps, warm)
         wbytes = used * per_expert
         ops = tokens * K * 2 * 3 * F * H
         gbs = wbytes / (ms * 1e-3) / 1e9
@@ -346,7 +349,7 @@ def moe_leg(rq, synth, torch, np, dev, timed):
         # the same step with routing on the device (logits in device memory)
         lg = torch.from_numpy(logits).to(dev)
         ms_d = timed(lambda i: rq.moe_ffn_grouped_device(x, tokens, H, lg, E, K, True, 1.0, gate, up, down, y),
-                     steps, 10)
+                     steps, warm)
         gbs_d = wbytes / (ms_d * 1e-3) / 1e9
         out[tag + "_device_routing"] = {"ms_per_step": round(ms_d, 4), "gbs": round(gbs_d, 1),
                                         "frac_hbm_peak": round(gbs_d / HBM_PEAK_GBS, 4)}

@@ -232,8 +232,8 @@ struct MoePlanArgs {
     MmqDesc tg, tu, td;         // templates (m, rows, wg_begin filled per expert)
     uint64_t w_stride_gu;       // bytes between experts in gate / up
     uint64_t w_stride_dn;       // ... in down
-    uint32_t tokens, k, E, pad;
-    uint32_t bm, ffn, hidden, f16;  // f16: descriptors read the f16 activation layout
+    uint32_t tokens, k, E, bm_dn;  // bm_dn: row tile of the down projection
+    uint32_t bm, ffn, hidden, f16;  // bm: row tile of gate / up; f16: descriptors read the f16 activation layout
     // GEMV form (few tokens; gemv_gu NULL: not written): per sorted pair q,
     // gemv_gu[2q], [2q+1] = gate, up of its token's row, gemv_dn[q] = down of
     // the pair's SiLU·up row, from templates whose w, x and y are the bases
@@ -353,12 +353,13 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     // inclusive scan over the experts (Hillis-Steele in LDS)
     __shared__ uint32_t scan_gu[kRouteMaxE], scan_dn[kRouteMaxE];
     const uint32_t tn_f = a.tg.tiles_n, tn_h = a.td.tiles_n;  // column tiles of gate / up and of down
-    uint32_t m = 0, tm = 0;
+    uint32_t m = 0, tm = 0, tmd = 0;
     if (tid < a.E) {
         m = cnt[tid];
         tm = (m + a.bm - 1u) / a.bm;
+        tmd = (m + a.bm_dn - 1u) / a.bm_dn;
         scan_gu[tid] = 2u * tm * tn_f;
-        scan_dn[tid] = tm * tn_h;
+        scan_dn[tid] = tmd * tn_h;
     }
     __syncthreads();
     for (uint32_t off = 1; off < a.E; off <<= 1) {
@@ -377,7 +378,7 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     if (tid < a.E) {
         const uint32_t e = tid;
         const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
-        const uint32_t wg_gu = scan_gu[e] - 2u * tm * tn_f, wg_dn = scan_dn[e] - tm * tn_h;
+        const uint32_t wg_gu = scan_gu[e] - 2u * tm * tn_f, wg_dn = scan_dn[e] - tmd * tn_h;
         // descriptors from the templates, filled in place in global memory
         MmqDesc* g = a.descs_gu + 2u * e;
         MmqDesc* u = g + 1;
@@ -401,7 +402,8 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         d->w = a.td.w + (uint64_t)e * a.w_stride_dn;
         g->rows = u->rows = a.pair_row + st;
         g->m = u->m = d->m = m;
-        g->tiles_m = u->tiles_m = d->tiles_m = tm;
+        g->tiles_m = u->tiles_m = tm;
+        d->tiles_m = tmd;
         g->y = a.tg.y + (uint64_t)st * a.ffn;
         u->y = a.tu.y + (uint64_t)st * a.ffn;
         if (a.f16) {  // xh rows of 2*ffn bytes, xsx records of ffn/256 * 32 bytes, xrs

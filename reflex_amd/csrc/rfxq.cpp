@@ -787,16 +787,28 @@ constexpr uint32_t kGemvRowsMax = 4;
 // above
 uint32_t f16_tile_m(uint32_t rows) { return rows <= 32u ? 32u : rows <= 64u ? 64u : kMmqBM; }
 
-// Row tile of a grouped MoE launch, `pairs` routed rows over `experts`
-// groups: f16 kernels 32-row tiles up to 12 rows per expert on average,
-// 64-row up to 64 (config 5 at 32 rows on average: 229 us per layer against
-// 255 us with 32-row and 266 us with 128-row tiles: fewer experts read twice),
-// 128 above; int8 kernels 64-row tiles up to 48.
-uint32_t moe_tile_m(uint32_t pairs, uint32_t experts, bool f16) {
+// Row tile of one grouped MoE GEMM, `pairs` routed rows over `experts`
+// groups, `tiles_n` column tiles per expert: f16 kernels 32-row tiles up to
+// 12 rows per expert on average, 128 above 64; in between 64 or 128,
+// whichever runs the launch's tiles (estimated from the average) in fewer
+// waves of resident workgroups (64-row tiles: 3 per CU for Q4_K, 2 for
+// Q6_K; 128-row tiles: 2 per CU), 128 on a tie. Config 5 (32 rows per expert
+// on average): gate + up, 768 tiles, stay at 64 rows (88 us against 105 us
+// at 128, which needs 2 waves), and the down projection, 1024 tiles and 2
+// waves either way, takes 128 (60 us against 67 us). int8 kernels: 64-row
+// tiles up to 48 rows on average.
+uint32_t moe_tile_m(uint32_t pairs, uint32_t experts, bool f16, uint32_t ty, uint32_t tiles_n, uint32_t cus) {
     if (!experts) return kMmqBM;
     const uint32_t avg = (pairs + experts - 1u) / experts;
-    if (f16) return avg <= 12u ? 32u : avg <= 64u ? 64u : kMmqBM;
-    return avg <= 48u ? 64u : kMmqBM;
+    if (!f16) return avg <= 48u ? 64u : kMmqBM;
+    if (avg <= 12u) return 32u;
+    if (avg > 64u) return kMmqBM;
+    auto waves = [&](uint32_t bm, uint32_t per_cu) {
+        const uint64_t tiles = (uint64_t)experts * ((avg + bm - 1u) / bm) * tiles_n;
+        const uint64_t slots = (uint64_t)std::max(1u, cus) * per_cu;
+        return (tiles + slots - 1u) / slots;
+    };
+    return waves(64u, ty == RFXQ_TYPE_Q6_K ? 2u : 3u) < waves(kMmqBM, 2u) ? 64u : kMmqBM;
 }
 
 rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o) {
@@ -2244,7 +2256,10 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     // used experts' average row count
     uint32_t used = 0;
     for (uint32_t e = 0; e < expert_count; e++) used += off[e + 1] > off[e];
-    const uint32_t bm = moe_tile_m(P, used, f16);
+    const uint32_t bn = tile_bn(f16);
+    const uint32_t bm_gu = moe_tile_m(P, used, f16, gate->ggml_type, 2u * ((ffn + bn - 1u) / bn), (uint32_t)c->cus);
+    const uint32_t bm_dn = moe_tile_m(P, used, f16, down->ggml_type, (hidden + bn - 1u) / bn, (uint32_t)c->cus);
+    uint32_t bm = bm_gu;  // the row tile of the descriptors add() writes
     std::vector<MmqDesc> descs;
     uint32_t wg_gu = 0;
     // act: the activation layouts (rows gathered through rws, or starting at row r0)
@@ -2271,7 +2286,6 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         d.type = ew.ggml_type;
         d.ldy = n;
         d.tiles_m = (m + bm - 1u) / bm;
-        const uint32_t bn = tile_bn(f16);
         d.tiles_n = (n + bn - 1u) / bn;
         d.splits = 1;
         d.sb_per_split = d.k / 256u;
@@ -2287,6 +2301,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     }
     const uint32_t n_gu = (uint32_t)descs.size();
     uint32_t wg_dn = 0;
+    bm = bm_dn;
     for (uint32_t e = 0; e < expert_count; e++) {
         const uint32_t m = off[e + 1] - off[e];
         if (!m) continue;
@@ -2305,13 +2320,13 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
 
     if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
     if (n_gu) {
-        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, bm))
+        if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, bm_gu))
             return rc;
     }
     if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
     if (n_dn) {
         if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
-                                f16, bm))
+                                f16, bm_dn))
             return rc;
     }
     if (int rc = launch_combine(c, dout, d_ci, d_cw, out, rows, top_k, hidden, stream)) return rc;
@@ -2352,7 +2367,7 @@ struct MoePlanArgs {
     MmqDesc* descs_dn;
     MmqDesc tg, tu, td;
     uint64_t w_stride_gu, w_stride_dn;
-    uint32_t tokens, k, E, pad;
+    uint32_t tokens, k, E, bm_dn;
     uint32_t bm, ffn, hidden, f16;
     GemvDesc* gemv_gu;
     GemvDesc* gemv_dn;
@@ -2433,8 +2448,10 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     MmqDesc* d_gu = reinterpret_cast<MmqDesc*>(B + o_dgu);
     MmqDesc* d_dn = reinterpret_cast<MmqDesc*>(B + o_ddn);
 
-    // the row tile by the average rows of the experts the pairs can reach
-    const uint32_t bm = moe_tile_m(P, std::min(expert_count, P), f16);
+    // row tiles by the average rows of the experts the pairs can reach
+    const uint32_t bn = tile_bn(f16), reach = std::min(expert_count, P);
+    const uint32_t bm = moe_tile_m(P, reach, f16, gate->ggml_type, 2u * ((ffn + bn - 1u) / bn), (uint32_t)c->cus);
+    const uint32_t bm_dn = moe_tile_m(P, reach, f16, down->ggml_type, (hidden + bn - 1u) / bn, (uint32_t)c->cus);
     MoePlanArgs pa;
     std::memset(&pa, 0, sizeof pa);
     pa.idx = d_idx;
@@ -2453,7 +2470,6 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         d->k = k;
         d->type = w0->ggml_type;
         d->ldy = n;
-        const uint32_t bn = tile_bn(f16);
         d->tiles_n = (n + bn - 1u) / bn;
         d->splits = 1;
         d->sb_per_split = k / 256u;
@@ -2468,6 +2484,7 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     pa.k = top_k;
     pa.E = expert_count;
     pa.bm = bm;
+    pa.bm_dn = bm_dn;
     pa.ffn = ffn;
     pa.hidden = hidden;
     GemvItem ig, iu, id;
@@ -2504,13 +2521,13 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
         // launch grids: upper bounds on the tiles (sum over experts of
         // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
-        const uint32_t tiles_bound = (P + bm - 1u) / bm + expert_count;
+        const uint32_t bound_gu = (P + bm - 1u) / bm + expert_count, bound_dn = (P + bm_dn - 1u) / bm_dn + expert_count;
         if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
-                                2u * tiles_bound * pa.tg.tiles_n, false, stream, f16, bm))
+                                2u * bound_gu * pa.tg.tiles_n, false, stream, f16, bm))
             return rc;
         if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
-        if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, tiles_bound * pa.td.tiles_n, false,
-                                stream, f16, bm))
+        if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, bound_dn * pa.td.tiles_n, false,
+                                stream, f16, bm_dn))
             return rc;
     }
     if (int rc = launch_combine(c, dout, pa.comb_idx, pa.comb_w, out, rows, top_k, hidden, stream)) return rc;
