@@ -14,6 +14,13 @@
 #pragma once
 #include "common.hpp"
 
+// Phase probes of rfxq_moe_plan: empty in the library; a timing harness
+// defines them.
+#ifndef MOE_PLAN_PROBE
+#define MOE_PLAN_PROBE(i)
+#define MOE_ROUTE_PROBE(i)
+#endif
+
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_gather(const float* __restrict__ src,
                                                                  const uint32_t* __restrict__ perm_row,
                                                                  float* __restrict__ dst, uint32_t num,
@@ -102,113 +109,116 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_moe_combine(const float* 
 constexpr uint32_t kRouteMaxE = 1024;    // experts per lane: up to 16
 constexpr uint32_t kPlanMaxPairs = 16384;  // sort keys in LDS
 
-// route_top_k_with_norm (src/moe.rs:47-98), one wave per token: softmax of
-// the logits (max subtracted; the sum over lanes then a butterfly, so it can
-// differ from a sequential sum in the last bit), the k best by probability
-// descending then expert index ascending, renormalised by their sum (in
-// selection order) when `normalize`; weights multiplied by `scale`.
-// Selection by rank rather than k rounds of a wave-wide arg-max (each a
-// chain of cross-lane shuffles): the probabilities go to LDS and every
-// expert counts those that precede it (greater, or equal at a lower index);
-// the experts of rank < k are the selection, in rank order. A NaN
-// probability ranks below every number, so the k indices are always valid
-// experts (such a token's weights are NaN).
-constexpr uint32_t kRouteLds = kRouteMaxE + 128u;  // floats per wave: probabilities, then k (p, e) slots
-// One wave routes token t (all 64 lanes take part); `sp` is the wave's
-// kRouteLds floats of LDS.
+// route_top_k_with_norm (src/moe.rs:47-98), one workgroup of G threads per
+// token: softmax of the logits (max subtracted; the sum by wave 0 as lane
+// sums over its experts l, l + 64, ... then a butterfly over the lanes, so it
+// can differ from a sequential sum in the last bit), the k best by
+// probability descending then expert index ascending, renormalised by their
+// sum (in selection order) when `normalize`; weights multiplied by `scale`.
+// Selection by rank: the ranking values go to LDS and every expert counts
+// those that precede it (greater, or equal at a lower index), the count split
+// over all G threads (G / E threads per expert, each over a slice of the
+// experts, summed by LDS atomics); the experts of rank < k are the selection,
+// in rank order. A NaN probability ranks below every number (value -0.5), so
+// the k indices are always valid experts (such a token's weights are NaN).
+struct RouteLds {
+    float rv[kRouteMaxE];      // ranking values (padding to whole float4s: -1)
+    float pv[kRouteMaxE];      // probabilities
+    uint32_t rank[kRouteMaxE];
+    float slot_p[64];
+    int32_t slot_e[64];
+    float red[16];             // per-wave maxima, then the sum
+};
+
+template <uint32_t G>
 __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits, uint32_t t, uint32_t E,
                                                 uint32_t k, uint32_t normalize, float scale,
-                                                int32_t* __restrict__ idx, float* __restrict__ wts, float* sp) {
-    const uint32_t lane = threadIdx.x & 63u;
+                                                int32_t* __restrict__ idx, float* __restrict__ wts, RouteLds& L) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const float* l = logits + (uint64_t)t * E;
-    constexpr uint32_t J = kRouteMaxE / 64u;
-    float p[J];
+    MOE_ROUTE_PROBE(0);
+    // max (exact in any order)
     float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        const uint32_t e = lane + 64u * j;
-        p[j] = e < E ? l[e] : -INFINITY;
-        mx = fmaxf(mx, p[j]);
+    for (uint32_t e = tid; e < E; e += G) {
+        const float v = l[e];
+        L.pv[e] = v;
+        mx = fmaxf(mx, v);
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    float sum = 0.0f;
+    if (lane == 0u) L.red[wave] = mx;
+    for (uint32_t e = tid; e < E; e += G) L.rank[e] = 0u;
+    __syncthreads();
+    mx = L.red[0];
 #pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        const uint32_t e = lane + 64u * j;
-        p[j] = e < E ? expf(p[j] - mx) : 0.0f;
-        sum += p[j];
+    for (uint32_t w = 1; w < G / 64u; w++) mx = fmaxf(mx, L.red[w]);
+    for (uint32_t e = tid; e < E; e += G) L.pv[e] = expf(L.pv[e] - mx);
+    __syncthreads();
+    MOE_ROUTE_PROBE(1);
+    if (wave == 0u) {
+        float sum = 0.0f;
+        for (uint32_t e = lane; e < E; e += 64u) sum += L.pv[e];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+        if (lane == 0u) L.red[0] = sum;
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
-    // ranking values: the probability, NaN as -0.5 (below every probability)
-#pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        const uint32_t e = lane + 64u * j;
+    __syncthreads();
+    const float sum = L.red[0];
+    const uint32_t E4 = (E + 3u) & ~3u;
+    for (uint32_t e = tid; e < E4; e += G) {
         if (e < E) {
-            p[j] = p[j] / sum;
-            sp[e] = p[j] == p[j] ? p[j] : -0.5f;
-        } else if (e < ((E + 3u) & ~3u)) {
-            sp[e] = -1.0f;  // padding to whole float4s: precedes nothing
+            const float p = L.pv[e] / sum;
+            L.pv[e] = p;
+            L.rv[e] = p == p ? p : -0.5f;
+        } else {
+            L.rv[e] = -1.0f;  // precedes nothing
         }
     }
-    float* slot_p = sp + kRouteMaxE;
-    int32_t* slot_e = reinterpret_cast<int32_t*>(sp + kRouteMaxE + 64u);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        const uint32_t e = lane + 64u * j;
-        if (64u * j < E) {  // wave-uniform
-            const float mine = e < E ? sp[e] : 0.0f;
-            // experts below this chunk precede on >=, above it on >, and
-            // within it on > or (== at a lower index)
-            const uint32_t lo = 64u * j, hi = min(64u * j + 64u, (E + 3u) & ~3u), end = (E + 3u) & ~3u;
-            uint32_t r = 0;
-#pragma unroll 8
-            for (uint32_t c = 0; c < lo; c += 4u) {
-                const float4 q = *reinterpret_cast<const float4*>(sp + c);
-                r += (uint32_t)(q.x >= mine) + (uint32_t)(q.y >= mine) + (uint32_t)(q.z >= mine) +
-                     (uint32_t)(q.w >= mine);
-            }
-#pragma unroll 4
-            for (uint32_t c = lo; c < hi; c += 4u) {
-                const float4 q = *reinterpret_cast<const float4*>(sp + c);
-                r += (q.x > mine || (q.x == mine && c < e)) ? 1u : 0u;
-                r += (q.y > mine || (q.y == mine && c + 1u < e)) ? 1u : 0u;
-                r += (q.z > mine || (q.z == mine && c + 2u < e)) ? 1u : 0u;
-                r += (q.w > mine || (q.w == mine && c + 3u < e)) ? 1u : 0u;
-            }
-#pragma unroll 8
-            for (uint32_t c = hi; c < end; c += 4u) {
-                const float4 q = *reinterpret_cast<const float4*>(sp + c);
-                r += (uint32_t)(q.x > mine) + (uint32_t)(q.y > mine) + (uint32_t)(q.z > mine) +
-                     (uint32_t)(q.w > mine);
-            }
-            if (e < E && r < k) {
-                slot_p[r] = p[j];
-                slot_e[r] = (int32_t)e;
-            }
+    __syncthreads();
+    // S slices of the experts per expert (S = G / E, at least 1)
+    const uint32_t S = G >= 2u * E ? G / E : 1u;
+    const uint32_t chunk = ((E4 / 4u + S - 1u) / S) * 4u;
+    for (uint32_t i = tid; i < E * S; i += G) {
+        const uint32_t e = i % E, c0 = (i / E) * chunk, c1 = min(E4, c0 + chunk);
+        const float mine = L.rv[e];
+        uint32_t r = 0;
+        for (uint32_t c = c0; c < c1; c += 4u) {
+            const float4 q = *reinterpret_cast<const float4*>(L.rv + c);
+            r += (q.x > mine || (q.x == mine && c < e)) ? 1u : 0u;
+            r += (q.y > mine || (q.y == mine && c + 1u < e)) ? 1u : 0u;
+            r += (q.z > mine || (q.z == mine && c + 2u < e)) ? 1u : 0u;
+            r += (q.w > mine || (q.w == mine && c + 3u < e)) ? 1u : 0u;
+        }
+        if (S > 1u) atomicAdd(&L.rank[e], r);
+        else L.rank[e] = r;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += G) {
+        const uint32_t r = L.rank[e];
+        if (r < k) {
+            L.slot_p[r] = L.pv[e];
+            L.slot_e[r] = (int32_t)e;
         }
     }
-    __builtin_amdgcn_wave_barrier();
-    float top_sum = 0.0f;  // in selection order
-    for (uint32_t s = 0; s < k; s++) top_sum += slot_p[s];
-    if (lane < k) {
-        const float sel_p = slot_p[lane];
+    __syncthreads();
+    MOE_ROUTE_PROBE(2);
+    if (tid < k) {
+        float top_sum = 0.0f;  // in selection order
+        for (uint32_t s2 = 0; s2 < k; s2++) top_sum += L.slot_p[s2];
+        const float sel_p = L.slot_p[tid];
         const float wv = normalize ? sel_p / top_sum : sel_p;
-        idx[(uint64_t)t * k + lane] = slot_e[lane];
-        wts[(uint64_t)t * k + lane] = wv * scale;
+        idx[(uint64_t)t * k + tid] = L.slot_e[tid];
+        wts[(uint64_t)t * k + tid] = wv * scale;
     }
+    __syncthreads();  // the scratch is free again
 }
 
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __restrict__ logits, uint32_t tokens,
                                                                 uint32_t E, uint32_t k, uint32_t normalize,
                                                                 float scale, int32_t* __restrict__ idx,
                                                                 float* __restrict__ wts) {
-    __shared__ __attribute__((aligned(16))) float sp[4][kRouteLds];
-    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (t >= tokens) return;
-    moe_route_token(logits, t, E, k, normalize, scale, idx, wts, sp[threadIdx.x >> 6]);
+    __shared__ __attribute__((aligned(16))) RouteLds L;
+    moe_route_token<256>(logits, blockIdx.x, E, k, normalize, scale, idx, wts, L);
 }
 
 // Grouping and descriptor tables, one workgroup of 1024 threads: the pairs
@@ -247,20 +257,39 @@ struct MoePlanArgs {
     float scale;
 };
 
+// Exclusive prefix sum of v over the 1024 threads of the workgroup (every
+// thread takes part): wave scans, then the wave totals (`tot`: 16 words of
+// LDS). Integer adds, so the grouping does not matter.
+__device__ __forceinline__ uint32_t plan_scan(uint32_t v, uint32_t* tot) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (uint32_t o = 1; o < 64u; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63u) tot[wave] = x;
+    __syncthreads();
+    uint32_t pre = 0;
+    for (uint32_t w = 0; w < wave; w++) pre += tot[w];
+    __syncthreads();  // tot is free again
+    return pre + x - v;
+}
+
 extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) {
     __shared__ uint16_t pe[kPlanMaxPairs];                        // expert of each pair
     __shared__ __attribute__((aligned(16))) float pw[kPlanMaxPairs];  // its weight (first: routing scratch)
-    static_assert(4u * kRouteLds <= kPlanMaxPairs, "routing scratch inside pw");
+    static_assert(sizeof(RouteLds) <= sizeof(float) * kPlanMaxPairs, "routing scratch inside pw");
     __shared__ uint32_t start[kRouteMaxE + 1], cnt[kRouteMaxE];
     const uint32_t tid = threadIdx.x, P = a.tokens * a.k;
     if (a.logits) {
-        float (*sp)[kRouteLds] = reinterpret_cast<float (*)[kRouteLds]>(pw);
-        if (tid < 256u)
-            for (uint32_t t = tid >> 6; t < a.tokens; t += 4u)
-                moe_route_token(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
-                                const_cast<float*>(a.wts), sp[tid >> 6]);
-        __syncthreads();  // (a workgroup barrier orders the global writes for the reads below)
+        // (its workgroup barriers order the global writes for the reads below)
+        RouteLds& L = *reinterpret_cast<RouteLds*>(pw);
+        for (uint32_t t = 0; t < a.tokens; t++)
+            moe_route_token<1024>(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
+                                  const_cast<float*>(a.wts), L);
     }
+    MOE_PLAN_PROBE(1);
     // Stable counting sort of the pairs by expert: the pairs' experts and
     // weights read once into LDS; a histogram and its exclusive scan give each
     // expert's first position; then, chunk by chunk, a pair's rank among the
@@ -279,20 +308,18 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         pw[i] = a.wts[i];
     }
     __syncthreads();
+    MOE_PLAN_PROBE(2);
     for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[pe[i]], 1u);
     __syncthreads();
+    __shared__ uint32_t tot[16];
     const uint32_t hist = tid < E ? base[tid] : 0u;
-    for (uint32_t off = 1; off < E; off <<= 1) {
-        const uint32_t o = (tid < E && tid >= off) ? base[tid - off] : 0u;
-        __syncthreads();
-        if (tid < E) base[tid] += o;
-        __syncthreads();
-    }
+    const uint32_t first = plan_scan(hist, tot);
     if (tid < E) {
-        base[tid] -= hist;  // inclusive -> exclusive
-        start[tid] = base[tid];
+        base[tid] = first;
+        start[tid] = first;
         cnt[tid] = hist;
     }
+    MOE_PLAN_PROBE(3);
     for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
         for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
         __syncthreads();
@@ -349,36 +376,21 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         __syncthreads();  // (the next chunk clears wcnt)
     }
     __syncthreads();
-    // per expert (one thread each): rows, tiles; workgroup offsets by an
-    // inclusive scan over the experts (Hillis-Steele in LDS)
-    __shared__ uint32_t scan_gu[kRouteMaxE], scan_dn[kRouteMaxE];
+    MOE_PLAN_PROBE(4);
+    if (a.gemv_gu) return;  // the GEMV form runs no MMQ launch
+    // per expert (one thread each): rows, tiles; workgroup offsets by
+    // exclusive scans over the experts
     const uint32_t tn_f = a.tg.tiles_n, tn_h = a.td.tiles_n;  // column tiles of gate / up and of down
     uint32_t m = 0, tm = 0, tmd = 0;
     if (tid < a.E) {
         m = cnt[tid];
         tm = (m + a.bm - 1u) / a.bm;
         tmd = (m + a.bm_dn - 1u) / a.bm_dn;
-        scan_gu[tid] = 2u * tm * tn_f;
-        scan_dn[tid] = tmd * tn_h;
     }
-    __syncthreads();
-    for (uint32_t off = 1; off < a.E; off <<= 1) {
-        uint32_t vg = 0, vd = 0;
-        if (tid < a.E && tid >= off) {
-            vg = scan_gu[tid - off];
-            vd = scan_dn[tid - off];
-        }
-        __syncthreads();
-        if (tid < a.E) {
-            scan_gu[tid] += vg;
-            scan_dn[tid] += vd;
-        }
-        __syncthreads();
-    }
+    const uint32_t wg_gu = plan_scan(2u * tm * tn_f, tot), wg_dn = plan_scan(tmd * tn_h, tot);
     if (tid < a.E) {
         const uint32_t e = tid;
         const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
-        const uint32_t wg_gu = scan_gu[e] - 2u * tm * tn_f, wg_dn = scan_dn[e] - tmd * tn_h;
         // descriptors from the templates, filled in place in global memory
         MmqDesc* g = a.descs_gu + 2u * e;
         MmqDesc* u = g + 1;
@@ -420,4 +432,5 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         u->wg_begin = wg_gu + tm * tn_f;
         d->wg_begin = wg_dn;
     }
+    MOE_PLAN_PROBE(5);
 }

@@ -2352,7 +2352,7 @@ int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_
         int32_t* idx;
         float* w;
     } a = {logits, tokens, expert_count, top_k, normalize ? 1u : 0u, weight_scale, 0, idx, weights};
-    if (int rc = launch(c->moe_route, (tokens + 3u) / 4u, 0, stream, &a, sizeof a, "rfxq_moe_route launch"))
+    if (int rc = launch(c->moe_route, tokens, 0, stream, &a, sizeof a, "rfxq_moe_route launch"))
         return rc;
     return ok();
 }
