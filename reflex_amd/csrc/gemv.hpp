@@ -53,6 +53,8 @@ struct GemvArgs {
     const GemvDesc* table;  // the descriptors (NULL: the first ndesc <= GEMV_INLINE of inl)
     const uint4* ranges;    // optional: per workgroup {d0, it0, d1, it1}
     uint32_t ndesc, part_floats;
+    uint32_t iters_each;    // without ranges: every descriptor's row iterations, when all share them (else 0)
+    uint32_t pad;
     GemvDesc inl[GEMV_INLINE];
 };
 
@@ -671,20 +673,31 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
         it1 = __builtin_amdgcn_readfirstlane(r.w);
     } else {
         // no range table: iterations split evenly by count, descriptor
-        // counts read from the descriptors (inline or a table)
+        // counts from iters_each or read from the descriptors (inline or a
+        // table; a table the device just wrote costs a round trip per read)
+        const uint32_t ie = args.iters_each;
         uint32_t total = 0;
-        for (uint32_t i = 0; i < args.ndesc; i++) total += gemv_iters(*gemv_desc(args, i));
+        if (ie) total = ie * args.ndesc;
+        else
+            for (uint32_t i = 0; i < args.ndesc; i++) total += gemv_iters(*gemv_desc(args, i));
         uint32_t g0 = (uint32_t)(((uint64_t)total * blockIdx.x) / gridDim.x);
         uint32_t g1 = (uint32_t)(((uint64_t)total * (blockIdx.x + 1u)) / gridDim.x);
-        d0 = 0;
-        for (uint32_t c; d0 + 1u < args.ndesc && g0 >= (c = gemv_iters(*gemv_desc(args, d0)));) {
-            g0 -= c;
-            d0++;
-        }
-        d1 = 0;
-        for (uint32_t c; d1 + 1u < args.ndesc && g1 > (c = gemv_iters(*gemv_desc(args, d1)));) {
-            g1 -= c;
-            d1++;
+        if (ie) {
+            d0 = min(g0 / ie, args.ndesc - 1u);
+            g0 -= d0 * ie;
+            d1 = g1 ? min((g1 - 1u) / ie, args.ndesc - 1u) : 0u;
+            g1 -= d1 * ie;
+        } else {
+            d0 = 0;
+            for (uint32_t c; d0 + 1u < args.ndesc && g0 >= (c = gemv_iters(*gemv_desc(args, d0)));) {
+                g0 -= c;
+                d0++;
+            }
+            d1 = 0;
+            for (uint32_t c; d1 + 1u < args.ndesc && g1 > (c = gemv_iters(*gemv_desc(args, d1)));) {
+                g1 -= c;
+                d1++;
+            }
         }
         it0 = __builtin_amdgcn_readfirstlane(g0);
         it1 = __builtin_amdgcn_readfirstlane(g1);

@@ -90,6 +90,7 @@ struct GemvArgs {
     const GemvDesc* table;
     const GemvRange* ranges;
     uint32_t ndesc, part_floats;
+    uint32_t iters_each, pad;
     GemvDesc inl[kGemvInline];
 };
 static_assert(sizeof(GemvDesc) == 56, "GemvDesc layout");
@@ -633,6 +634,10 @@ int gemv_launch_counted(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* 
     if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
     a.ndesc = (uint32_t)v.size();
     a.table = table;
+    // one iteration count for every descriptor: the kernel need not read them
+    a.iters_each = v.empty() ? 0u : v[0].iters;
+    for (const auto& it : v)
+        if (it.iters != a.iters_each) a.iters_each = 0u;
     if (!table)
         for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
     return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
