@@ -2118,6 +2118,17 @@ int rfxq_silu_and_mul(const float* gate, const float* up, float* out, uint64_t n
     return ok();
 }
 
+}  // extern "C"
+
+namespace {
+int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
+                       const uint32_t* host_idx, const float* host_w, uint32_t expert_count, uint32_t top_k,
+                       int normalize, float weight_scale, const rfxq_weight* gate, const rfxq_weight* up,
+                       const rfxq_weight* down, float* out, hipStream_t stream);
+}  // namespace
+
+extern "C" {
+
 int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits_host,
                          uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
                          const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
@@ -2183,7 +2194,17 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
 
     // Few tokens (decode): every routed pair is a GEMV of its expert's
     // slices (gate and up in one launch, down in another): weights are read
-    // once per pair at HBM rate instead of through 128-row MMQ tiles.
+    // once per pair at HBM rate instead of through 128-row MMQ tiles. The
+    // host's routing goes up in one copy and the device plans the launches
+    // (rfxq_moe_ffn_grouped_device's pipeline, same results); expert counts
+    // that pipeline does not take are planned here.
+    if (rows <= kMoeGemvRows && expert_count >= 4u && expert_count <= kRouteMaxE && top_k <= 64u &&
+        gate->len == up->len) {
+        std::vector<float> wsc(rwts.size());
+        for (size_t i = 0; i < wsc.size(); i++) wsc[i] = rwts[i] * weight_scale;
+        return moe_grouped_device(x, rows, hidden, nullptr, ridx.data(), wsc.data(), expert_count, top_k, normalize,
+                                  weight_scale, gate, up, down, out, stream);
+    }
     if (rows <= kMoeGemvRows) {
         const uint64_t g_gate = 0;
         const uint64_t g_up = g_gate + align256((uint64_t)P * ffn * 4u);
@@ -2383,11 +2404,28 @@ struct MoePlanArgs {
 };
 static_assert(sizeof(MoePlanArgs) == 616, "MoePlanArgs layout");
 
+
 int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
                                 uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
                                 const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
                                 hipStream_t stream) {
-    if (!x || !out || !router_logits || !gate || !up || !down)
+    if (!router_logits) return fail(RFXQ_ERR_INVALID_INPUT, "moe_ffn_grouped_device: NULL argument");
+    return moe_grouped_device(x, rows, hidden, router_logits, nullptr, nullptr, expert_count, top_k, normalize,
+                              weight_scale, gate, up, down, out, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The device-planned pipeline: routing on the device from `router_logits`,
+// or the host's routing (`host_idx`, `host_w`: rows x top_k experts and
+// weights already multiplied by weight_scale) uploaded in one copy.
+int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
+                       const uint32_t* host_idx, const float* host_w, uint32_t expert_count, uint32_t top_k,
+                       int normalize, float weight_scale, const rfxq_weight* gate, const rfxq_weight* up,
+                       const rfxq_weight* down, float* out, hipStream_t stream) {
+    if (!x || !out || !gate || !up || !down)
         return fail(RFXQ_ERR_INVALID_INPUT, "moe_ffn_grouped_device: NULL argument");
     if (rows == 0) return ok();
     if (gate->expert_count != expert_count || up->expert_count != expert_count || down->expert_count != expert_count)
@@ -2504,7 +2542,12 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
         pa.vd = id.d;
     }
 
-    if (gemv_form) {  // few tokens: the plan launch routes them too
+    if (host_idx) {  // routed on the host
+        std::vector<uint8_t> host(o_w - o_idx + (uint64_t)P * 4u, 0);
+        std::memcpy(host.data(), host_idx, (uint64_t)P * 4u);
+        std::memcpy(host.data() + (o_w - o_idx), host_w, (uint64_t)P * 4u);
+        if (int rc = stage_upload(c, d_idx, host.data(), host.size(), stream)) return rc;
+    } else if (gemv_form) {  // few tokens: the plan launch routes them too
         pa.logits = router_logits;
         pa.normalize = normalize ? 1u : 0u;
         pa.scale = weight_scale;
@@ -2538,6 +2581,10 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
     if (int rc = launch_combine(c, dout, pa.comb_idx, pa.comb_w, out, rows, top_k, hidden, stream)) return rc;
     return ok();
 }
+
+}  // namespace
+
+extern "C" {
 
 // ---------------------------------------------------------------- GGUF files
 
