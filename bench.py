@@ -292,8 +292,10 @@ def decode_8b_leg(rq, synth, torch, np, dev, timed):
     4096x14336 Q6_K; 138 MB), and the tied LM head 151936x1024 Q6_K (128 MB),
     each with three rotated weight copies (beyond the 256 MB Infinity Cache)."""
     out = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(synth.seed_for(4, 0, 98))
     for tag, layer in (("layer", synth.QWEN3_8B_LAYER), ("lm_head", [synth.LM_HEAD])):
-        xs = {k: torch.randn(k, device=dev) for k in {k for *_, k in layer}}
+        xs = {k: torch.randn(k, device=dev, generator=gen) for k in sorted({k for *_, k in layer})}
         plans, keep = [], []
         for c in range(3):
             items = []
