@@ -300,7 +300,10 @@ int rfxq_silu_and_mul(const float* gate, const float* up, float* out, uint64_t n
  * experts' gate/up MMQ as one grouped launch, SiLU*up, the down MMQ as one
  * grouped launch and a fixed-order weighted combine into out[rows][hidden]
  * (overwritten). gate/up: [hidden, ffn, E]; down: [ffn, hidden, E]. One
- * host-to-device copy of the routing table; no per-expert launches. */
+ * host-to-device copy of the routing table; no per-expert launches. Up to 4
+ * rows (with 4 <= expert_count <= 1024 and top_k <= 64) run every routed pair
+ * as GEMVs planned on the device from the copied routing, the launches of
+ * rfxq_moe_ffn_grouped_device. */
 int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits_host,
                          uint32_t expert_count, uint32_t top_k, int normalize, float weight_scale,
                          const rfxq_weight* gate, const rfxq_weight* up, const rfxq_weight* down, float* out,
@@ -322,7 +325,8 @@ int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_
  * per-expert row lists, src/model/dense.rs:1539-1546, 1602-1605), so the
  * call adds no host synchronisation and no host-to-device copy. Up to 4
  * tokens run every routed pair as GEMVs, as the host-routed path does; more
- * take the grouped MMQ path (64-row tiles for short expert groups). Requires
+ * take the grouped MMQ path (row tiles per GEMM by the expert groups' average
+ * rows and the waves of workgroups their tiles need). Requires
  * 4 <= expert_count <= 1024, top_k <= 64 and rows * top_k <= 16384.
  * Routing errors of the host path (non-finite softmax sums) are not
  * reported: such tokens get non-finite outputs. */
