@@ -224,6 +224,17 @@ def test_moe_ffn_grouped_device_decode(rq, orc, tokens, k):
     assert orc.rel_err_row_l2(y_d, ref) < TOL
 
 
+@pytest.mark.parametrize("tokens,experts,k", [(1, 1024, 64), (3, 512, 16), (4, 6, 6)])
+def test_moe_decode_wide_routing(rq, orc, tokens, experts, k):
+    """Decode with many experts: the plan launch routes each token with all
+    1024 threads (one rank count per expert and thread at 1024 experts, up to
+    170 threads per expert at 6), the host-routed call plans on the device
+    from its own routing; both meet the bound and agree."""
+    y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, experts, 256, 256, k, 970 + experts)
+    assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
+    assert orc.rel_err_row_l2(y_d, ref) < TOL
+
+
 def test_moe_ffn_grouped_device_decode_in_graph(rq, orc):
     """The GEMV form of the device-routed layer replays from a HIP graph too."""
     tokens, experts, hidden, ffn, k = 2, 32, 1024, 512, 4
