@@ -779,11 +779,29 @@ uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 //   REFLEX_QUANT_MMA_TILE=64);
 // - split-K: none once the tiles cover half the CUs (each CU holds two
 //   workgroups; a split costs a partials round trip and a reduce launch),
-//   else enough splits for about two workgroups per CU, each of at least two
-//   super-blocks (one with 32-row tiles); REFLEX_QUANT_MMA_SPLITS forces the
-//   count.
+//   else the smallest split (at least two super-blocks; one with 32-row
+//   tiles) whose workgroups all fit in two per CU (split_sb);
+//   REFLEX_QUANT_MMA_SPLITS forces the count.
 enum : uint32_t { PATH_GEMV_ROWS = RFXQ_PATH_GEMV_ROWS, PATH_MMQ_INT8 = RFXQ_PATH_MMQ_INT8, PATH_MMQ_F16 = RFXQ_PATH_MMQ_F16 };
 constexpr uint32_t kGemvRowsMax = 4;
+
+// Super-blocks per split-K workgroup for the GEMMs of one launch (their
+// tile counts and super-blocks per row): the fewest, at least min_sb, whose
+// workgroups (tiles x ceil(nsb / W) per GEMM) fit in `budget`, so that the
+// launch runs as one wave of workgroups. (With the splits rounded up
+// instead, the 8B layer's v + down launch made 544 workgroups for 512
+// places: a second wave of 32 that started when the first v workgroups
+// ended and finished well after the rest.)
+uint32_t split_sb(const std::vector<std::pair<uint32_t, uint32_t>>& tiles_nsb, uint32_t min_sb, uint32_t budget) {
+    uint32_t max_nsb = 1;
+    for (const auto& t : tiles_nsb) max_nsb = std::max(max_nsb, t.second);
+    for (uint32_t w = std::max(1u, min_sb); w < max_nsb; w++) {
+        uint64_t total = 0;
+        for (const auto& t : tiles_nsb) total += (uint64_t)t.first * ((t.second + w - 1u) / w);
+        if (total <= budget) return w;
+    }
+    return max_nsb;
+}
 
 
 // Row tile of the f16 kernels for a GEMM (or an expert group averaging
@@ -835,9 +853,11 @@ rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows,
     const uint32_t tiles = ((rows + p.tile_m - 1u) / p.tile_m) * ((n + p.tile_n - 1u) / p.tile_n);
     uint32_t splits = 1;
     if (o.quant_mma_splits) splits = o.quant_mma_splits;
-    else if (2u * tiles < std::max(cus, 1u))
+    else if (2u * tiles < std::max(cus, 1u)) {
         // 32-row tiles stream weights (few rows): splits down to one super-block
-        splits = std::min((2u * cus + tiles - 1u) / tiles, std::max(1u, p.tile_m == 32u ? nsb : nsb / 2u));
+        const uint32_t w = split_sb({{tiles, nsb}}, p.tile_m == 32u ? 1u : 2u, 2u * std::max(cus, 1u));
+        splits = (nsb + w - 1u) / w;
+    }
     splits = std::min(std::max(1u, splits), nsb);
     p.sb_per_split = (nsb + splits - 1u) / splits;
     p.splits = (nsb + p.sb_per_split - 1u) / p.sb_per_split;
@@ -1220,12 +1240,15 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
     for (uint32_t t = 0; t < kGroupKernels; t++) {
         auto& v = g->descs[t];
         if (v.empty() || (!forced && 2u * g->wgs[t] >= cus)) continue;
-        const uint32_t want = forced ? forced : (2u * cus + g->wgs[t] - 1u) / g->wgs[t];
+        // one split size for the launch, so its workgroups take alike
+        std::vector<std::pair<uint32_t, uint32_t>> tn;
+        for (const auto& d : v) tn.push_back({d.tiles_m * d.tiles_n, d.k / 256u});
+        const uint32_t w_sb = split_sb(tn, group_tile_m(t) == 32u ? 1u : 2u, 2u * std::max(cus, 1u));
         uint32_t wg = 0;
         for (uint32_t i = 0; i < v.size(); i++) {
             MmqDesc& d = v[i];
             const uint32_t nsb = d.k / 256u;
-            const uint32_t s = std::min(want, forced || group_tile_m(t) == 32u ? nsb : std::max(1u, nsb / 2u));
+            const uint32_t s = forced ? std::min(forced, nsb) : (nsb + w_sb - 1u) / w_sb;
             d.sb_per_split = (nsb + s - 1u) / s;
             d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
             if (d.splits > 1u) {
