@@ -18,6 +18,8 @@
 // defines them.
 #ifndef MOE_PLAN_PROBE
 #define MOE_PLAN_PROBE(i)
+#endif
+#ifndef MOE_ROUTE_PROBE
 #define MOE_ROUTE_PROBE(i)
 #endif
 
