@@ -696,21 +696,69 @@ int gemv_items(Ctx* c, const rfxq_gemv_item* items, uint32_t count, hipStream_t 
     return RFXQ_OK;
 }
 
-// A plan's ranges, balanced by bytes: workgroup g starts at the first
-// iteration (in descriptor order) whose start lies at or after g/grid of all
-// weight bytes; the last range ends at the end of the last descriptor.
+// A plan's ranges, balanced by cost: workgroup g starts at the first
+// iteration (in descriptor order) whose start lies at or after g/grid of the
+// launch's cost; the last range ends at the end of the last descriptor. An
+// iteration costs its weight bytes, times kGemvLongCost for a GEMV whose x
+// exceeds kGemvLongK elements and whose rows take several passes (its x
+// staging and passes make its bytes slower), and no range runs into such a
+// GEMV from the one before it: the descriptors split into segments at each
+// one's start, each segment gets workgroups in proportion to its cost
+// (largest remainders) and balances them within itself. (The 8B layer's
+// down projection, K = 14336: 32.9 us by bytes; 28.1 us this way. A
+// workgroup that ran the end of up and the start of down staged both x's
+// and finished last; the measured time jumped between 28 and 35 us with the
+// position of that boundary.)
+constexpr uint32_t kGemvLongK = 4096;
+constexpr double kGemvLongCost = 1.5;
+uint64_t gemv_iter_cost(const GemvItem& it) {
+    return it.d.k > kGemvLongK && it.passes ? (uint64_t)((double)it.iter_bytes * kGemvLongCost) : it.iter_bytes;
+}
+
 void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector<GemvRange>* ranges,
                       std::vector<uint32_t>* max_iters) {
+    // segments [seg[s], seg[s + 1]) of descriptors and their costs
+    std::vector<uint32_t> seg{0u};
+    for (uint32_t d = 1; d < v.size(); d++)
+        if (gemv_iter_cost(v[d]) != v[d].iter_bytes) seg.push_back(d);
+    seg.push_back((uint32_t)v.size());
+    const uint32_t ns = (uint32_t)seg.size() - 1u;
+    std::vector<uint64_t> scost(ns, 0);
     uint64_t total = 0;
-    for (const auto& it : v) total += it.iters * it.iter_bytes;
+    for (uint32_t s2 = 0; s2 < ns; s2++) {
+        for (uint32_t d = seg[s2]; d < seg[s2 + 1u]; d++) scost[s2] += v[d].iters * gemv_iter_cost(v[d]);
+        total += scost[s2];
+    }
+    // workgroups per segment: proportional, at least one, largest remainders
+    std::vector<uint32_t> sg(ns, 1u);
+    if (grid > ns) {
+        std::vector<std::pair<double, uint32_t>> rem;
+        uint32_t used = 0;
+        for (uint32_t s2 = 0; s2 < ns; s2++) {
+            const double want = total ? (double)(grid - ns) * (double)scost[s2] / (double)total : 0.0;
+            sg[s2] += (uint32_t)want;
+            used += (uint32_t)want;
+            rem.push_back({want - (double)(uint32_t)want, s2});
+        }
+        std::sort(rem.begin(), rem.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
+        for (uint32_t r = 0; used < grid - ns; r++, used++) sg[rem[r % ns].second]++;
+    }
     std::vector<std::pair<uint32_t, uint32_t>> start(grid + 1u);
     uint32_t g = 0;
-    uint64_t pos = 0;
-    for (uint32_t d = 0; d < v.size() && g < grid; d++) {
-        for (uint32_t i = 0; i < v[d].iters && g < grid; i++) {
-            while (g < grid && pos >= (total * g + grid - 1u) / grid) start[g++] = {d, i};
-            pos += v[d].iter_bytes;
+    for (uint32_t s2 = 0; s2 < ns && g < grid; s2++) {
+        const uint32_t g0 = g, gn = std::min(sg[s2], grid - g0);
+        uint64_t pos = 0;
+        for (uint32_t d = seg[s2]; d < seg[s2 + 1u] && g < g0 + gn; d++) {
+            const uint64_t c = gemv_iter_cost(v[d]);
+            for (uint32_t i = 0; i < v[d].iters && g < g0 + gn; i++) {
+                while (g < g0 + gn && pos >= (scost[s2] * (g - g0) + gn - 1u) / gn) start[g++] = {d, i};
+                pos += c;
+            }
         }
+        // workgroups the segment could not fill (fewer iterations): empty
+        // ranges at its end
+        const uint32_t dl = seg[s2 + 1u] - 1u;
+        while (g < g0 + gn) start[g++] = {dl, v[dl].iters};
     }
     while (g < grid) start[g++] = {(uint32_t)v.size() - 1u, v.back().iters};  // empty tail ranges
     start[grid] = {(uint32_t)v.size() - 1u, v.back().iters};
