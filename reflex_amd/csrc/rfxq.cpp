@@ -705,9 +705,10 @@ int gemv_items(Ctx* c, const rfxq_gemv_item* items, uint32_t count, hipStream_t 
 // GEMV from the one before it: the descriptors split into segments at each
 // one's start, each segment gets workgroups in proportion to its cost
 // (largest remainders) and balances them within itself. (The 8B layer's
-// down projection, K = 14336: 32.9 us by bytes; 28.1 us this way. A
-// workgroup that ran the end of up and the start of down staged both x's
-// and finished last; the measured time jumped between 28 and 35 us with the
+// down projection, K = 14336: 32.9 us by bytes; 28.1 us this way, and
+// 27.8-28.3 us for any cost factor from 1.2 to 2.0. A workgroup that ran the
+// end of up and the start of down staged both x's and finished last; without
+// the segments the measured time jumped between 28 and 35 us with the
 // position of that boundary.)
 constexpr uint32_t kGemvLongK = 4096;
 constexpr double kGemvLongCost = 1.5;
