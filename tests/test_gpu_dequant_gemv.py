@@ -329,3 +329,33 @@ def test_gemv_large_plans_interleaved_repeat(rq):
             plan.run()
             for (_, _, y), ref in zip(items, singles):
                 assert np.array_equal(y.cpu().numpy(), ref), f"run {rep}"
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_gemv_plan_long_rows_get_their_own_workgroups(rq, orc, order):
+    """GEMVs with K > 4096 (several passes per row) start a range segment of
+    their own with workgroups in proportion to their cost: a long GEMV with
+    only 8 rows (fewer row iterations than its share of workgroups: empty
+    ranges), first or between short ones, equals its single call bit for bit
+    and meets the bound."""
+    shapes = [(Q4K, 64, 4096), (Q6K, 8, 14336), (Q4K, 4096, 1024), (Q8_0, 40, 8192)]
+    if order:
+        shapes = shapes[1:] + shapes[:1]
+    items, singles, refs = [], [], []
+    for i, (ty, n, k) in enumerate(shapes):
+        w_np = orc.synthetic(ty, k, n, 1200 + i)
+        w = _weight(rq, ty, w_np, n, k)
+        xs = synth.activations(k, 1210 + i)
+        x = _dev(xs)
+        singles.append(rq.gemv(x, w).cpu().numpy())
+        items.append((x, w, torch.full((n,), float("nan"), device=DEV)))
+        refs.append((ty, n, k, w_np, xs))
+    plan = rq.GemvPlan(items)
+    for _ in range(2):
+        plan.run()
+        for (_, _, y), s in zip(items, singles):
+            assert np.array_equal(y.cpu().numpy(), s)
+    ty, n, k, w_np, xs = refs[0 if order else 1]
+    want = orc.reference_gemm(ty, w_np, n, k, xs)[0]
+    got = items[0 if order else 1][2].cpu().numpy()
+    assert orc.rel_err_row_l2(got[None], want[None]) < 5e-4
