@@ -1370,27 +1370,41 @@ int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipSt
 int route_top_k(const float* logits, uint32_t n, uint32_t k, bool normalize, uint32_t* idx, float* w) {
     if (!logits || n == 0) return fail(RFXQ_ERR_OTHER, "route_top_k: logits must not be empty");
     if (k == 0 || k > n) return fail(RFXQ_ERR_OTHER, "route_top_k: k (%u) must be in 1..=%u (logits.len())", k, n);
+    // probabilities on the stack up to kRouteStack experts (heap above)
+    constexpr uint32_t kRouteStack = 1024;
+    float stack_probs[kRouteStack];
+    std::vector<float> heap_probs;
+    float* probs = stack_probs;
+    if (n > kRouteStack) {
+        heap_probs.resize(n);
+        probs = heap_probs.data();
+    }
     float maxl = -INFINITY;
     for (uint32_t i = 0; i < n; i++) maxl = std::max(maxl, logits[i]);
-    thread_local std::vector<float> probs;
-    thread_local std::vector<uint32_t> best;
-    probs.resize(n);
-    float sum = 0.0f;
     for (uint32_t i = 0; i < n; i++) probs[i] = std::exp(logits[i] - maxl);
+    float sum = 0.0f;
     for (uint32_t i = 0; i < n; i++) sum += probs[i];
     if (!std::isfinite(sum) || sum <= 0.0f)
         return fail(RFXQ_ERR_OTHER, "route_top_k: softmax sum is non-finite or non-positive (%g)", (double)sum);
     for (uint32_t i = 0; i < n; i++) probs[i] = probs[i] / sum;
     // the k best in (probability descending, index ascending) order: the
     // first k of a stable sort, by insertion into a sorted list of k
-    best.clear();
+    uint32_t stack_best[65];
+    std::vector<uint32_t> heap_best;
+    uint32_t* best = stack_best;
+    if (k + 1u > 65u) {
+        heap_best.resize(k + 1u);
+        best = heap_best.data();
+    }
+    uint32_t nb = 0;
     for (uint32_t i = 0; i < n; i++) {
         const float p = probs[i];
-        if (best.size() == k && !(p > probs[best.back()])) continue;  // ties keep the lower index
-        uint32_t pos = (uint32_t)best.size();
-        while (pos > 0 && p > probs[best[pos - 1]]) pos--;
-        best.insert(best.begin() + pos, i);
-        if (best.size() > k) best.pop_back();
+        if (nb == k && !(p > probs[best[nb - 1u]])) continue;  // ties keep the lower index
+        uint32_t pos = nb;
+        while (pos > 0 && p > probs[best[pos - 1u]]) pos--;
+        for (uint32_t q = nb; q > pos; q--) best[q] = best[q - 1u];
+        best[pos] = i;
+        if (nb < k) nb++;
     }
     float top_sum = 0.0f;
     for (uint32_t t = 0; t < k; t++) top_sum += probs[best[t]];
