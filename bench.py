@@ -48,6 +48,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="skip prefill, 8B and CPU legs")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-only", action="store_true",
+                    help="only the CPU baseline leg, as one JSON line (no GPU; run by the full bench in a child "
+                         "process with the caller's OpenMP settings)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only replay the fused GEMV plan and a calibration copy (for rocprofv3 --pmc runs)")
     ap.add_argument("--prefill-probe", action="store_true",
@@ -62,6 +65,18 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is design-only", file=sys.stderr)
         return 2
+    if args.cpu_only:
+        import numpy as np
+
+        from reflex_amd import synth
+
+        layer, L = synth.QWEN3_06B_LAYER, synth.QWEN3_06B_LAYERS
+        host_w = {(li, pi): synth.weights(ty, n, k, synth.seed_for(2, li, pi))
+                  for li in range(L) for pi, (_, ty, n, k) in enumerate(layer)}
+        print(json.dumps(cpu_leg(host_w, layer, L, np)), flush=True)
+        return 0
+    # the caller's environment, for the CPU baseline's child process
+    child_env = dict(os.environ)
 
     # The host-routed MoE call routes its tokens on OpenMP threads. With the
     # default (active) wait policy, idle OpenMP workers spin and take cores
@@ -248,7 +263,13 @@ def main() -> int:
         result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
     torch.cuda.empty_cache()
     if not args.quick and not args.no_cpu:
-        result["cpu_baseline"] = cpu_leg(host_w, layer, L, np)
+        # in a child process with the caller's OpenMP settings: the passive
+        # waiting set above slows the baseline's many short parallel regions
+        import subprocess
+
+        out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-only"], env=child_env,
+                             capture_output=True, text=True, timeout=300, check=True).stdout
+        result["cpu_baseline"] = json.loads(out.strip().splitlines()[-1])
     print(json.dumps(result), flush=True)
     return 0
 
