@@ -215,12 +215,18 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
     __syncthreads();  // the scratch is free again
 }
 
+// With xh set, the workgroup then writes its token's row of x in the f16
+// activation layout (rfxq_act_f16_wg's row, the same values), so the grouped
+// MMQ path needs no launch of its own for it.
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route(const float* __restrict__ logits, uint32_t tokens,
                                                                 uint32_t E, uint32_t k, uint32_t normalize,
                                                                 float scale, int32_t* __restrict__ idx,
-                                                                float* __restrict__ wts) {
+                                                                float* __restrict__ wts, const float* __restrict__ x,
+                                                                uint32_t hidden, uint16_t* __restrict__ xh,
+                                                                uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
     __shared__ __attribute__((aligned(16))) RouteLds L;
     moe_route_token<256>(logits, blockIdx.x, E, k, normalize, scale, idx, wts, L);
+    if (xh) act_f16_row_wg(QuantSrcPlain{x, hidden, nullptr}, blockIdx.x, hidden, xh, xsx, xrs, nullptr);
 }
 
 // Grouping and descriptor tables, one workgroup of 1024 threads: the pairs

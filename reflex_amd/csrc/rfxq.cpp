@@ -2207,6 +2207,27 @@ int rfxq_silu_and_mul(const float* gate, const float* up, float* out, uint64_t n
 }  // extern "C"
 
 namespace {
+// rfxq_moe_route over `tokens` workgroups; with xh, each also writes its
+// token's row of x (hidden values) in the f16 layout (xh, xsx, xrs)
+int moe_route_launch(Ctx* c, const float* logits, uint32_t tokens, uint32_t E, uint32_t k, int normalize, float scale,
+                     int32_t* idx, float* w, const float* x, uint32_t hidden, uint16_t* xh, uint16_t* xsx, float* xrs,
+                     hipStream_t stream) {
+    struct {
+        const float* l;
+        uint32_t tokens, E, k, normalize;
+        float scale;
+        uint32_t pad;
+        int32_t* idx;
+        float* w;
+        const float* x;
+        uint32_t hidden, pad2;
+        uint16_t* xh;
+        uint16_t* xsx;
+        float* xrs;
+    } a = {logits, tokens, E, k, normalize ? 1u : 0u, scale, 0, idx, w, x, hidden, 0, xh, xsx, xrs};
+    return launch(c->moe_route, tokens, 0, stream, &a, sizeof a, "rfxq_moe_route launch");
+}
+
 int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
                        const uint32_t* host_idx, const float* host_w, uint32_t expert_count, uint32_t top_k,
                        int normalize, float weight_scale, const rfxq_weight* gate, const rfxq_weight* up,
@@ -2456,15 +2477,8 @@ int rfxq_moe_route_device(const float* logits, uint32_t tokens, uint32_t expert_
                     std::min(expert_count, 64u));
     Ctx* c;
     if (int rc = current_ctx(&c)) return rc;
-    struct {
-        const float* l;
-        uint32_t tokens, E, k, normalize;
-        float scale;
-        uint32_t pad;
-        int32_t* idx;
-        float* w;
-    } a = {logits, tokens, expert_count, top_k, normalize ? 1u : 0u, weight_scale, 0, idx, weights};
-    if (int rc = launch(c->moe_route, tokens, 0, stream, &a, sizeof a, "rfxq_moe_route launch"))
+    if (int rc = moe_route_launch(c, logits, tokens, expert_count, top_k, normalize, weight_scale, idx, weights, nullptr,
+                                  0, nullptr, nullptr, nullptr, stream))
         return rc;
     return ok();
 }
@@ -2637,9 +2651,14 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
         pa.logits = router_logits;
         pa.normalize = normalize ? 1u : 0u;
         pa.scale = weight_scale;
-    } else if (int rc = rfxq_moe_route_device(router_logits, rows, expert_count, top_k, normalize, weight_scale,
-                                              d_idx, d_w, stream)) {
-        return rc;
+    } else {
+        // routing, and with the f16 layout the token rows of x in the same launch
+        if (int rc = moe_route_launch(c, router_logits, rows, expert_count, top_k, normalize, weight_scale, d_idx, d_w,
+                                      f16 ? x : nullptr, hidden,
+                                      f16 ? reinterpret_cast<uint16_t*>(B + o_x + Lx.xh) : nullptr,
+                                      f16 ? reinterpret_cast<uint16_t*>(B + o_x + Lx.xsx) : nullptr,
+                                      f16 ? reinterpret_cast<float*>(B + o_x + Lx.xrs) : nullptr, stream))
+            return rc;
     }
     if (int rc = launch(c->moe_plan, 1, 0, stream, &pa, sizeof pa, "rfxq_moe_plan launch", 1024)) return rc;
     if (gemv_form) {
@@ -2652,7 +2671,8 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
         if (int rc = rfxq_silu_and_mul(gout, uout, gout, (uint64_t)P * ffn, stream)) return rc;
         if (int rc = gemv_launch_counted(c, dn, pa.gemv_dn, stream)) return rc;
     } else {
-        if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16, stream)) return rc;
+        // (the f16 rows came with the routing; host-routed calls convert here)
+        if (int rc = launch_act(c, x, rows, hidden, B + o_x, Lx, !f16, f16 && host_idx, stream)) return rc;
         // launch grids: upper bounds on the tiles (sum over experts of
         // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
         const uint32_t bound_gu = (P + bm - 1u) / bm + expert_count, bound_dn = (P + bm_dn - 1u) / bm_dn + expert_count;
