@@ -191,10 +191,12 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, rows: int, k: int, eps: float) -> np.n
     return out.reshape(rows, k)
 
 
-def moe_ffn_grouped_reference(x, routes, gate_w, up_w, down_w, ty, hidden, ffn, n_experts):
+def moe_ffn_grouped_reference(x, routes, gate_w, up_w, down_w, ty, hidden, ffn, n_experts, down_ty=None):
     """dense.rs:1509-1559 semantics on the host: for each expert, gather its rows,
     gate/up GEMM, silu*up, down GEMM, weighted scatter-add. f64 matmuls on the
-    dequantized expert slices (quant_expert_weight: kernels.rs:2656-2694)."""
+    dequantized expert slices (quant_expert_weight: kernels.rs:2656-2694).
+    `down_ty` is the down projection's type when it differs (Q4_K_M files
+    store it as Q6_K)."""
     rows = x.shape[0]
     out = np.zeros((rows, hidden), dtype=np.float32)
     groups = [[] for _ in range(n_experts)]
@@ -212,7 +214,7 @@ def moe_ffn_grouped_reference(x, routes, gate_w, up_w, down_w, ty, hidden, ffn, 
         g = reference_gemm(ty, gate_w[e * g_len:(e + 1) * g_len], ffn, hidden, xe)
         u = reference_gemm(ty, up_w[e * g_len:(e + 1) * g_len], ffn, hidden, xe)
         a = silu_and_mul(g, u)
-        dn = reference_gemm(ty, down_w[e * d_len:(e + 1) * d_len], hidden, ffn, a)
+        dn = reference_gemm(ty if down_ty is None else down_ty, down_w[e * d_len:(e + 1) * d_len], hidden, ffn, a)
         out[rr] += ww[:, None] * dn
     return out
 
@@ -336,7 +338,8 @@ def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) 
     f16(16(q-8) * f16(d*sc/16)) for the high-nibble ones, plus the constant
     part f16(8*d*sc - dmin*m) against the f16 hi + lo block sums. Q6_K:
     f16((q-32) * f16(d*sc)) for codes from low nibbles, f16(16(q-32) *
-    f16(d*sc/16)) for codes from high nibbles. Any difference between the kernel and this is the
+    f16(d*sc/16)) for codes from high nibbles. Q8_0: f16(q * d). Any
+    difference between the kernel and this is the
     kernel's own f32 accumulation."""
     x2 = np.ascontiguousarray(x.reshape(-1, k), dtype=np.float32)
     rows = x2.shape[0]
@@ -380,6 +383,13 @@ def mmqh_model_reference(ty: int, w: np.ndarray, n: int, k: int, x: np.ndarray) 
         code = (q - 32).astype(np.float64) * np.repeat(np.where(hi, 16.0, 1.0), 16, axis=2)
         wop = _f16(code.reshape(n, k) * np.repeat(s16.reshape(n, -1), 16, axis=1))
         y = hv @ wop.T
+    elif ty == Q8_0:
+        # f16(q * d): one rounding of the exact product of the code and the f16 d
+        b = np.ascontiguousarray(w, dtype=np.uint8).reshape(n, k // 32, 34)
+        d = b[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+        q = b[:, :, 2:34].view(np.int8).astype(np.float64)
+        wop = _f16(q * d[:, :, None]).reshape(n, k)
+        y = hv @ wop.T
     else:
-        raise ValueError("mmqh_model_reference: Q4_K and Q6_K only")
+        raise ValueError("mmqh_model_reference: Q4_K, Q6_K and Q8_0 only")
     return (y * xrs[:, None].astype(np.float64)).astype(np.float32)

@@ -145,6 +145,12 @@ RFXQ_DEV uint32_t act_row(const MmqDesc& ds, uint32_t r) {
     return ds.rows ? (uint32_t)ds.rows[r] : r;
 }
 
+// First activation row of the tile's buffer resource: the tile's own first
+// row (m0) when rows are not gathered, so that offsets stay within 32 bits
+// for any row count; 0 for a gathered GEMM, whose source rows can be any
+// (the host keeps those activations under 4 GiB).
+RFXQ_DEV uint32_t act_base(const MmqDesc& ds, uint32_t m0) { return ds.rows ? 0u : m0; }
+
 // y rows of one 32-row activation tile: acc[r] is weight column
 // 8*(r/4) + 4*h + r%4 of the 32-column tile starting at c_base
 RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t c_base, uint32_t h, const v16f_t& acc,
@@ -264,20 +270,23 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const uint32_t rec_bytes = nsb * 32u;
     uint8_t* const sx_lds = lds + 2u * kAct;
 
-    // Weight columns past the matrix read past the buffer: zeros, no fault.
-    // Activation rows are clamped or gathered (act_row): always in bounds.
-    const rsrc_t r_act = make_rsrc(ds.xq, 0xFFFFFFFFu);
-    const rsrc_t r_w = make_rsrc(ds.w, ds.n * row_bytes);
-    const rsrc_t r_sx = make_rsrc(ds.xds, 0xFFFFFFFFu);
+    // Buffers start at the tile (tile_base): 32-bit offsets for any matrix
+    // size. Weight columns past the matrix read past the buffer: zeros, no
+    // fault. Activation rows are clamped or gathered (act_row): in bounds.
+    const uint32_t rb = act_base(ds, m0);
+    const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
+    const rsrc_t r_w = make_rsrc(ds.w + (uint64_t)n0 * row_bytes, min(BN, ds.n - n0) * row_bytes);
+    const rsrc_t r_sx =
+        make_rsrc(reinterpret_cast<const uint8_t*>(ds.xds) + (uint64_t)rb * rec_bytes, 0xFFFFFFFFu);
     // Staged activations: piece 256u + tid is chunk tid%8 of row 32u + tid/8
     // (LDS + 4096u); LDS chunk c of row r holds logical chunk c ^ ((r/2)%8).
     // Sx: half tid%2 of row tid/2 (threads below 2 BM).
     const uint32_t ra = tid >> 3, ca = tid & 7u;
     uint32_t g_act[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + 16u * ca;
+    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * ca;
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
-    const uint32_t g_sx = act_row(ds, m0 + (tid >> 1)) * rec_bytes + 16u * (tid & 1u);
+    const uint32_t g_sx = (act_row(ds, m0 + (tid >> 1)) - rb) * rec_bytes + 16u * (tid & 1u);
     // Weights go straight to registers (no other wave reads a wave's
     // columns): lane (l32, h) of n-tile j loads, per stage, half h of the 32
     // quant bytes of column 64w + 32j + l32, and that column's 16-byte
@@ -286,7 +295,7 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         col[j] = 64u * w + 32u * j + l32;
-        g_h[j] = (n0 + col[j]) * row_bytes;
+        g_h[j] = col[j] * row_bytes;
         g_q[j] = g_h[j] + 16u + 16u * h;
     }
     const uint32_t nst = 4u * (sb1 - sb0);
@@ -452,6 +461,8 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 
 template <int MT>
 RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds);
+template <int MT>
+RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds);
 
 // One (32 MT)x256 tile (and one split-K range): the descriptor made uniform,
 // the tile decoded, and the rows computed by the body of as many 32-row tiles
@@ -474,7 +485,8 @@ RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
     auto run = [&](auto mt) {
         constexpr int M = decltype(mt)::value;
         if constexpr (TY == TY_Q4K) mmqh_q4k_rows<M>(ds, m0, n0, ks, lds);
-        else mmqh_q6k_rows<M>(ds, m0, n0, ks, lds);
+        else if constexpr (TY == TY_Q6K) mmqh_q6k_rows<M>(ds, m0, n0, ks, lds);
+        else mmqh_q80_rows<M>(ds, m0, n0, ks, lds);
     };
     if constexpr (MT >= 4) {
         if (sub >= 4u) return run(std::integral_constant<int, 4>{});
@@ -514,21 +526,24 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const uint32_t nsb = ds.k / 256u;
     const uint32_t sb0 = ks * ds.sb_per_split;
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
-    const uint32_t row_bytes = nsb * 210u;  // a multiple of 4 (nsb is even)
+    const uint32_t row_bytes = nsb * 210u;  // 2 mod 4 for an odd nsb
 
-    // The weights' buffer starts at the dword at or below ds.w (2-byte aligned);
-    // sh0 = the bytes between. Columns past the matrix read zeros.
-    const uintptr_t wa = reinterpret_cast<uintptr_t>(ds.w);
+    // The weights' buffer starts at the dword at or below the tile's first
+    // column (2-byte aligned); sh0 = the bytes between. Columns start 0 or 2
+    // bytes past a dword, super-blocks too: the 16-byte pieces are read with
+    // unaligned loads. Columns past the matrix read zeros.
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(ds.w + (uint64_t)n0 * row_bytes);
     const uint32_t sh0 = (uint32_t)(wa & 3u);
-    const rsrc_t r_act = make_rsrc(ds.xq, 0xFFFFFFFFu);
-    const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), ds.n * row_bytes + sh0);
+    const uint32_t rb = act_base(ds, m0);
+    const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
+    const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), min(BN, ds.n - n0) * row_bytes + sh0);
     const uint32_t ra = tid >> 3, ca = tid & 7u;
     // activations: the Q4_K tile's staging, but the stage's logical chunks 4-7
     // (group B) sit 128 bytes after chunks 0-3 (group A) in the f16 row
     uint32_t g_act[MT];
     const uint32_t cofs = 16u * ca + (ca >= 4u ? 64u : 0u);
 #pragma unroll
-    for (int u = 0; u < MT; u++) g_act[u] = act_row(ds, m0 + ra + 32u * u) * ds.ldq + cofs;
+    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + cofs;
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
     // Weights straight to registers: lane (l32, h) of n-tile j loads, per
     // stage, positions [16h, 16h + 16) of the ql and qh pieces of column
@@ -538,7 +553,7 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         col[j] = 64u * w + 32u * j + l32;
-        g_c[j] = (n0 + col[j]) * row_bytes + 16u * h;
+        g_c[j] = col[j] * row_bytes + 16u * h;
     }
     const uint32_t nst = 4u * (sb1 - sb0);
 
@@ -700,3 +715,181 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, TY_Q6K, 4, 2)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m32, TY_Q6K, 1, 3)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m64, TY_Q6K, 2, 2)
+
+// ---------------------------------------------------------------- Q8_0
+//
+// A Q8_0 block (src/dequant.rs:220-226) is an f16 d and 32 int8 codes:
+// w = d * q. The weight operand is f16(q * d), rounded once from an exact
+// product: the code byte, its sign bit flipped (q + 128), is permuted into
+// the mantissa of an f16 1024.0 (1024 + q + 128), an exact add of -1152
+// leaves q, and one multiply by the f16 pair (d, d) rounds. A 64-k stage is
+// two blocks (e = 0, 1); lane half h holds codes [16h, 16h + 16) of each, so
+// step t = 2e + s2 takes codes 32e + 16h + 8 s2 + [0, 8), the activations'
+// logical chunk 4e + 2h + s2, as for Q4_K. Blocks are 34 bytes: the pieces
+// are 2-byte aligned, read with unaligned buffer loads. Split-K ranges count
+// in units of 256 weights (8 blocks, four stages), as for the K-quants.
+
+namespace mmqh {
+// f16 pairs f16(q * d) of one code dword v (bytes q0..q3, signs flipped by
+// the caller: v ^ 0x80808080) in the activations' (q0, q2), (q1, q3) order
+RFXQ_DEV u2_t q80_codes_f16(uint32_t v, h2_t dv, uint32_t mg) {
+    const h2_t off = h2_t{(half_t)-1152.0f, (half_t)-1152.0f};
+    h2_t a = as_h2(__builtin_amdgcn_perm(mg, v, 0x04020400u)) + off;
+    h2_t b = as_h2(__builtin_amdgcn_perm(mg, v, 0x04030401u)) + off;
+    asm("" : "+v"(a), "+v"(b));  // keep the exact adds and the rounding multiplies apart (no fma)
+    return u2_t{h2_bits(a * dv), h2_bits(b * dv)};
+}
+}  // namespace mmqh
+
+// One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q8_0 weights:
+// the Q4_K tile's activation staging and MFMA schedule, with Q8_0 operands.
+template <int MT>
+RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+    using namespace mmqh;
+    constexpr uint32_t kAct = Tile<MT>::kAct;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsb = ds.k / 256u;
+    const uint32_t sb0 = ks * ds.sb_per_split;
+    const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
+    const uint32_t row_bytes = nsb * 272u;
+
+    // weights: the dword at or below the tile's first column (2-byte aligned)
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(ds.w + (uint64_t)n0 * row_bytes);
+    const uint32_t sh0 = (uint32_t)(wa & 3u);
+    const uint32_t rb = act_base(ds, m0);
+    const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
+    const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), min(BN, ds.n - n0) * row_bytes + sh0);
+    const uint32_t ra = tid >> 3, ca = tid & 7u;
+    uint32_t g_act[MT];
+#pragma unroll
+    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * ca;
+    const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
+    // lane (l32, h) of n-tile j: column 64w + 32j + l32, codes [16h, +16) of
+    // each block, and each block's d
+    uint32_t g_c[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) g_c[j] = (64u * w + 32u * j + l32) * row_bytes + sh0;
+    const uint32_t nst = 4u * (sb1 - sb0);
+
+    u4_t sa[MT], qn[2][2];
+    uint32_t dn[2][2];
+    auto load_act = [&](uint32_t st) {
+        const uint32_t sl = min(st, nst - 1u);
+        const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
+#pragma unroll
+        for (int u = 0; u < MT; u++)
+            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 128u * g, 0);
+    };
+    auto load_w = [&](uint32_t st) {
+        const uint32_t sl = min(st, nst - 1u);
+        const uint32_t blk = 8u * sb0 + 2u * sl;  // the stage's first block in the row
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t o = 34u * (blk + e);
+                qn[j][e] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], o + 2u + 16u * h, 0);
+                dn[j][e] = __builtin_amdgcn_raw_buffer_load_b16(r_w, g_c[j], o, 0);
+            }
+    };
+    auto store_act = [&](uint32_t st) {
+        uint8_t* S = lds + (st & 1u) * kAct;
+#pragma unroll
+        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
+    };
+
+    v16f_t acc[MT][2];
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v16f_t{};
+    uint32_t a_act[2][2];
+#pragma unroll
+    for (int e = 0; e < 2; e++)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) a_act[e][s2] = l32 * 8u + ((4u * e + 2u * h + s2) ^ ((l32 >> 1) & 7u));
+    uint32_t mg = 0x64646464u, sgn = 0x80808080u;
+    asm("" : "+v"(mg), "+v"(sgn));
+
+    if (nst > 0u) {
+        load_w(0u);
+        load_act(0u);
+        store_act(0u);
+    }
+    __syncthreads();
+    for (uint32_t st = 0; st < nst; st++) {
+        u4_t q[2][2];
+        h2_t dv[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                q[j][e] = qn[j][e] ^ u4_t{sgn, sgn, sgn, sgn};
+                dv[j][e] = as_h2(splat16<0>(dn[j][e]));
+            }
+        load_w(st + 1u);
+        load_act(st + 1u);
+        const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
+        auto wop = [&](int t, int j) {
+            const int e = t >> 1, s2 = t & 1;
+            const u2_t lo = q80_codes_f16(q[j][e][2 * s2], dv[j][e], mg);
+            const u2_t hi = q80_codes_f16(q[j][e][2 * s2 + 1], dv[j][e], mg);
+            return u4_t{lo.x, lo.y, hi.x, hi.y};
+        };
+        u4_t Xc[MT], Wc[2];
+#pragma unroll
+        for (int i = 0; i < MT; i++) Xc[i] = S16[256u * i + a_act[0][0]];
+        Wc[0] = wop(0, 0);
+        Wc[1] = wop(0, 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            u4_t Xn[MT], Wn[2];
+            if (t < 3) {
+                const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
+#pragma unroll
+                for (int i = 0; i < MT; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
+                Wn[0] = wop(t + 1, 0);
+                Wn[1] = wop(t + 1, 1);
+            }
+#pragma unroll
+            for (int i = 0; i < MT; i++) {
+                acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
+                acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
+            }
+            if (t < 3) {
+#pragma unroll
+                for (int u = 0; u < MT; u++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < MT; u++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < MT; i++) Xc[i] = Xn[i];
+                Wc[0] = Wn[0];
+                Wc[1] = Wn[1];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        store_act(st + 1u);
+        __syncthreads();
+    }
+
+    float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
+    const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const uint32_t row = m0 + 32u * i + l32;
+        const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) store_tile(ds, y, row, n0 + 64u * w + 32u * j, h, acc[i][j], scale, vec);
+    }
+}
+
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0, TY_Q8_0, 4, 2)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0_m32, TY_Q8_0, 1, 4)
+RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0_m64, TY_Q8_0, 2, 3)

@@ -144,7 +144,7 @@ struct Ctx {
     hipModule_t mod = nullptr;
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr, reduce_multi = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
-    hipFunction_t mmqh[2][3] = {};  // [type][128-row, 32-row, 64-row tiles]
+    hipFunction_t mmqh[3][3] = {};  // [Q4_K, Q6_K, Q8_0][128-row, 32-row, 64-row tiles]
     hipFunction_t act_f16 = nullptr, act_f16_multi = nullptr, act_f16_wg = nullptr, act_f16_multi_wg = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
@@ -152,6 +152,7 @@ struct Ctx {
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
     void* scratch = nullptr;  // this device's fixed scratch array (rfxq_gemm_no_alloc)
+    hipError_t scratch_err = hipSuccess;  // why `scratch` is NULL on a loaded device
     // device area for per-call descriptor tables (grow-only, separate from ws)
     void* tab = nullptr;
     uint64_t tab_bytes = 0;
@@ -215,6 +216,9 @@ int load_ctx(int device, Ctx** out) {
         {&c->mmqh[1][1], "rfxq_mmqh_q6k_m32"},
         {&c->mmqh[0][2], "rfxq_mmqh_q4k_m64"},
         {&c->mmqh[1][2], "rfxq_mmqh_q6k_m64"},
+        {&c->mmqh[2][0], "rfxq_mmqh_q8_0"},
+        {&c->mmqh[2][1], "rfxq_mmqh_q8_0_m32"},
+        {&c->mmqh[2][2], "rfxq_mmqh_q8_0_m64"},
         {&c->act_f16, "rfxq_act_f16"},
         {&c->act_f16_multi, "rfxq_act_f16_multi"},
         {&c->act_f16_wg, "rfxq_act_f16_wg"},
@@ -239,9 +243,10 @@ int load_ctx(int device, Ctx** out) {
         if (e != hipSuccess)
             return fail(RFXQ_ERR_GPU, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
     }
-    // the fixed scratch of rfxq_gemm_no_alloc, resolved now (the device is current)
-    if (hipError_t e = rfxq_scratch::setup(device, &c->scratch); e != hipSuccess)
-        return fail(RFXQ_ERR_GPU, "scratch symbol address on device %d: %s", device, hipGetErrorString(e));
+    // the fixed scratch of rfxq_gemm_no_alloc, resolved now (the device is
+    // current); a failure disables only that entry point, which reports it
+    c->scratch_err = rfxq_scratch::setup(device, &c->scratch);
+    if (c->scratch_err != hipSuccess) c->scratch = nullptr;
     *out = c.get();
     g_ctx[device] = std::move(c);
     return RFXQ_OK;
@@ -579,10 +584,11 @@ void gemv_shape(GemvItem* it, uint32_t k) {
 // leave most CUs idle while it runs (measured on a 139 MB launch: 34.6 us
 // against 44.0 us with 1062 workgroups). Only launches of more than 512 KB
 // per resident workgroup take whole waves of workgroups instead.
-uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) {
+uint32_t gemv_grid(const Ctx* c, const GemvItem* v, size_t n) {
     uint64_t total_iters = 0, total_bytes = 0;
     uint32_t kmax = 0;
-    for (const auto& it : v) {
+    for (size_t i = 0; i < n; i++) {
+        const GemvItem& it = v[i];
         total_iters += it.iters;
         total_bytes += it.iters * it.iter_bytes;
         kmax = std::max(kmax, it.d.k);
@@ -599,6 +605,7 @@ uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) {
     }
     return (uint32_t)std::max<uint64_t>(1u, std::min<uint64_t>(g, total_iters));
 }
+uint32_t gemv_grid(const Ctx* c, const std::vector<GemvItem>& v) { return gemv_grid(c, v.data(), v.size()); }
 
 // LDS bytes for a launch whose workgroups hold at most `max_iters` iterations
 // of one GEMV: a row buffer (results and several-pass partials; a multiple of
@@ -621,26 +628,36 @@ int gemv_lds(const std::vector<GemvItem>& v, const std::vector<uint32_t>& max_it
 // range table): over up to kGemvInline descriptors passed inline (`table`
 // NULL), or over a table the device writes (in the order of `v`, whose
 // shapes it shares).
-int gemv_launch_counted(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* table, hipStream_t stream) {
+// (No host allocation: rfxq_gemm_no_alloc launches through here.)
+int gemv_launch_counted(Ctx* c, const GemvItem* v, size_t n, const GemvDesc* table, hipStream_t stream) {
+    if (!table && n > kGemvInline) return fail(RFXQ_ERR_OTHER, "gemv: %zu inline descriptors", n);
     uint64_t total = 0;
-    for (const auto& it : v) total += it.iters;
-    const uint32_t grid = gemv_grid(c, v);
+    for (size_t i = 0; i < n; i++) total += v[i].iters;
+    const uint32_t grid = gemv_grid(c, v, n);
     const uint32_t per_wg = (uint32_t)((total + grid - 1u) / grid);  // no range holds more iterations
-    std::vector<uint32_t> max_iters(v.size());
-    for (size_t i = 0; i < v.size(); i++) max_iters[i] = std::min(per_wg, v[i].iters);
+    // LDS as gemv_lds, each workgroup holding at most per_wg iterations of a GEMV
+    uint32_t part = 0, kmax = 0;
+    for (size_t i = 0; i < n; i++) {
+        part = std::max(part, std::min(per_wg, v[i].iters) * v[i].rows_iter);
+        kmax = std::max(kmax, v[i].d.k);
+    }
     GemvArgs a;
     std::memset(&a, 0, sizeof a);
-    uint32_t lds;
-    if (int rc = gemv_lds(v, max_iters, &a.part_floats, &lds)) return rc;
-    a.ndesc = (uint32_t)v.size();
+    a.part_floats = (std::max(part, 4u) + 3u) & ~3u;
+    const uint32_t lds = a.part_floats * 4u + kmax * 2u + kmax / 4u;
+    if (lds > kMaxLds) return fail(RFXQ_ERR_OTHER, "gemv: launch needs %u bytes of LDS", lds);
+    a.ndesc = (uint32_t)n;
     a.table = table;
     // one iteration count for every descriptor: the kernel need not read them
-    a.iters_each = v.empty() ? 0u : v[0].iters;
-    for (const auto& it : v)
-        if (it.iters != a.iters_each) a.iters_each = 0u;
+    a.iters_each = n ? v[0].iters : 0u;
+    for (size_t i = 0; i < n; i++)
+        if (v[i].iters != a.iters_each) a.iters_each = 0u;
     if (!table)
-        for (size_t i = 0; i < v.size(); i++) a.inl[i] = v[i].d;
+        for (size_t i = 0; i < n; i++) a.inl[i] = v[i].d;
     return launch(c->gemv, grid, lds, stream, &a, sizeof a, "rfxq_gemv launch");
+}
+int gemv_launch_counted(Ctx* c, const std::vector<GemvItem>& v, const GemvDesc* table, hipStream_t stream) {
+    return gemv_launch_counted(c, v.data(), v.size(), table, stream);
 }
 
 int gemv_launch_inline(Ctx* c, const std::vector<GemvItem>& v, hipStream_t stream) {
@@ -782,29 +799,31 @@ void gemv_split_bytes(const std::vector<GemvItem>& v, uint32_t grid, std::vector
 
 // ------------------------------------------------------------------ MMQ planning
 
-// Q4_K and Q6_K prefill GEMMs run on the f16-activation kernels
-// (rfxq_mmqh_q4k, rfxq_mmqh_q6k: f16 activations scaled per row, weights as f16
-// operands, f32 accumulation in the matrix core) unless REFLEX_MMQ_F16=0
-// selects the int8 MMQ kernels (Q8_1 activations, per-32 int32 block dots).
-// Q8_0 always takes the int8 kernels.
+// Prefill GEMMs run on the f16-activation kernels (rfxq_mmqh_q4k / _q6k /
+// _q8_0: f16 activations scaled per row, weights as f16 operands, f32
+// accumulation in the matrix core) unless REFLEX_MMQ_F16=0 selects the int8
+// MMQ kernels (Q8_1 activations, per-32 int32 block dots). The int8 format's
+// own error exceeds the 1e-3 bound at some shapes, so the default never falls
+// back to it: a GEMM the f16 kernels cannot run takes the GEMV path.
 constexpr uint32_t kMmqThreads = 256;  // every MMQ kernel's workgroup
 bool mmq_f16() { return opt().mmq_f16 != 0; }
 
-bool f16_capable(uint32_t ty, uint64_t k, uint64_t n, uint64_t rows) {
-    const uint64_t nsb = k / 256u;
-    uint64_t bb;
-    if (ty == RFXQ_TYPE_Q4_K) bb = 144u;
-    else if (ty == RFXQ_TYPE_Q6_K && nsb % 2u == 0u) bb = 210u;
-    else return false;
-    const uint64_t lim = 0xF0000000ull;  // every buffer offset of the kernel's loads fits in 32 bits
-    return (n + 256u) * nsb * bb < lim && (rows + 128u) * k * 2u < lim;
+// The f16 kernels run any Q4_K, Q6_K or Q8_0 GEMM with k a multiple of 256:
+// their buffer resources start at the tile (weights at its first column,
+// activations at its first row), so offsets fit in 32 bits for any size. A
+// gathered GEMM (MoE expert groups: `gather_src` source rows, 0 = not
+// gathered) addresses every source row from the buffer start, so its f16
+// activations must stay below the limit.
+bool f16_capable(uint32_t ty, uint64_t k, uint64_t gather_src) {
+    if (ty != RFXQ_TYPE_Q4_K && ty != RFXQ_TYPE_Q6_K && ty != RFXQ_TYPE_Q8_0) return false;
+    if (k == 0 || k % 256u) return false;
+    const uint64_t lim = 0xF0000000ull;
+    return gather_src * k * 2u < lim;
 }
 
-// an f16 kernel for this GEMM: f16 mode, Q4_K or Q6_K (the Q6_K kernel needs
-// an even number of super-blocks per row, so that rows start 4-byte aligned),
-// and every buffer offset of the kernel's loads fits in 32 bits
-bool f16_kernel(const rfxq_weight* w, uint32_t rows) {
-    return mmq_f16() && f16_capable(w->ggml_type, w->in_features, w->out_features, rows);
+// an f16 kernel for a gathered GEMM of `src_rows` source rows in f16 mode
+bool f16_kernel(const rfxq_weight* w, uint32_t src_rows) {
+    return mmq_f16() && f16_capable(w->ggml_type, w->in_features, src_rows);
 }
 
 // weight columns per workgroup tile: 256 on the f16 kernels, 128 on the int8 ones
@@ -814,14 +833,13 @@ uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 // the MMA kernel and its split-K, kernels.rs:628-713 quant_mma_splits /
 // block_rows / max_rows and :2144-2169, re-derived for MI355X):
 // - one GEMV per row (PATH_GEMV_ROWS) for a single row, with the MMA path off
-//   (REFLEX_QUANT_MMA=0), above REFLEX_QUANT_MMA_MAX_ROWS, for Q8_0 in f16
-//   mode (no f16-activation Q8_0 kernel; the int8 format's error floor
-//   exceeds the north star's bound), with in_features not a multiple of 256,
-//   and up to REFLEX_QUANT_FUSED_MAX_ROWS rows (default 16) on the int8 path,
-//   up to kGemvRowsMax of them on the f16 path (a GEMV per row re-reads the
-//   weights, cheaper than the few-row tiles' launch pair below 5 rows);
-// - otherwise the f16-activation kernels (PATH_MMQ_F16: Q4_K, and Q6_K with an
-//   even super-block count per row): 32-row tiles up to 32 rows (the fused
+//   (REFLEX_QUANT_MMA=0), above REFLEX_QUANT_MMA_MAX_ROWS, with in_features
+//   not a multiple of 256, and up to REFLEX_QUANT_FUSED_MAX_ROWS rows
+//   (default 16) on the int8 path, up to kGemvRowsMax of them on the f16
+//   path (a GEMV per row re-reads the weights, cheaper than the few-row
+//   tiles' launch pair below 5 rows);
+// - otherwise the f16-activation kernels (PATH_MMQ_F16: Q4_K, Q6_K and Q8_0,
+//   the default): 32-row tiles up to 32 rows (the fused
 //   few-row form: each weight read once for all rows), 64-row tiles up to
 //   64, 128-row tiles above,
 //   or the int8 kernels (PATH_MMQ_INT8; 64-row tiles with
@@ -887,10 +905,10 @@ rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows,
     rfxq_gemm_policy p;
     std::memset(&p, 0, sizeof p);
     p.splits = 1;
-    const bool f16 = o.mmq_f16 && k % 256u == 0 && f16_capable(ty, k, n, rows);
+    const bool f16 = o.mmq_f16 && f16_capable(ty, k, 0);
     const bool gemv = rows <= 1 || !o.quant_mma || (o.quant_mma_max_rows && rows > o.quant_mma_max_rows) ||
                       (rows <= o.fused_max_rows && (!f16 || rows <= kGemvRowsMax)) || k % 256u != 0 ||
-                      (ty == RFXQ_TYPE_Q8_0 && o.mmq_f16);
+                      (o.mmq_f16 && !f16);
     if (gemv) {
         p.path = PATH_GEMV_ROWS;
         return p;
@@ -1079,7 +1097,7 @@ int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const 
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && !dots && ty != RFXQ_TYPE_Q8_0) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : tile_m == 64u ? 2 : 0];
+    if (f16 && !dots) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : tile_m == 64u ? 2 : 0];
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch", kMmqThreads);
 }
 
@@ -1749,9 +1767,12 @@ int rfxq_gemm_no_alloc(const float* x, uint64_t x_len, const rfxq_weight* w, uin
         auto it = g_ctx.find(dev);
         if (it != g_ctx.end()) c = it->second.get();
     }
-    if (!c || !c->scratch)
+    if (!c)
         return fail(RFXQ_ERR_INVALID_INPUT, "gemm_no_alloc: device %d is not initialised; call rfxq_init(%d) first",
                     dev, dev);
+    if (!c->scratch)
+        return fail(RFXQ_ERR_GPU, "gemm_no_alloc: the fixed scratch array of device %d is unavailable: %s", dev,
+                    hipGetErrorString(c->scratch_err));
     rfxq_options o;
     if (int rc = get_options(&o)) return rc;
     if (rows == 1 ||
@@ -1766,7 +1787,7 @@ int rfxq_gemm_no_alloc(const float* x, uint64_t x_len, const rfxq_weight* w, uin
                 if (int rc = make_gemv_item(x + (uint64_t)(r0 + j) * w->in_features, w,
                                             y + (uint64_t)(r0 + j) * w->out_features, &v[j]))
                     return rc;
-            if (int rc = gemv_launch_counted(c, std::vector<GemvItem>(v, v + cnt), nullptr, stream)) return rc;
+            if (int rc = gemv_launch_counted(c, v, cnt, nullptr, stream)) return rc;
         }
         return ok();
     }
@@ -1944,7 +1965,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_q8_1_item& it = items[i];
         const uint32_t k = it.w->in_features;
-        const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, it.w->out_features, rows);
+        const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, 0);
         const uint32_t tile_m = f16 ? (rows <= 32u ? 32u : kMmqBM) : o.quant_mma_tile == 64u ? 64u : kMmqBM;
         const uint32_t t = type_index(it.w->ggml_type) + 3u * group_variant(f16, tile_m);
         MmqDesc d;
@@ -2312,7 +2333,10 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         return moe_grouped_device(x, rows, hidden, nullptr, ridx.data(), wsc.data(), expert_count, top_k, normalize,
                                   weight_scale, gate, up, down, out, stream);
     }
-    if (rows <= kMoeGemvRows) {
+    // f16 mode with token activations past the f16 kernels' gathered-row
+    // limit: every pair runs as GEMVs too (the int8 format would miss 1e-3)
+    const bool f16 = f16_kernel(&g0, rows) && f16_kernel(&u0, rows) && f16_kernel(&d0, P);
+    if (rows <= kMoeGemvRows || (mmq_f16() && !f16)) {
         const uint64_t g_gate = 0;
         const uint64_t g_up = g_gate + align256((uint64_t)P * ffn * 4u);
         const uint64_t g_down = g_up + align256((uint64_t)P * ffn * 4u);
@@ -2358,8 +2382,7 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
     }
 
     // workspace layout: x and the SiLU·up rows in the layouts the expert
-    // GEMMs read (f16 kernels for Q4_K / Q6_K experts, int8 otherwise)
-    const bool f16 = f16_kernel(&g0, rows) && f16_kernel(&u0, rows) && f16_kernel(&d0, P);
+    // GEMMs read (f16 kernels, or int8 with REFLEX_MMQ_F16=0)
     const ActLayout Lx = act_layout_sel(rows, hidden, !f16, f16);
     const ActLayout Ls = act_layout_sel(P, ffn, !f16, f16);
     const uint64_t o_x = 0;
@@ -2561,6 +2584,9 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
     // workspace: quantized tokens, gate/up outputs, quantized SiLU·up, down
     // outputs, routing, grouping and descriptor tables
     const bool f16 = f16_kernel(&g0, rows) && f16_kernel(&u0, rows) && f16_kernel(&d0, P);
+    if (mmq_f16() && !f16)
+        return fail(RFXQ_ERR_OTHER, "moe_ffn_grouped_device: %u tokens x %u hidden exceed the f16 kernels' 4 GiB "
+                    "gathered-activation range (use rfxq_moe_ffn_grouped)", rows, hidden);
     const ActLayout Lx = act_layout_sel(rows, hidden, !f16, f16);
     const ActLayout Ls = act_layout_sel(P, ffn, !f16, f16);
     const uint64_t o_x = 0;

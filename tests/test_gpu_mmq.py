@@ -1,6 +1,6 @@
 """GPU parity of the prefill GEMM path.
 
-Default path (f16 activations; rfxq_act_f16 + rfxq_mmqh_q4k / rfxq_mmqh_q6k):
+Default path (f16 activations; rfxq_act_f16 + rfxq_mmqh_q4k / _q6k / _q8_0):
 the activation stage is bit-exact with the oracle's act_f16; every GEMM output
 is within the north star's literal 1e-3 (max error over a row normalised by
 the row's L2 norm) of dequant.rs + f64 host matmul, at every BASELINE config 3
@@ -216,20 +216,73 @@ def test_gemm_row_counts(rq, orc, ty, m):
     _check_gemm(rq, orc, ty, m, n, k, w_np, x)
 
 
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("m,n,k", [(33, 200, 256), (129, 1000, 2048), (300, 136, 4096), (64, 130, 768),
-                                   (513, 3072, 1024)])
+                                   (513, 3072, 1024), (200, 520, 1280)])
 def test_gemm_ragged_shapes(rq, orc, ty, m, n, k):
     """Ragged M and N, K from one super-block up (Q6_K rows with an odd
-    super-block count, k = 256 and 768, run on the int8 kernel and are held to
-    its format model only)."""
+    super-block count, k = 256, 768 and 1280, start 2 bytes past a dword),
+    held to the literal 1e-3 against dequant + f64 and to the kernel's model."""
     w_np = synth.weights(ty, n, k, 90 + m)
     x = synth.activations(m * k, 91 + m).reshape(m, k)
-    if ty == Q6K and (k // 256) % 2:
-        y = rq.gemm(_dev(x), _weight(rq, ty, w_np, n, k), m).cpu().numpy().reshape(m, n)
-        assert orc.rel_err_row_l2(y, orc.mmq_model_reference(ty, w_np, n, k, x)) < 3e-5
-    else:
-        _check_gemm(rq, orc, ty, m, n, k, w_np, x)
+    _check_gemm(rq, orc, ty, m, n, k, w_np, x)
+
+
+@pytest.mark.parametrize("k", [256, 768, 1280])
+@pytest.mark.parametrize("m", [5, 40, 100, 512])
+def test_gemm_q6k_odd_superblocks(rq, orc, m, k):
+    """Q6_K with an odd super-block count per row (Q4_K_M MoE down projections:
+    ffn 768) on the f16 kernels at every tile height."""
+    n = 2048
+    assert rq.gemm_policy(Q6K, k, n, m)["path"] == rq.PATH_MMQ_F16
+    w_np = synth.weights(Q6K, n, k, 700 + m + k)
+    x = synth.activations(m * k, 701 + m + k).reshape(m, k)
+    _check_gemm(rq, orc, Q6K, m, n, k, w_np, x)
+
+
+@pytest.mark.parametrize("m", [2, 5, 32, 512])
+def test_gemm_q8_0_config1_matrix(rq, orc, m):
+    """Q8_0 prefill on BASELINE config 1's 1024 x 1024 matrix: GEMV rows at 2,
+    the f16 tiles from 5 rows."""
+    n = k = 1024
+    w_np = synth.weights(Q8_0, n, k, 800 + m)
+    x = synth.activations(m * k, 801 + m).reshape(m, k)
+    _check_gemm(rq, orc, Q8_0, m, n, k, w_np, x)
+
+
+def test_gemm_q8_0_large(rq, orc):
+    """Q8_0 at an 8B-class shape, M = 512, 64 sampled rows."""
+    n, k, m = 4096, 4096, 512
+    w_np = synth.weights(Q8_0, n, k, 810)
+    x = synth.activations(m * k, 811).reshape(m, k)
+    rows = np.sort(np.random.default_rng(812).choice(m, 64, replace=False))
+    _check_gemm(rq, orc, Q8_0, m, n, k, w_np, x, rows)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
+def test_gemm_weight_past_4gib(rq, orc, ty):
+    """A weight whose last columns lie more than 4 GiB past its start (the
+    kernels' buffer resources start at each column tile): zero blocks up to
+    the last 300 columns, which hold random blocks and are checked against the
+    reference; every zero column must come out exactly 0."""
+    k, m = 256, 40
+    qk, bb = {Q4K: (256, 144), Q6K: (256, 210), Q8_0: (32, 34)}[ty]
+    rb = k // qk * bb
+    tail = 300
+    n = (4 * 2**30 + 64 * 2**20) // rb + tail
+    w_tail = synth.weights(ty, tail, k, 820 + ty)
+    buf = torch.zeros(n * rb, dtype=torch.uint8, device=DEV)
+    buf[(n - tail) * rb:] = _dev(w_tail)
+    w = rq.Weight(rq.GgmlType(ty), buf, [k, n])
+    assert rq.gemm_policy(ty, k, n, m)["path"] == rq.PATH_MMQ_F16
+    x = synth.activations(m * k, 821).reshape(m, k)
+    y = rq.gemm(_dev(x), w, m).reshape(m, n)
+    assert int(torch.count_nonzero(y[:, :n - tail])) == 0
+    yt = y[:, n - tail:].cpu().numpy()
+    del y, buf
+    e = orc.rel_err_row_l2(yt, orc.reference_gemm(ty, w_tail, tail, k, x))
+    print(f"type {ty}: columns past 4 GiB, row-L2 error {e:.2e}")
+    assert e < TOL
 
 
 def test_gemm_rows_independent_and_deterministic(rq, orc, opts):
@@ -246,7 +299,7 @@ def test_gemm_rows_independent_and_deterministic(rq, orc, opts):
     assert np.array_equal(y1[:130], y2)
 
 
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 def test_gemm_split_k_matches_unsplit(rq, orc, opts, ty):
     n, k, m = 512, 4096, 64
     w_np = synth.weights(ty, n, k, 12)
@@ -282,7 +335,7 @@ def test_gemm_caller_workspace(rq, orc):
 
 def test_gemm_batch_and_plan_match_single_gemms(rq, orc, opts):
     """Grouped GEMMs (each activation brought into its layouts once, one launch
-    per weight type, Q8_0 rows as GEMVs) give the single-GEMM results bit for
+    per weight type) give the single-GEMM results bit for
     bit (split-K off on both sides; by default a group this small splits K)."""
     rows = 300
     shapes = [(Q4K, 768, 1024), (Q4K, 256, 1024), (Q6K, 256, 1024), (Q8_0, 512, 1024), (Q4K, 640, 2048)]
@@ -330,7 +383,7 @@ def test_gemm_batch_errors(rq):
         rq.gemm_batch([(x, w1, y), (x, w2, y)], 64)   # one x with two in_features
 
 
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("scale,offset", [(3000.0, 2500.0), (1e5, 0.0), (1e-6, 0.0)])
 def test_gemm_activation_range(rq, orc, ty, scale, offset):
     """Activations far from N(0,1) (SiLU·up outputs of MoE layers reach 1e5):

@@ -10,7 +10,7 @@ from reflex_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-Q4K = 12
+Q4K, Q6K = 12, 14
 DEV = "cuda:0"
 TOL = 1e-3   # the north star's bound (row-L2 normalised max error), for the layer's final output
 
@@ -211,6 +211,33 @@ def test_moe_ffn_grouped_device(rq, orc, tokens, experts, hidden, ffn, k):
     y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, experts, hidden, ffn, k, 800 + tokens)
     assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
     assert orc.rel_err_row_l2(y_d, ref) < TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 64, 512])
+def test_moe_q6k_down_projection(rq, orc, tokens):
+    """Q4_K_M-style experts: gate/up Q4_K, down Q6_K at ffn 768 (three
+    super-blocks per row, rows 2 bytes past a dword), host and device routing,
+    every token against the host reference at the literal 1e-3."""
+    experts, hidden, ffn, top_k, seed = 128, 2048, 768, 8, 950 + tokens
+    gate = synth.weights(Q4K, experts * ffn, hidden, seed)
+    up = synth.weights(Q4K, experts * ffn, hidden, seed + 1)
+    down = synth.weights(Q6K, experts * hidden, ffn, seed + 2)
+    x = _dev(synth.activations(tokens * hidden, seed + 3))
+    logits = synth.normals(seed + 4, tokens * experts).reshape(tokens, experts)
+    ws = (rq.Weight(rq.GgmlType.Q4K, _dev(gate), [hidden, ffn, experts]),
+          rq.Weight(rq.GgmlType.Q4K, _dev(up), [hidden, ffn, experts]),
+          rq.Weight(rq.GgmlType.Q6K, _dev(down), [ffn, hidden, experts]))
+    out_h = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, top_k, True, 1.0, *ws, out_h)
+    out_d = torch.empty(tokens * hidden, device=DEV)
+    rq.moe_ffn_grouped_device(x, tokens, hidden, _dev(logits), experts, top_k, True, 1.0, *ws, out_d)
+    routes = [orc.route_top_k(logits[t], top_k) for t in range(tokens)]
+    ref = orc.moe_ffn_grouped_reference(x.cpu().numpy().reshape(tokens, hidden), routes, gate, up, down, Q4K,
+                                        hidden, ffn, experts, down_ty=Q6K)
+    for name, o in (("host", out_h), ("device", out_d)):
+        e = orc.rel_err_row_l2(o.cpu().numpy().reshape(tokens, hidden), ref)
+        print(f"MoE {tokens} tokens, Q6_K down, {name} routing: row-L2 error {e:.2e}")
+        assert e < TOL
 
 
 @pytest.mark.parametrize("tokens,k", [(1, 8), (4, 8), (1, 1), (2, 1), (5, 8)])

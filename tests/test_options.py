@@ -112,11 +112,15 @@ def test_policy_paths(rq):
     with rq.options(mmq_f16=0):   # the int8 path keeps GEMVs up to fused_max_rows
         assert pol(Q4K, 1024, 2048, 16)["path"] == G
         assert pol(Q4K, 1024, 2048, 17)["path"] == I8
-    # the f16 kernels: Q4_K, and Q6_K with an even super-block count per row
-    assert pol(Q6K, 1024, 1024, 512)["path"] == F16
-    assert pol(Q6K, 768, 1024, 512)["path"] == I8
-    # Q8_0 has no f16 kernel: GEMVs in f16 mode, the int8 kernel otherwise
-    assert pol(Q8_0, 1024, 1024, 512)["path"] == G
+    # the f16 kernels take Q4_K, Q6_K (any super-block count per row) and Q8_0;
+    # the default never picks the int8 format, whose error exceeds 1e-3
+    for k in (256, 768, 1024, 1280):
+        assert pol(Q6K, k, 1024, 512)["path"] == F16
+    assert pol(Q8_0, 1024, 1024, 512)["path"] == F16
+    assert pol(Q8_0, 1024, 1024, 5)["path"] == F16
+    assert pol(Q8_0, 1024, 1024, 4)["path"] == G
+    # weights far past 4 GiB: the kernels' buffers start at each tile
+    assert pol(Q4K, 256, 40_000_000, 512)["path"] == F16
     with rq.options(mmq_f16=0):
         p = pol(Q8_0, 1024, 1024, 512)
         assert p["path"] == I8 and (p["tile_m"], p["tile_n"]) == (128, 128)

@@ -485,7 +485,7 @@ def _q6k_block(d, sc, q):
     return bytes(blk)
 
 
-@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 def test_mmqh_model_reference_exact_case(orc, ty):
     """Where every f16 rounding of the f16-operand model is exact (integer
     activations with row maxima in [256, 512): scale 1; power-of-two d and
@@ -503,8 +503,12 @@ def test_mmqh_model_reference_exact_case(orc, ty):
             m = rng.integers(0, 64, 8).tolist()
             blocks.append(_q4k_block(2.0 ** -4, 2.0 ** -5, sc, m, rng.integers(0, 16, 256).tolist(),
                                      rng.integers(0, 16, 256).tolist()))
-        else:
+        elif ty == Q6K:
             blocks.append(_q6k_block(2.0 ** -6, rng.integers(-15, 16, 16), rng.integers(0, 64, 256).tolist()))
+        else:   # eight Q8_0 blocks: power-of-two d (exact f16(q * d)), codes over all of int8
+            for _ in range(8):
+                d = 2.0 ** int(rng.integers(-9, -3))
+                blocks.append(bytes(f16b(d)) + rng.integers(-128, 128, 32).astype(np.int8).tobytes())
     w = np.frombuffer(b"".join(blocks), np.uint8).copy()
     x = rng.integers(-300, 301, (rows, k)).astype(np.float32)
     x[:, 7] = 300
