@@ -260,6 +260,14 @@ def main() -> int:
     if not args.quick:
         result["decode_8b"] = decode_8b_leg(rq, synth, torch, np, dev, timed)
         result["prefill"] = prefill_leg(rq, synth, torch, np, dev, timed)
+        # the metric's second half as top-level keys (the config 3 set)
+        pf = result["prefill"]["qwen3_06b_m512"]
+        result["prefill_tops"] = pf["tops"]
+        result["prefill_frac_int8_peak"] = pf["frac_int8_peak"]
+        result["prefill_frac_f16_peak"] = pf["frac_f16_peak"]
+        result["prefill_ms_per_step"] = pf["ms_per_step"]
+        result["prefill_kernel"] = "rfxq_mmqh_q4k (+ rfxq_mmqh_q6k for v_proj)"
+        result["q8_0"] = q8_0_leg(rq, synth, torch, np, dev, timed)
         result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
     torch.cuda.empty_cache()
     if not args.quick and not args.no_cpu:
@@ -340,6 +348,55 @@ def decode_8b_leg(rq, synth, torch, np, dev, timed):
         print(f"decode 8B {tag}: {ms * 1e3:.1f} us/step  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)",
               file=sys.stderr, flush=True)
         del plans, keep
+    return out
+
+
+def q8_0_leg(rq, synth, torch, np, dev, timed):
+    """Q8_0 weights: BASELINE config 1's 1024 x 1024 matrix at M=1 (one GEMV;
+    1.1 MB, so the figure is launch latency, not bandwidth: 64 rotated copies
+    keep it out of the L2) and at M=512, and one Qwen3-8B layer with every
+    projection in Q8_0 at M=512 (a Q8_0 model's prefill)."""
+    out = {}
+    n = k = 1024
+    copies = [rq.Weight.from_blocks(synth.Q8_0, synth.weights(synth.Q8_0, n, k, synth.seed_for(1, c, 0)), k, n,
+                                    device=dev) for c in range(64)]
+    x = torch.from_numpy(synth.activations(k, synth.seed_for(1, 0, 1))).to(dev)
+    y = torch.empty(n, device=dev)
+    ms = timed(lambda i: rq.gemv_to(x, copies[i % 64], y), 2000, 500)
+    nbytes = synth.weight_bytes(synth.Q8_0, n, k) + 4 * (n + k)
+    out["config1_gemv_m1"] = {"us_per_call": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                              "mb_per_call": round(nbytes / 1e6, 3)}
+    print(f"Q8_0 config 1 GEMV M=1: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
+    xs = torch.randn(512 * k, device=dev)
+    ys = torch.empty(512 * n, device=dev)
+    plan = rq.GemmPlan([(xs, copies[0], ys)], 512)
+    ms = timed(lambda i: plan.run(), 200, 50)
+    tops = 2 * 512 * n * k / (ms * 1e-3) / 1e12
+    out["config1_gemm_m512"] = {"us_per_call": round(ms * 1e3, 1), "tops": round(tops, 1)}
+    print(f"Q8_0 config 1 GEMM M=512: {ms * 1e3:.1f} us  {tops:.0f} TOPS", file=sys.stderr, flush=True)
+    del plan, copies
+    group = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o",
+             "gate_proj": "gu", "up_proj": "gu", "down_proj": "down"}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4343)
+    xs, items, keep = {}, [], []
+    for pi, (name, _, n, k) in enumerate(synth.QWEN3_8B_LAYER):
+        g = group[name]
+        if g not in xs:
+            xs[g] = torch.randn(512 * k, device=dev, generator=gen)
+        w = rq.Weight.from_blocks(synth.Q8_0, synth.weights(synth.Q8_0, n, k, synth.seed_for(4, 7, pi)), k, n,
+                                  device=dev)
+        keep.append(w)
+        items.append((xs[g], w, torch.empty(512 * n, device=dev)))
+    plan = rq.GemmPlan(items, 512)
+    ms = timed(lambda i: plan.run(), 40, 80)
+    ops = sum(2 * 512 * n * k for _, _, n, k in synth.QWEN3_8B_LAYER)
+    tops = ops / (ms * 1e-3) / 1e12
+    out["qwen3_8b_m512_1layer_q8_0"] = {"ms_per_step": round(ms, 3), "tops": round(tops, 1),
+                                        "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                        "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4)}
+    print(f"Q8_0 8B layer M=512: {ms:.3f} ms  {tops:.0f} TOPS", file=sys.stderr, flush=True)
+    del plan, items, keep
     return out
 
 

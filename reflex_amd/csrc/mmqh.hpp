@@ -65,7 +65,8 @@ struct Tile {
     static constexpr uint32_t BM = 32u * MT;
     static constexpr uint32_t kAct = BM * 128u;  // activation stage: BM rows x 64 f16
     static constexpr uint32_t kSx = BM * 32u;    // Q4_K: the super-block's Sx records of BM rows
-    static constexpr uint32_t kLds = 2u * kAct + kSx;
+    static constexpr uint32_t kScale = BM * 4u;  // the rows' scales 2^e (f32), for the stores
+    static constexpr uint32_t kLds = 2u * kAct + kSx + kScale;
 };
 static_assert(Tile<4>::kLds <= 81920, "two workgroups per CU");
 
@@ -151,26 +152,34 @@ RFXQ_DEV uint32_t act_row(const MmqDesc& ds, uint32_t r) {
 // (the host keeps those activations under 4 GiB).
 RFXQ_DEV uint32_t act_base(const MmqDesc& ds, uint32_t m0) { return ds.rows ? 0u : m0; }
 
-// y rows of one 32-row activation tile: acc[r] is weight column
-// 8*(r/4) + 4*h + r%4 of the 32-column tile starting at c_base
-RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t c_base, uint32_t h, const v16f_t& acc,
-                         float scale, bool vec) {
-    if (row >= ds.m) return;
-    float* yr = y + (uint64_t)row * ds.ldy;
+// The accumulator of a 32x32 output tile (mfma16: A = activations, B =
+// weights): lane (l32, h) holds weight column l32 and activation rows
+// 8 q4 + 4 h + r (q4, r in [0, 4)) as acc[4 q4 + r]. Stored as dwords: the
+// 32 lanes of a half write one row's 32 consecutive columns (128 contiguous
+// bytes per row and instruction; float4 stores of the transposed layout
+// touched 32 rows per instruction and cost ~16% of the 0.6B prefill set).
+// `row` = the tile's row 4h, `sc` = the LDS scales 2^e of rows row..row+27.
+RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col, const v16f_t& acc,
+                         const float* sc) {
+    if (col >= ds.n) return;
+    float* yc = y + col;
 #pragma unroll
     for (int q4 = 0; q4 < 4; q4++) {
-        const uint32_t c0 = c_base + 8u * q4 + 4u * h;
-        const float a0 = acc[4 * q4] * scale, a1 = acc[4 * q4 + 1] * scale;
-        const float a2 = acc[4 * q4 + 2] * scale, a3 = acc[4 * q4 + 3] * scale;
-        if (vec && c0 + 3u < ds.n) {
-            *reinterpret_cast<float4*>(yr + c0) = make_float4(a0, a1, a2, a3);
-        } else {
-            if (c0 < ds.n) yr[c0] = a0;
-            if (c0 + 1u < ds.n) yr[c0 + 1u] = a1;
-            if (c0 + 2u < ds.n) yr[c0 + 2u] = a2;
-            if (c0 + 3u < ds.n) yr[c0 + 3u] = a3;
+        const float4 s4 = *reinterpret_cast<const float4*>(sc + 8 * q4);
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t m = row + 8u * q4 + r;
+            if (m < ds.m) yc[(uint64_t)m * ds.ldy] = acc[4 * q4 + r] * sv[r];
         }
     }
+}
+
+// the rows' scales 2^e into LDS (read by store_tile); visible after the
+// first barrier of the tile loop
+RFXQ_DEV void stage_row_scales(const MmqDesc& ds, uint32_t m0, uint32_t bm, float* sc_lds) {
+    const uint32_t t = threadIdx.x;
+    if (t < bm) sc_lds[t] = m0 + t < ds.m ? ds.xrs[act_row(ds, m0 + t)] : 0.0f;
 }
 
 // Workgroup b of a g-workgroup launch as a tile index such that the tiles
@@ -182,8 +191,11 @@ RFXQ_DEV uint32_t xcd_tile(uint32_t b, uint32_t g) {
     return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + slot;
 }
 
-RFXQ_DEV v16f_t mfma16(u4_t a, u4_t b, v16f_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(a), as_h8(b), c, 0, 0, 0);
+// c += w . x over one 16-k step: w = weight operand (32 columns), x =
+// activation operand (32 rows); the result's rows are the activation rows
+// (A = x, B = w), see store_tile
+RFXQ_DEV v16f_t mfma16(u4_t w, u4_t x, v16f_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(x), as_h8(w), c, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------- Q6_K
@@ -349,6 +361,7 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
         load_act(0u);
         store_act(0u);
     }
+    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
     __syncthreads();
     MMQH_PROBE_BEGIN();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
@@ -449,14 +462,12 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
+    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
 #pragma unroll
-    for (int i = 0; i < MT; i++) {
-        const uint32_t row = m0 + 32u * i + l32;
-        const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) store_tile(ds, y, row, n0 + 64u * w + 32u * j, h, acc[i][j], scale, vec);
-    }
+        for (int j = 0; j < 2; j++)
+            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
 }
 
 template <int MT>
@@ -610,6 +621,7 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
         load_act(0u);
         store_act(0u);
     }
+    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
     __syncthreads();
     MMQH_PROBE_BEGIN();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
@@ -702,14 +714,12 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
+    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
 #pragma unroll
-    for (int i = 0; i < MT; i++) {
-        const uint32_t row = m0 + 32u * i + l32;
-        const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) store_tile(ds, y, row, n0 + 64u * w + 32u * j, h, acc[i][j], scale, vec);
-    }
+        for (int j = 0; j < 2; j++)
+            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
 }
 
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, TY_Q6K, 4, 2)
@@ -746,7 +756,7 @@ RFXQ_DEV u2_t q80_codes_f16(uint32_t v, h2_t dv, uint32_t mg) {
 template <int MT>
 RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
     using namespace mmqh;
-    constexpr uint32_t kAct = Tile<MT>::kAct;
+    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nsb = ds.k / 256u;
@@ -815,6 +825,7 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
         load_act(0u);
         store_act(0u);
     }
+    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
     __syncthreads();
     for (uint32_t st = 0; st < nst; st++) {
         u4_t q[2][2];
@@ -880,14 +891,12 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     }
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const bool vec = (ds.ldy & 3u) == 0u && ((uintptr_t)ds.y & 15u) == 0u;
+    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
 #pragma unroll
-    for (int i = 0; i < MT; i++) {
-        const uint32_t row = m0 + 32u * i + l32;
-        const float scale = row < ds.m ? ds.xrs[act_row(ds, row)] : 0.0f;
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) store_tile(ds, y, row, n0 + 64u * w + 32u * j, h, acc[i][j], scale, vec);
-    }
+        for (int j = 0; j < 2; j++)
+            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
 }
 
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0, TY_Q8_0, 4, 2)
