@@ -266,6 +266,7 @@ def main() -> int:
         result["prefill_frac_int8_peak"] = pf["frac_int8_peak"]
         result["prefill_frac_f16_peak"] = pf["frac_f16_peak"]
         result["prefill_ms_per_step"] = pf["ms_per_step"]
+        result["prefill_tops_with_act_pass"] = pf["tops_with_act_pass"]
         result["prefill_kernel"] = "rfxq_mmqh_q4k (+ rfxq_mmqh_q6k for v_proj)"
         result["q8_0"] = q8_0_leg(rq, synth, torch, np, dev, timed)
         result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
@@ -461,31 +462,41 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
         cfg = 3 if nl > 1 else 4
         group = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o",
                  "gate_proj": "gu", "up_proj": "gu", "down_proj": "down"}
-        items, keep = [], []
+        items, q_items, keep = [], [], []
         for li in range(nl):
-            xs = {}
+            xs, acts = {}, {}
             for pi, (name, ty, n, k) in enumerate(layer):
                 g = group[name]
                 if g not in xs:
                     xs[g] = torch.randn(512 * k, device=dev, generator=gen)
+                    acts[g] = rq.quantize_act_q8_1(xs[g], 512, k)
                 w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(cfg, li, pi)), k, n, device=dev)
                 y = torch.empty(512 * n, device=dev)
                 keep.append(w)
                 items.append((xs[g], w, y))
-        plan = rq.GemmPlan(items, 512)
+                q_items.append((acts[g], w, y))
         ops = sum(2 * 512 * n * k for _, _, n, k in layer) * nl
         # warm-up long enough for the clocks to settle (~30 ms of load)
         steps, warm = (20, 40) if nl > 1 else (40, 80)
-        ms = timed(lambda i: plan.run(), steps, warm)
-        tops = ops / (ms * 1e-3) / 1e12
+        # the GEMM kernels alone, from activation buffers a producer wrote
+        # (the reference times its MMA kernel the same way,
+        # quantized-mma-prefill.md:518-528; the activation pass is below)
+        qplan = rq.GemmPlan(q_items, 512, quantized=True)
+        ms = timed(lambda i: qplan.run(), steps, warm)
+        del qplan
+        # the same GEMMs from f32 activations: one f16 activation pass first
+        plan = rq.GemmPlan(items, 512)
+        ms_a = timed(lambda i: plan.run(), steps, warm)
+        tops, tops_a = ops / (ms * 1e-3) / 1e12, ops / (ms_a * 1e-3) / 1e12
         out[tag] = {"tops": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4),
                     "ms_per_step": round(ms, 3), "gop_per_step": round(ops / 1e9, 1),
                     "dtype": "f16 MFMA, f32 accumulate" if rq.get_options()["mmq_f16"] else "int8 MFMA (Q8_1)",
-                    "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4),
-                    "gemms_per_step": len(items)}
-        print(f"prefill {tag}: {ms:.3f} ms/step  {tops:.0f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak)",
-              file=sys.stderr, flush=True)
-        del plan, items, keep
+                    "gemms_per_step": len(items),
+                    "tops_with_act_pass": round(tops_a, 1), "ms_per_step_with_act_pass": round(ms_a, 3)}
+        print(f"prefill {tag}: GEMMs {ms:.3f} ms/step  {tops:.0f} TOPS ({tops / INT8_PEAK_TOPS:.1%} of int8 peak); "
+              f"with the activation pass {ms_a:.3f} ms  {tops_a:.0f} TOPS", file=sys.stderr, flush=True)
+        del plan, items, q_items, keep
     # config 4's tied LM head at M=512 (one GEMM, 151936 x 1024 Q6_K) and the
     # few-row GEMMs of short prompts (the reference's fused-path measurements:
     # 12 and 29 rows) over one Qwen3-0.6B layer set, weights read once per step
@@ -501,6 +512,27 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
                                     "frac_f16_peak": round(tops / F16_PEAK_TOPS, 4), "ms_per_step": round(ms, 3)}
     print(f"prefill lm_head M=512: {ms:.3f} ms  {tops:.0f} TOPS", file=sys.stderr, flush=True)
     del plan, w, x, y
+    # reference point: the 8B gate GEMM (512 x 4096 x 14336) as a plain f16
+    # GEMM on pre-dequantized weights (torch.matmul: hipBLASLt), against the
+    # Q4_K kernel on the same shape (the reference compares its MMA kernel
+    # with f16 cuBLAS the same way, quantized-mma-prefill.md:518-528)
+    name, ty, n, k = synth.QWEN3_8B_LAYER[4]
+    a16 = torch.randn(512, k, device=dev, dtype=torch.float16, generator=gen)
+    b16 = torch.randn(k, n, device=dev, dtype=torch.float16, generator=gen)
+    ms_f16 = timed(lambda i: torch.matmul(a16, b16), 40, 20)
+    w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(4, 0, 4)), k, n, device=dev)
+    act = rq.quantize_act_q8_1(torch.randn(512 * k, device=dev, generator=gen), 512, k)
+    y = torch.empty(512 * n, device=dev)
+    qplan = rq.GemmPlan([(act, w, y)], 512, quantized=True)
+    ms_q = timed(lambda i: qplan.run(), 40, 20)
+    ops = 2 * 512 * n * k
+    out["gate_8b_m512_vs_f16_gemm"] = {"q4k_kernel_us": round(ms_q * 1e3, 1),
+                                       "q4k_kernel_tops": round(ops / (ms_q * 1e-3) / 1e12, 1),
+                                       "f16_hipblaslt_us": round(ms_f16 * 1e3, 1),
+                                       "f16_hipblaslt_tops": round(ops / (ms_f16 * 1e-3) / 1e12, 1)}
+    print(f"8B gate 512x4096x14336: Q4_K kernel {ms_q * 1e3:.1f} us, f16 hipBLASLt on dequantized weights "
+          f"{ms_f16 * 1e3:.1f} us", file=sys.stderr, flush=True)
+    del qplan, w, act, y, a16, b16
     layer = synth.QWEN3_06B_LAYER
     ws = [rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(3, 0, pi)), k, n, device=dev)
           for pi, (_, ty, n, k) in enumerate(layer)]

@@ -271,6 +271,14 @@ typedef struct rfxq_gemm_q8_1_item {
 
 int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, hipStream_t stream);
 
+/* rfxq_gemm_plan_create over activation buffers already written (by the
+ * producers above): the plan's run launches only the GEMM kernels (and the
+ * split-K reduces), no activation pass. Run and destroy it as any plan. The
+ * buffers are read at run time, so a producer may rewrite them between runs.
+ * No reference counterpart (see rfxq_act_q8_1_size). */
+int rfxq_gemm_q8_1_plan_create(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, int device,
+                               rfxq_gemm_plan** out);
+
 /* ---- MoE ----------------------------------------------------------------- */
 
 /* src/moe.rs:47-98 route_top_k_with_norm on the host: softmax, top-k by

@@ -735,9 +735,14 @@ RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k_m64, TY_Q6K, 2, 2)
 // leaves q, and one multiply by the f16 pair (d, d) rounds. A 64-k stage is
 // two blocks (e = 0, 1); lane half h holds codes [16h, 16h + 16) of each, so
 // step t = 2e + s2 takes codes 32e + 16h + 8 s2 + [0, 8), the activations'
-// logical chunk 4e + 2h + s2, as for Q4_K. Blocks are 34 bytes: the pieces
-// are 2-byte aligned, read with unaligned buffer loads. Split-K ranges count
-// in units of 256 weights (8 blocks, four stages), as for the K-quants.
+// logical chunk 4e + 2h + s2, as for Q4_K. Blocks are 34 bytes, so the
+// stage's block pair (68 bytes) starts on a dword when the weights do: then
+// lane half h reads it with dword-aligned loads (bytes [16h, +20) and
+// [36 + 16h, +16), and the dword holding the d of the other half) and shifts
+// block 0's codes by two bytes (v_alignbyte; unaligned 16-byte loads ran the
+// kernel ~1.5x slower). Weights that start 2 bytes past a dword take the
+// unaligned loads. Split-K ranges count in units of 256 weights (8 blocks,
+// four stages), as for the K-quants.
 
 namespace mmqh {
 // f16 pairs f16(q * d) of one code dword v (bytes q0..q3, signs flipped by
@@ -753,8 +758,8 @@ RFXQ_DEV u2_t q80_codes_f16(uint32_t v, h2_t dv, uint32_t mg) {
 
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q8_0 weights:
 // the Q4_K tile's activation staging and MFMA schedule, with Q8_0 operands.
-template <int MT>
-RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+template <int MT, bool AL>
+RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
     using namespace mmqh;
     constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
@@ -777,11 +782,20 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
     // lane (l32, h) of n-tile j: column 64w + 32j + l32, codes [16h, +16) of
     // each block, and each block's d
-    uint32_t g_c[2];
+    // (the lane-varying parts of an offset go in the VGPR offset: a
+    // lane-varying SGPR offset would make the compiler loop over lanes)
+    uint32_t g_c[2], g_q[2];
 #pragma unroll
-    for (int j = 0; j < 2; j++) g_c[j] = (64u * w + 32u * j + l32) * row_bytes + sh0;
+    for (int j = 0; j < 2; j++) {
+        g_c[j] = (64u * w + 32u * j + l32) * row_bytes + sh0;
+        g_q[j] = g_c[j] + (AL ? 16u * h : 2u + 16u * h);
+    }
+    const uint32_t e_off = h ? 0u : 32u;  // aligned form: the dword with the other half's d
     const uint32_t nst = 4u * (sb1 - sb0);
 
+    // raw stage data per column: unaligned form qn = codes of blocks 0, 1 and
+    // dn = their d; aligned form qn[0] = bytes [16h, +16), qn[1] = bytes
+    // [36 + 16h, +16), dn[0] = the dword after qn[0], dn[1] = the other d's dword
     u4_t sa[MT], qn[2][2];
     uint32_t dn[2][2];
     auto load_act = [&](uint32_t st) {
@@ -794,14 +808,25 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     auto load_w = [&](uint32_t st) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t blk = 8u * sb0 + 2u * sl;  // the stage's first block in the row
+        if constexpr (AL) {
+            const uint32_t o = 34u * blk;  // dword aligned (blk is even)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const uint32_t o = 34u * (blk + e);
-                qn[j][e] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], o + 2u + 16u * h, 0);
-                dn[j][e] = __builtin_amdgcn_raw_buffer_load_b16(r_w, g_c[j], o, 0);
+            for (int j = 0; j < 2; j++) {
+                qn[j][0] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], o, 0);
+                dn[j][0] = __builtin_amdgcn_raw_buffer_load_b32(r_w, g_q[j], o + 16u, 0);
+                qn[j][1] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], o + 36u, 0);
+                dn[j][1] = __builtin_amdgcn_raw_buffer_load_b32(r_w, g_c[j] + e_off, o, 0);
             }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t o = 34u * (blk + e);
+                    qn[j][e] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], o, 0);
+                    dn[j][e] = __builtin_amdgcn_raw_buffer_load_b16(r_w, g_c[j], o, 0);
+                }
+        }
     };
     auto store_act = [&](uint32_t st) {
         uint8_t* S = lds + (st & 1u) * kAct;
@@ -831,12 +856,23 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
         u4_t q[2][2];
         h2_t dv[2][2];
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 2; j++) {
+            if constexpr (AL) {
+                const u4_t a = qn[j][0];
+                const uint32_t b = dn[j][0], e = dn[j][1];
+                q[j][0] = u4_t{alignbyte(a.y, a.x, 2u), alignbyte(a.z, a.y, 2u), alignbyte(a.w, a.z, 2u),
+                               alignbyte(b, a.w, 2u)} ^ u4_t{sgn, sgn, sgn, sgn};
+                q[j][1] = qn[j][1] ^ u4_t{sgn, sgn, sgn, sgn};
+                dv[j][0] = as_h2(splat16<0>(h ? e : a.x));
+                dv[j][1] = as_h2(h ? splat16<1>(b) : splat16<1>(e));
+            } else {
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                q[j][e] = qn[j][e] ^ u4_t{sgn, sgn, sgn, sgn};
-                dv[j][e] = as_h2(splat16<0>(dn[j][e]));
+                for (int e = 0; e < 2; e++) {
+                    q[j][e] = qn[j][e] ^ u4_t{sgn, sgn, sgn, sgn};
+                    dv[j][e] = as_h2(splat16<0>(dn[j][e]));
+                }
             }
+        }
         load_w(st + 1u);
         load_act(st + 1u);
         const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
@@ -897,6 +933,12 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 #pragma unroll
         for (int j = 0; j < 2; j++)
             store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+}
+
+template <int MT>
+RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+    if ((reinterpret_cast<uintptr_t>(ds.w) & 3u) == 0u) mmqh_q80_rows_t<MT, true>(ds, m0, n0, ks, lds);
+    else mmqh_q80_rows_t<MT, false>(ds, m0, n0, ks, lds);
 }
 
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0, TY_Q8_0, 4, 2)

@@ -1209,6 +1209,8 @@ struct GemmGroup {
         uint64_t off = 0;  // workspace offset of the layouts L
         ActLayout L;
         bool need_i8 = false, need_h = false;
+        const uint8_t* ext = nullptr;  // a caller's activation buffer (every layout, act_layout): not quantized here
+        uint8_t* base(uint8_t* ws) const { return ext ? const_cast<uint8_t*>(ext) : ws + off; }
     };
     std::vector<Act> acts;
     std::vector<MmqDesc> descs[kGroupKernels];
@@ -1236,7 +1238,11 @@ uint32_t group_tile_m(uint32_t g) {
 }
 uint32_t group_variant(bool f16, uint32_t tile_m) { return f16 ? (tile_m == 32u ? 3u : tile_m == 64u ? 4u : 2u) : (tile_m == 64u ? 1u : 0u); }
 
-int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus) {
+// `ext` (optional, one per item): the items' x are caller activation buffers
+// (rfxq_act_q8_1_size layouts, already quantized): every GEMM takes an MMQ
+// kernel (f16 unless REFLEX_MMQ_F16=0) and the group quantizes nothing.
+int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, GemmGroup* g, uint32_t cus,
+                     bool ext = false) {
     if (!items || count == 0 || rows == 0) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: empty");
     rfxq_options o;
     if (int rc = get_options(&o)) return rc;
@@ -1245,10 +1251,16 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_weight(it.w, "gemm group")) return rc;
         if (!it.x || !it.y) return fail(RFXQ_ERR_INVALID_INPUT, "gemm group: item %u has a NULL x or y", i);
-        if (reinterpret_cast<uintptr_t>(it.x) % 16u)
-            return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not 16-byte aligned", i);
+        if (reinterpret_cast<uintptr_t>(it.x) % (ext ? 256u : 16u))
+            return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not %u-byte aligned", i, ext ? 256u : 16u);
         const uint32_t k = it.w->in_features;
-        const rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o);
+        rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o);
+        if (ext) {
+            if (int rc = check_act(it.x, rows, k, "gemm_q8_1 plan")) return rc;
+            const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, 0);
+            pol.path = f16 ? PATH_MMQ_F16 : PATH_MMQ_INT8;
+            pol.tile_m = f16 ? f16_tile_m(rows) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
+        }
         if (pol.path == PATH_GEMV_ROWS) {
             for (uint32_t r = 0; r < rows; r++)
                 g->gemv_rows.push_back({it.x + (uint64_t)r * k, it.w, it.y + (uint64_t)r * it.w->out_features});
@@ -1262,6 +1274,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             GemmGroup::Act act;
             act.x = it.x;
             act.k = k;
+            if (ext) act.ext = reinterpret_cast<const uint8_t*>(it.x);
             g->acts.push_back(act);
         } else if (g->acts[ai].k != k) {
             return fail(RFXQ_ERR_OTHER, "gemm group: one x used with in_features %u and %u", g->acts[ai].k, k);
@@ -1271,6 +1284,10 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         else g->acts[ai].need_i8 = true;
     }
     for (auto& a : g->acts) {
+        if (a.ext) {
+            a.L = act_layout(rows, a.k);
+            continue;
+        }
         a.L = act_layout_sel(rows, a.k, a.need_i8, a.need_h);
         a.off = g->ws_bytes;
         g->ws_bytes += a.L.total;
@@ -1369,7 +1386,7 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
         for (size_t i = 0; i < g->descs[t].size(); i++) {
             MmqDesc& d = g->descs[t][i];
             const GemmGroup::Act& a = g->acts[g->act_of[t][i]];
-            act_desc(&d, ws + a.off, a.L, group_f16(t), d.k);
+            act_desc(&d, a.base(ws), a.L, group_f16(t), d.k);
         }
     for (auto& r : g->reduces) {
         r.part = reinterpret_cast<float*>(ws + r.off);
@@ -1379,7 +1396,8 @@ void bind_gemm_group(GemmGroup* g, uint8_t* ws) {
 
 int run_gemm_quant(Ctx* c, const GemmGroup& g, uint8_t* ws, uint32_t rows, hipStream_t stream) {
     for (const auto& a : g.acts)
-        if (int rc = launch_act(c, a.x, rows, a.k, ws + a.off, a.L, a.need_i8, a.need_h, stream)) return rc;
+        if (!a.ext)
+            if (int rc = launch_act(c, a.x, rows, a.k, ws + a.off, a.L, a.need_i8, a.need_h, stream)) return rc;
     return RFXQ_OK;
 }
 
@@ -1922,11 +1940,9 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
     if (int rc = get_options(&o)) return rc;
     if (gemm_policy(w->ggml_type, k, n, rows, (uint32_t)c->cus, o).path == PATH_GEMV_ROWS) {
         // a buffer holds no f32 copy for GEMVs: its few rows run on the MMQ kernel
-        // (f16 layout when the weight allows it, else int8)
         o.fused_max_rows = 0;
         o.quant_mma = 1;
         o.quant_mma_max_rows = 0;
-        o.mmq_f16 = o.mmq_f16 && w->ggml_type != RFXQ_TYPE_Q8_0;
     }
     // one row plans as two (same tiles): the policy sends single rows to the GEMV
     const GemmPlan p = plan_gemm(c, w, std::max(rows, 2u), o);
@@ -2003,8 +2019,8 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
     return ok();
 }
 
-int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, int device,
-                          rfxq_gemm_plan** out) {
+static int gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, int device,
+                            rfxq_gemm_plan** out, bool ext) {
     if (!out) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_plan_create: out is NULL");
     *out = nullptr;
     int prev = 0;
@@ -2015,7 +2031,7 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
     auto plan = std::make_unique<rfxq_gemm_plan>();
     plan->device = device;
     plan->rows = rows;
-    if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g, (uint32_t)c->cus);
+    if (rc == RFXQ_OK) rc = build_gemm_group(items, count, rows, &plan->g, (uint32_t)c->cus, ext);
     uint64_t tables = 0;
     if (rc == RFXQ_OK) {
         tables = align256(plan->g.acts.size() * sizeof(QuantDesc)) + align256(plan->g.acts.size() * sizeof(ActF16Desc));
@@ -2041,8 +2057,9 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
         std::vector<ActF16Desc> hq;
         plan->hwave = true;  // one kernel for all f16 layouts: row per wave only if every activation allows it
         for (const auto& a : plan->g.acts)
-            if (a.need_h && !act_f16_wave(rows, a.k)) plan->hwave = false;
+            if (!a.ext && a.need_h && !act_f16_wave(rows, a.k)) plan->hwave = false;
         for (const auto& a : plan->g.acts) {
+            if (a.ext) continue;
             uint8_t* ab = base + a.off;
             if (a.need_i8) {
                 const uint32_t wgs = quant_grid((uint64_t)rows * (a.k / 32u));
@@ -2081,6 +2098,19 @@ int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t 
     }
     *out = plan.release();
     return ok();
+}
+
+int rfxq_gemm_plan_create(const rfxq_gemm_item* items, uint32_t count, uint32_t rows, int device,
+                          rfxq_gemm_plan** out) {
+    return gemm_plan_create(items, count, rows, device, out, false);
+}
+
+int rfxq_gemm_q8_1_plan_create(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, int device,
+                               rfxq_gemm_plan** out) {
+    if (!items && count) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_plan_create: items is NULL");
+    std::vector<rfxq_gemm_item> v(count);
+    for (uint32_t i = 0; i < count; i++) v[i] = {static_cast<const float*>(items[i].act), items[i].w, items[i].y};
+    return gemm_plan_create(v.data(), count, rows, device, out, true);
 }
 
 int rfxq_gemm_plan_run(const rfxq_gemm_plan* plan, hipStream_t stream) {

@@ -431,15 +431,20 @@ def gemm_q8_1_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows
 
 
 class GemmPlan:
-    """gemm_batch with its tables and activation workspace built once."""
+    """gemm_batch with its tables and activation workspace built once. With
+    ``quantized=True`` the items' first members are activation buffers
+    (act_q8_1_size layouts, written by a producer) and a run launches only
+    the GEMM kernels."""
 
-    def __init__(self, items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int):
+    def __init__(self, items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int, quantized: bool = False):
         arr, self._keep = _items(items)
         self._tensors = items
         h = ctypes.c_void_p()
         dev = items[0][0].device.index or 0
         self._lib = lib()  # kept so that __del__ works during interpreter shutdown
-        _check(self._lib.rfxq_gemm_plan_create(arr, len(items), rows, dev, ctypes.byref(h)))
+        create = self._lib.rfxq_gemm_q8_1_plan_create if quantized else self._lib.rfxq_gemm_plan_create
+        _check(create(ctypes.cast(arr, ctypes.c_void_p) if quantized else arr, len(items), rows, dev,
+                      ctypes.byref(h)))
         self._h = h
 
     def run(self) -> None:

@@ -71,17 +71,14 @@ def test_silu_and_mul_q8_1(rq, rows, k):
 @pytest.mark.parametrize("ty", [Q4K, Q6K, Q8_0])
 @pytest.mark.parametrize("rows,n,k", [(512, 1024, 1024), (64, 512, 4096), (300, 136, 2048)])
 def test_gemm_from_activation_buffer(rq, opts, ty, rows, n, k):
-    """GEMMs from a buffer equal rfxq_gemm on the f32 activation. A buffer holds
-    no f32 copy, so Q8_0 reads its int8 layout: compared with rfxq_gemm on the
-    int8 kernels (REFLEX_MMQ_F16=0), where f16 mode runs Q8_0 rows as GEMVs."""
+    """GEMMs from a buffer equal rfxq_gemm on the f32 activation, on the f16
+    kernels and on the int8 ones (REFLEX_MMQ_F16=0)."""
     x = _dev(synth.activations(rows * k, 5 + rows))
     w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, 6 + n), k, n, device=DEV)
-    if ty == Q8_0:
-        opts(mmq_f16=0)
-    want = rq.gemm(x, w, rows)
-    opts(mmq_f16=1)
     act = rq.quantize_act_q8_1(x, rows, k)
-    assert torch.equal(rq.gemm_q8_1(act, w, rows), want)
+    for f16 in (1, 0):
+        opts(mmq_f16=f16)
+        assert torch.equal(rq.gemm_q8_1(act, w, rows), rq.gemm(x, w, rows)), f"mmq_f16={f16}"
 
 
 def test_gemm_q8_1_batch(rq, opts):
@@ -98,10 +95,7 @@ def test_gemm_q8_1_batch(rq, opts):
     refs = []
     for (act, w, _), (ty, n, k) in zip(items, shapes):
         r = torch.empty(rows * n, device=DEV)
-        if ty == Q8_0:   # the buffer's int8 layout (see test_gemm_from_activation_buffer)
-            opts(mmq_f16=0)
         rq.gemm_batch([(xa if k == 1024 else xb, w, r)], rows)
-        opts(mmq_f16=1)
         refs.append(r)
     rq.gemm_q8_1_batch(items, rows)
     for (_, _, y), r in zip(items, refs):
@@ -116,3 +110,27 @@ def test_fused_producer_errors(rq):
     act = torch.empty(rq.act_q8_1_size(4, 1024) + 256, dtype=torch.uint8, device=DEV)
     with pytest.raises(rq.ReflexError, match="256-byte aligned"):
         rq.gemm_q8_1(act[16:], w, 4)
+
+
+def test_gemm_q8_1_plan_matches_f32_plan(rq):
+    """A plan over activation buffers (rfxq_gemm_q8_1_plan_create: GEMM kernels
+    only) gives the f32 plan's results bit for bit (same kernels, tiles and
+    split-K), for a 0.6B layer's GEMMs at 512 rows and an 8B layer's at 40."""
+    for layer, rows, seed in ((synth.QWEN3_06B_LAYER, 512, 5), (synth.QWEN3_8B_LAYER, 40, 6)):
+        group = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o",
+                 "gate_proj": "gu", "up_proj": "gu", "down_proj": "down"}
+        xs, acts, f32_items, q_items = {}, {}, [], []
+        for pi, (name, ty, n, k) in enumerate(layer):
+            g = group[name]
+            if g not in xs:
+                xs[g] = torch.from_numpy(synth.activations(rows * k, seed * 100 + pi)).to(DEV)
+                acts[g] = rq.quantize_act_q8_1(xs[g], rows, k)
+            w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, seed * 100 + 50 + pi), k, n, device=DEV)
+            f32_items.append((xs[g], w, torch.empty(rows * n, device=DEV)))
+            q_items.append((acts[g], w, torch.full((rows * n,), float("nan"), device=DEV)))
+        rq.GemmPlan(f32_items, rows).run()
+        plan = rq.GemmPlan(q_items, rows, quantized=True)
+        for _ in range(2):
+            plan.run()
+            for (_, _, a), (_, _, b) in zip(f32_items, q_items):
+                assert torch.equal(a, b)

@@ -250,6 +250,26 @@ def test_gemm_q8_0_config1_matrix(rq, orc, m):
     _check_gemm(rq, orc, Q8_0, m, n, k, w_np, x)
 
 
+@pytest.mark.parametrize("ty", [Q6K, Q8_0])
+@pytest.mark.parametrize("m", [40, 300])
+def test_gemm_weights_two_bytes_past_a_dword(rq, orc, ty, m):
+    """Q6_K and Q8_0 weights need only 2-byte alignment: weights starting 2
+    bytes past a dword (the Q8_0 tile's unaligned-load form) give the same
+    results as the same blocks dword aligned."""
+    n, k = 520, 2048
+    w_np = synth.weights(ty, n, k, 830 + m)
+    buf = torch.zeros(w_np.size + 16, dtype=torch.uint8, device=DEV)
+    buf[2:2 + w_np.size] = _dev(w_np)
+    w2 = rq.Weight(rq.GgmlType(ty), buf, [k, n], offset=2, len=w_np.size)
+    w4 = _weight(rq, ty, w_np, n, k)
+    x = _dev(synth.activations(m * k, 831 + m))
+    y2 = rq.gemm(x, w2, m)
+    assert torch.equal(y2, rq.gemm(x, w4, m))
+    e = orc.rel_err_row_l2(y2.cpu().numpy().reshape(m, n),
+                           orc.reference_gemm(ty, w_np, n, k, x.cpu().numpy().reshape(m, k)))
+    assert e < TOL
+
+
 def test_gemm_q8_0_large(rq, orc):
     """Q8_0 at an 8B-class shape, M = 512, 64 sampled rows."""
     n, k, m = 4096, 4096, 512
