@@ -10,3 +10,4 @@
 #include "mmq.hpp"
 #include "mmqh.hpp"
 #include "moe.hpp"
+#include "moe_decode.hpp"

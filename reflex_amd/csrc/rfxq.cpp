@@ -149,6 +149,8 @@ struct Ctx {
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
     hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
+    // MoE decode kernels: [Q4_K, Q6_K, Q8_0][4, 8, 16, 32 lanes per row]
+    hipFunction_t moe_dec_gu[3][4] = {}, moe_dec_dn[3][4] = {};
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
     void* scratch = nullptr;  // this device's fixed scratch array (rfxq_gemm_no_alloc)
@@ -243,6 +245,17 @@ int load_ctx(int device, Ctx** out) {
         if (e != hipSuccess)
             return fail(RFXQ_ERR_GPU, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
     }
+    static const char* const kDecTy[3] = {"q4k", "q6k", "q8_0"};
+    for (int t = 0; t < 3; t++)
+        for (int l = 0; l < 4; l++)
+            for (int g = 0; g < 2; g++) {
+                char name[64];
+                std::snprintf(name, sizeof name, "rfxq_moe_dec_%s_%s_%d", g ? "down" : "gu", kDecTy[t], 4 << l);
+                hipFunction_t* f = g ? &c->moe_dec_dn[t][l] : &c->moe_dec_gu[t][l];
+                hipError_t e = hipModuleGetFunction(f, c->mod, name);
+                if (e != hipSuccess)
+                    return fail(RFXQ_ERR_GPU, "hipModuleGetFunction(%s): %s", name, hipGetErrorString(e));
+            }
     // the fixed scratch of rfxq_gemm_no_alloc, resolved now (the device is
     // current); a failure disables only that entry point, which reports it
     c->scratch_err = rfxq_scratch::setup(device, &c->scratch);
@@ -2571,6 +2584,103 @@ int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, 
 
 namespace {
 
+// ------------------------------------------------------------------ MoE decode (two launches)
+
+// Mirror of MoeDecArgs (moe_decode.hpp).
+struct MoeDecArgs {
+    const float* x;
+    const float* logits;
+    int32_t* idx;
+    float* wts;
+    const uint8_t* wg;
+    const uint8_t* wu;
+    const uint8_t* wd;
+    uint64_t eb_gu, eb_dn;
+    float* s;
+    float* out;
+    uint32_t tokens, E, k, hidden, ffn, normalize;
+    float scale;
+    uint32_t nb1, nr1;
+    uint32_t nb2, nr2;
+    uint32_t lds_x1, lds_x2;
+};
+constexpr uint32_t kDecRouteMaxE = 256;  // moe_decode.hpp
+
+// Lanes per row of the decode kernels: a power of two in [4, 32] dividing the
+// row's units, with at least `min_units` units per lane (fewer loads in
+// flight per lane below that) when the row allows; -1 if none divides.
+int dec_lpr(uint32_t units, uint32_t min_units, uint32_t max_lpr) {
+    int best = -1;
+    for (int l = 3; l >= 0; l--) {
+        const uint32_t lpr = 4u << l;
+        if (lpr > max_lpr || units % lpr) continue;
+        if (best < 0) best = l;  // the widest that divides
+        if (units / lpr >= min_units) return l;
+    }
+    return best;
+}
+
+// The two-launch decode pipeline (moe_decode.hpp) when its limits hold:
+// rows tokens of up to kMoeGemvRows, k <= 64, hidden and k * ffn <= 16384, at
+// most kDecRouteMaxE experts when it routes,
+// stacked weights below 4 GiB, row units that split over 4..32 lanes. Routing
+// from `logits` (device) in the first launch, or from idx / wts already in
+// device memory. s: workspace [rows][k][ffn]. Returns RFXQ_OK with *done =
+// false when the shapes fall outside the limits (nothing launched).
+int moe_decode_launch(Ctx* c, const float* x, uint32_t rows, uint32_t hidden, const float* logits, int32_t* idx,
+                      float* wts, uint32_t E, uint32_t k, int normalize, float scale, const rfxq_weight* gate,
+                      const rfxq_weight* up, const rfxq_weight* down, float* s, float* out, hipStream_t stream,
+                      bool* done) {
+    *done = false;
+    const uint32_t ffn = gate->out_features;
+    const int tg = type_index(gate->ggml_type), td = type_index(down->ggml_type);
+    auto unit_k = [](uint32_t ty) { return ty == RFXQ_TYPE_Q8_0 ? 32u : 64u; };
+    const uint64_t lim = 0xF0000000ull;
+    if (rows == 0 || rows > kMoeGemvRows || k == 0 || k > 64u || hidden > 16384u || (uint64_t)k * ffn > 16384u ||
+        (logits && E > kDecRouteMaxE) ||
+        gate->len >= lim || up->len >= lim || down->len >= lim || hidden % 256u || ffn % 256u)
+        return RFXQ_OK;
+    const int l1 = dec_lpr(hidden / unit_k(gate->ggml_type), 4u, 32u);
+    const int l2 = dec_lpr(ffn / unit_k(down->ggml_type), 2u, std::min(32u, 256u / k));
+    if (l1 < 0 || l2 < 0) return RFXQ_OK;
+    MoeDecArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.x = x;
+    a.logits = logits;
+    a.idx = idx;
+    a.wts = wts;
+    a.wg = static_cast<const uint8_t*>(gate->data);
+    a.wu = static_cast<const uint8_t*>(up->data);
+    a.wd = static_cast<const uint8_t*>(down->data);
+    a.eb_gu = gate->len / E;
+    a.eb_dn = down->len / E;
+    a.s = s;
+    a.out = out;
+    a.tokens = rows;
+    a.E = E;
+    a.k = k;
+    a.hidden = hidden;
+    a.ffn = ffn;
+    a.normalize = normalize ? 1u : 0u;
+    a.scale = scale;
+    const uint32_t lpr1 = 4u << l1, lpr2 = 4u << l2;
+    a.nr1 = 2u * (64u / lpr1);  // waves 0-1 gate rows, 2-3 up rows
+    a.nb1 = (ffn + a.nr1 - 1u) / a.nr1;
+    a.nr2 = (256u / lpr2) / k;  // (row, slot) items per workgroup
+    a.nb2 = (hidden + a.nr2 - 1u) / a.nr2;
+    a.lds_x1 = 0u;
+    a.lds_x2 = 768u;  // experts, weights, combine order
+    const uint32_t K2 = k * ffn;
+    const uint32_t lds1 = a.lds_x1 + hidden * 2u + hidden / 4u + 16u + 2u * a.nr1 * 4u;
+    const uint32_t lds2 = a.lds_x2 + K2 * 2u + K2 / 4u + 16u + a.nr2 * k * 4u;
+    if (int rc = launch(c->moe_dec_gu[tg][l1], rows * k * a.nb1, lds1, stream, &a, sizeof a, "rfxq_moe_dec_gu launch"))
+        return rc;
+    if (int rc = launch(c->moe_dec_dn[td][l2], rows * a.nb2, lds2, stream, &a, sizeof a, "rfxq_moe_dec_down launch"))
+        return rc;
+    *done = true;
+    return RFXQ_OK;
+}
+
 // The device-planned pipeline: routing on the device from `router_logits`,
 // or the host's routing (`host_idx`, `host_w`: rows x top_k experts and
 // weights already multiplied by weight_scale) uploaded in one copy.
@@ -2715,6 +2825,13 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
                                       f16 ? reinterpret_cast<uint16_t*>(B + o_x + Lx.xsx) : nullptr,
                                       f16 ? reinterpret_cast<float*>(B + o_x + Lx.xrs) : nullptr, stream))
             return rc;
+    }
+    if (gemv_form) {  // two launches (moe_decode.hpp) where the shapes allow them
+        bool done = false;
+        if (int rc = moe_decode_launch(c, x, rows, hidden, host_idx ? nullptr : router_logits, d_idx, d_w, expert_count,
+                                       top_k, normalize, weight_scale, gate, up, down, gout, out, stream, &done))
+            return rc;
+        if (done) return ok();
     }
     if (int rc = launch(c->moe_plan, 1, 0, stream, &pa, sizeof pa, "rfxq_moe_plan launch", 1024)) return rc;
     if (gemv_form) {
