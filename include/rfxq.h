@@ -177,9 +177,10 @@ uint64_t rfxq_gemm_workspace_size(const rfxq_weight* w, uint32_t rows);
 
 /* Model::gemm (src/model/kernels.rs:2197) on a quantized-resident weight:
  * y[rows][N] = x[rows][K] . W^T, on the path rfxq_gemm_policy_for names: one
- * decode GEMV per row (a single row, up to fused_max_rows rows, Q8_0 in f16
- * mode), or activations brought into the f16 (Q4_K, Q6_K) or int8 Q8_1
- * layout and the MFMA MMQ kernel (replacing gemm_quant_mma,
+ * decode GEMV per row (a single row, up to 4 rows, K not a multiple of 256),
+ * or activations brought into the f16 layout and the f16-MFMA MMQ kernels
+ * for Q4_K, Q6_K and Q8_0 (the int8 Q8_1 layout and kernels with
+ * REFLEX_MMQ_F16=0) (replacing gemm_quant_mma,
  * kernels.rs:2262-2340). `workspace` may be NULL (the library then uses its
  * own grow-only per-device buffer: calls on different streams must then not
  * overlap, and a call that would grow it fails under graph capture) or hold
