@@ -1334,9 +1334,11 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
     // a kernel whose tiles would leave CUs idle splits K (fixed-order reduce);
     // REFLEX_QUANT_MMA_SPLITS sets the split count, as for single GEMMs
     const uint32_t forced = o.quant_mma_splits;
+    bool split_small[kGroupKernels] = {};
     for (uint32_t t = 0; t < kGroupKernels; t++) {
         auto& v = g->descs[t];
         if (v.empty() || (!forced && 2u * g->wgs[t] >= cus)) continue;
+        split_small[t] = true;
         // one split size for the launch, so its workgroups take alike
         std::vector<std::pair<uint32_t, uint32_t>> tn;
         for (const auto& d : v) tn.push_back({d.tiles_m * d.tiles_n, d.k / 256u});
@@ -1348,6 +1350,66 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             const uint32_t s = forced ? std::min(forced, nsb) : (nsb + w_sb - 1u) / w_sb;
             d.sb_per_split = (nsb + s - 1u) / s;
             d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
+            if (d.splits > 1u) {
+                const uint64_t n = (uint64_t)rows * d.n;
+                g->reduces.push_back({t, i, g->ws_bytes, d.y, nullptr, n, d.splits});
+                g->ws_bytes += align256((uint64_t)d.splits * n * 4u);
+            }
+            d.wg_begin = wg;
+            wg += d.tiles_m * d.tiles_n * d.splits;
+        }
+        g->wgs[t] = wg;
+    }
+    // A launch of many tiles with GEMMs of very different K (a Q8_0 layer's
+    // down projection, K = 14336, among K = 4096 GEMMs): a GEMM whose tiles
+    // run over 3x the launch's median super-blocks splits K to about the
+    // median, and such a launch starts its longest tiles first, so that they
+    // do not run alone at its end.
+    for (uint32_t t = 0; t < kGroupKernels && !forced; t++) {
+        auto& v = g->descs[t];
+        if (v.size() < 2u || split_small[t]) continue;
+        std::vector<std::pair<uint32_t, uint32_t>> by_sb;  // (super-blocks per tile, tiles)
+        uint64_t all = 0;
+        for (const auto& d : v) {
+            by_sb.push_back({d.sb_per_split, d.tiles_m * d.tiles_n * d.splits});
+            all += by_sb.back().second;
+        }
+        std::sort(by_sb.begin(), by_sb.end());
+        uint64_t acc = 0;
+        uint32_t med = by_sb.back().first;
+        for (const auto& e : by_sb)
+            if ((acc += e.second) * 2u >= all) {
+                med = e.first;
+                break;
+            }
+        bool changed = false;
+        for (uint32_t i = 0; i < v.size(); i++) {
+            MmqDesc& d = v[i];
+            if (d.splits != 1u || d.sb_per_split <= 3u * med) continue;
+            const uint32_t nsb = d.k / 256u, s = (nsb + med - 1u) / med;
+            d.sb_per_split = (nsb + s - 1u) / s;
+            d.splits = (nsb + d.sb_per_split - 1u) / d.sb_per_split;
+            changed = true;
+        }
+        // longest tiles first (stable), descriptors and their activations
+        // alike; a launch with no split keeps its order, which groups the
+        // GEMMs that read one activation buffer
+        if (!changed) continue;
+        std::vector<uint32_t> ord(v.size());
+        for (uint32_t i = 0; i < ord.size(); i++) ord[i] = i;
+        std::stable_sort(ord.begin(), ord.end(),
+                         [&](uint32_t a, uint32_t b) { return v[a].sb_per_split > v[b].sb_per_split; });
+        std::vector<MmqDesc> nv;
+        std::vector<uint32_t> na;
+        for (uint32_t i : ord) {
+            nv.push_back(v[i]);
+            na.push_back(g->act_of[t][i]);
+        }
+        v.swap(nv);
+        g->act_of[t].swap(na);
+        uint32_t wg = 0;
+        for (uint32_t i = 0; i < v.size(); i++) {
+            MmqDesc& d = v[i];
             if (d.splits > 1u) {
                 const uint64_t n = (uint64_t)rows * d.n;
                 g->reduces.push_back({t, i, g->ws_bytes, d.y, nullptr, n, d.splits});

@@ -394,6 +394,35 @@ def test_gemm_batch_and_plan_match_single_gemms(rq, orc, opts):
     assert orc.rel_err_row_l2(first[2].reshape(rows, n), ref) < TOL
 
 
+def test_gemm_plan_long_k_among_short(rq, orc):
+    """A launch of many tiles whose GEMMs differ in K (a Q8_0 layer's down
+    projection among K = 1024 GEMMs): the long GEMM splits K to about the
+    launch's median and its tiles run first. Results stay within f32 rounding
+    of the single GEMMs and within the north star's bound of the reference."""
+    rows = 512
+    shapes = [(Q8_0, 2048, 1024), (Q8_0, 2048, 1024), (Q8_0, 1024, 4096)]
+    xa = synth.activations(rows * 1024, 91)
+    xb = synth.activations(rows * 4096, 92)
+    items, w_nps = [], []
+    for i, (ty, n, k) in enumerate(shapes):
+        w_nps.append(synth.weights(ty, n, k, 93 + i))
+        items.append((_dev(xa if k == 1024 else xb), _weight(rq, ty, w_nps[-1], n, k),
+                      torch.empty(rows * n, device=DEV)))
+    singles = [rq.gemm(x, w, rows).cpu().numpy() for x, w, _ in items]
+    plan = rq.GemmPlan(items, rows)
+    for _ in range(2):
+        plan.run()
+        for (_, _, y), ref in zip(items, singles):
+            assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+    rq.gemm_batch(items, rows)
+    for (_, _, y), ref in zip(items, singles):
+        assert np.abs(y.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+    sample = np.arange(0, rows, 17)
+    ref = orc.reference_gemm(Q8_0, w_nps[2], 1024, 4096, xb.reshape(rows, 4096)[sample])
+    y = items[2][2].cpu().numpy().reshape(rows, 1024)[sample]
+    assert orc.rel_err_row_l2(y, ref) < TOL
+
+
 def test_gemm_batch_errors(rq):
     x = _dev(synth.activations(64 * 1024, 3))
     w1 = _weight(rq, Q4K, synth.weights(Q4K, 256, 1024, 1), 256, 1024)
