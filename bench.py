@@ -53,8 +53,9 @@ def main() -> int:
                          "process with the caller's OpenMP settings)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only replay the fused GEMV plan and a calibration copy (for rocprofv3 --pmc runs)")
-    ap.add_argument("--prefill-probe", action="store_true",
-                    help="only run the 8B gate GEMM (14336x4096 Q4_K, M=512) 5 times (for rocprofv3 --pmc runs)")
+    ap.add_argument("--prefill-probe", nargs="?", const="gate8b", choices=("gate8b", "set06b"),
+                    help="only run the 8B gate GEMM (14336x4096 Q4_K, M=512; gate8b, the default) or the "
+                         "Qwen3-0.6B M=512 set's GEMM plan (set06b) a few times (for rocprofv3 --pmc runs)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, WRITE_SIZE) of a "
                          "--traffic-probe run into profiles/gemv_decode06b_traffic.json")
@@ -95,6 +96,16 @@ def main() -> int:
     rq.init(0)
     stream = torch.cuda.current_stream()
 
+    if args.prefill_probe == "set06b":
+        # the GEMM launches of bench's config 3 step (activation buffers written once)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(4242)
+        _, q_items, keep = prefill_set(rq, synth, torch, dev, synth.QWEN3_06B_LAYER, synth.QWEN3_06B_LAYERS, 3, gen)
+        qplan = rq.GemmPlan(q_items, 512, quantized=True)
+        for _ in range(10):
+            qplan.run()
+        torch.cuda.synchronize()
+        return 0
     if args.prefill_probe:
         name, ty, n, k = synth.QWEN3_8B_LAYER[4]
         w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(4, 0, 4)), k, n, device=dev)
@@ -447,6 +458,28 @@ def moe_leg(rq, synth, torch, np, dev, timed):
     return out
 
 
+def prefill_set(rq, synth, torch, dev, layer, nl, cfg, gen):
+    """nl layers of M=512 GEMMs, each layer with its own four activations (q/k/v
+    share one, as do gate/up; o and down have their own): (f32 items, items
+    over activation buffers written once by rfxq_quantize_act_q8_1, weights)."""
+    group = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o",
+             "gate_proj": "gu", "up_proj": "gu", "down_proj": "down"}
+    items, q_items, keep = [], [], []
+    for li in range(nl):
+        xs, acts = {}, {}
+        for pi, (name, ty, n, k) in enumerate(layer):
+            g = group[name]
+            if g not in xs:
+                xs[g] = torch.randn(512 * k, device=dev, generator=gen)
+                acts[g] = rq.quantize_act_q8_1(xs[g], 512, k)
+            w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(cfg, li, pi)), k, n, device=dev)
+            y = torch.empty(512 * n, device=dev)
+            keep.append(w)
+            items.append((xs[g], w, y))
+            q_items.append((acts[g], w, y))
+    return items, q_items, keep
+
+
 def prefill_leg(rq, synth, torch, np, dev, timed):
     """M=512 MMQ GEMMs: the 0.6B layer set (config 3) and one 8B layer (config 4).
 
@@ -459,22 +492,7 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
     gen.manual_seed(4242)
     for tag, layer, nl in (("qwen3_06b_m512", synth.QWEN3_06B_LAYER, synth.QWEN3_06B_LAYERS),
                            ("qwen3_8b_m512_1layer", synth.QWEN3_8B_LAYER, 1)):
-        cfg = 3 if nl > 1 else 4
-        group = {"q_proj": "qkv", "k_proj": "qkv", "v_proj": "qkv", "o_proj": "o",
-                 "gate_proj": "gu", "up_proj": "gu", "down_proj": "down"}
-        items, q_items, keep = [], [], []
-        for li in range(nl):
-            xs, acts = {}, {}
-            for pi, (name, ty, n, k) in enumerate(layer):
-                g = group[name]
-                if g not in xs:
-                    xs[g] = torch.randn(512 * k, device=dev, generator=gen)
-                    acts[g] = rq.quantize_act_q8_1(xs[g], 512, k)
-                w = rq.Weight.from_blocks(ty, synth.weights(ty, n, k, synth.seed_for(cfg, li, pi)), k, n, device=dev)
-                y = torch.empty(512 * n, device=dev)
-                keep.append(w)
-                items.append((xs[g], w, y))
-                q_items.append((acts[g], w, y))
+        items, q_items, keep = prefill_set(rq, synth, torch, dev, layer, nl, 3 if nl > 1 else 4, gen)
         ops = sum(2 * 512 * n * k for _, _, n, k in layer) * nl
         # warm-up long enough for the clocks to settle (~30 ms of load)
         steps, warm = (20, 40) if nl > 1 else (40, 80)

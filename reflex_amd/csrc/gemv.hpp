@@ -32,13 +32,6 @@
 #pragma once
 #include "common.hpp"
 
-// Phase probes: empty in the library; a timing harness defines them.
-#ifndef GEMV_PROBE
-#define GEMV_PROBE_BEGIN()
-#define GEMV_PROBE(i)
-#define GEMV_PROBE_END()
-#define GEMV_PROBE_WAIT()
-#endif
 
 struct GemvDesc {
     const uint8_t* w;  // raw blocks, row-major [n][k / QK]
@@ -561,14 +554,12 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
     // (the previous segment's are drained here), and results go to LDS and
     // are stored after the last wait.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    GEMV_PROBE_BEGIN();
     XRegs xr;
     gemv_x_load(dsc.x, k, xr, tid);
 #pragma unroll
     for (int t = 0; t < kRing; t++) issue(t);
     if (restage) lds_barrier();  // every wave is done with the previous segment's x
     const float y_scale = gemv_stage_x(dsc.x, k, T::XHI, xr, lds_x, lds_s, lds_p, tid);
-    GEMV_PROBE(0);
 
     // f16 1024.0 in both halves, kept in a VGPR: gfx9 VOP3 takes at most one
     // SGPR/constant, so (v & mask) | magic is one v_and_or_b32 only this way
@@ -587,7 +578,6 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
                 // most those of the other kRing - 1 slots are outstanding
                 // (stores issued since only make this wait longer)
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRing - 1) * NJ) : "memory");
-                GEMV_PROBE_WAIT();
                 const typename T::Raw rr = T::fetch(ring[t], uo + sh, unit);
                 issue(t);  // the slot's reads are done (fetch waits for them): refill it during the math
                 float acc = T::dot(rr, unit, xv, magic);
@@ -605,15 +595,12 @@ RFXQ_DEV void gemv_rows(const GemvDesc& dsc, uint32_t row_begin, uint32_t row_en
             }
         }
     }
-    GEMV_PROBE(1);
     // no copy may land in LDS after the workgroup is gone (or in the next
     // segment's reads)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     for (uint32_t i = tid; i < row_end - row_begin; i += 256u)
         bst4f(yr, (row_begin + i) * 4u, __builtin_bit_cast(float, lds_ld32(out0 + 4u * i)) * y_scale);
-    GEMV_PROBE(2);
-    GEMV_PROBE_END();
 }
 
 template <typename T>

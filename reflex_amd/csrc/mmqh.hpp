@@ -46,13 +46,6 @@
 #include "common.hpp"
 #include "mmq.hpp"
 
-// Phase probes of the tile loops: empty in the library; a timing harness
-// defines them to accumulate cycle counts per phase.
-#ifndef MMQH_PROBE
-#define MMQH_PROBE_BEGIN()
-#define MMQH_PROBE(i)
-#define MMQH_PROBE_END()
-#endif
 
 namespace mmqh {
 
@@ -363,7 +356,6 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     }
     stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
     __syncthreads();
-    MMQH_PROBE_BEGIN();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
         for (uint32_t g = 0; g < 4u; g++) {
@@ -390,7 +382,6 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                     acc[i][1] = mfma16(cop[1], sxo, acc[i][1]);
                 }
             }
-            MMQH_PROBE(0);
             uint32_t sm[2][2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
@@ -452,14 +443,10 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            MMQH_PROBE(1);
             store_act(st + 1u);
-            MMQH_PROBE(2);
             __syncthreads();
-            MMQH_PROBE(3);
         }
     }
-    MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
@@ -623,7 +610,6 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     }
     stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
     __syncthreads();
-    MMQH_PROBE_BEGIN();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
         for (uint32_t g = 0; g < 4u; g++) {
@@ -638,7 +624,6 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
             load_w(st + 1u);
             load_act(st + 1u);
             const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
-            MMQH_PROBE(0);
             // groups A (e = 0) and B (e = 1): multipliers i = 4n + s + 2e
             uint32_t sm[2][2];
 #pragma unroll
@@ -704,14 +689,10 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            MMQH_PROBE(1);
             store_act(st + 1u);
-            MMQH_PROBE(2);
             __syncthreads();
-            MMQH_PROBE(3);
         }
     }
-    MMQH_PROBE_END();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);

@@ -14,14 +14,6 @@
 #pragma once
 #include "common.hpp"
 
-// Phase probes of rfxq_moe_plan: empty in the library; a timing harness
-// defines them.
-#ifndef MOE_PLAN_PROBE
-#define MOE_PLAN_PROBE(i)
-#endif
-#ifndef MOE_ROUTE_PROBE
-#define MOE_ROUTE_PROBE(i)
-#endif
 
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_gather(const float* __restrict__ src,
                                                                  const uint32_t* __restrict__ perm_row,
@@ -138,7 +130,6 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
                                                 int32_t* __restrict__ idx, float* __restrict__ wts, RouteLds& L) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const float* l = logits + (uint64_t)t * E;
-    MOE_ROUTE_PROBE(0);
     // max (exact in any order)
     float mx = -INFINITY;
     for (uint32_t e = tid; e < E; e += G) {
@@ -156,7 +147,6 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
     for (uint32_t w = 1; w < G / 64u; w++) mx = fmaxf(mx, L.red[w]);
     for (uint32_t e = tid; e < E; e += G) L.pv[e] = expf(L.pv[e] - mx);
     __syncthreads();
-    MOE_ROUTE_PROBE(1);
     if (wave == 0u) {
         float sum = 0.0f;
         for (uint32_t e = lane; e < E; e += 64u) sum += L.pv[e];
@@ -203,7 +193,6 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
         }
     }
     __syncthreads();
-    MOE_ROUTE_PROBE(2);
     if (tid < k) {
         float top_sum = 0.0f;  // in selection order
         for (uint32_t s2 = 0; s2 < k; s2++) top_sum += L.slot_p[s2];
@@ -297,7 +286,6 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
             moe_route_token<1024>(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
                                   const_cast<float*>(a.wts), L);
     }
-    MOE_PLAN_PROBE(1);
     // Stable counting sort of the pairs by expert: the pairs' experts and
     // weights read once into LDS; a histogram and its exclusive scan give each
     // expert's first position; then, chunk by chunk, a pair's rank among the
@@ -316,7 +304,6 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         pw[i] = a.wts[i];
     }
     __syncthreads();
-    MOE_PLAN_PROBE(2);
     for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[pe[i]], 1u);
     __syncthreads();
     __shared__ uint32_t tot[16];
@@ -327,7 +314,6 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         start[tid] = first;
         cnt[tid] = hist;
     }
-    MOE_PLAN_PROBE(3);
     for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
         for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
         __syncthreads();
@@ -384,7 +370,6 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         __syncthreads();  // (the next chunk clears wcnt)
     }
     __syncthreads();
-    MOE_PLAN_PROBE(4);
     if (a.gemv_gu) return;  // the GEMV form runs no MMQ launch
     // per expert (one thread each): rows, tiles; workgroup offsets by
     // exclusive scans over the experts
@@ -440,5 +425,4 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         u->wg_begin = wg_gu + tm * tn_f;
         d->wg_begin = wg_dn;
     }
-    MOE_PLAN_PROBE(5);
 }
