@@ -57,11 +57,64 @@ template <int MT>
 struct Tile {
     static constexpr uint32_t BM = 32u * MT;
     static constexpr uint32_t kAct = BM * 128u;  // activation stage: BM rows x 64 f16
-    static constexpr uint32_t kSx = BM * 32u;    // Q4_K: the super-block's Sx records of BM rows
-    static constexpr uint32_t kScale = BM * 4u;  // the rows' scales 2^e (f32), for the stores
-    static constexpr uint32_t kLds = 2u * kAct + kSx + kScale;
 };
-static_assert(Tile<4>::kLds <= 81920, "two workgroups per CU");
+
+// Tile pipeline. Activations (and Q4_K's Sx records) are copied straight
+// into LDS (buffer_load ... lds) kActDepth - 1 stages ahead, into
+// kActDepth stage buffers that are distinct LDS objects, so that the
+// compiler's wait counting sees that a stage's reads do not alias the copies
+// in flight; weights go to registers WA stages ahead (2, or 1 where two
+// stages of weight registers would not fit). Stage s issues stage s + WA's
+// weight loads, then stage s + 3's copies (with the Sx records when s + 3
+// starts a super-block). A stage ends with a counted wait for the next
+// stage's copies, which were issued two stages earlier, and a barrier; the
+// count is the operations issued after them, fixed by the stage's position g
+// in its super-block because every stage issues the same loads whatever its
+// position in the range (the last stage's data again past the range's end).
+// The prologue issues the copies of stages 0-2 and the weights of stages
+// 0..WA-1 in the same order (copies 0, 1, weights 0, copies 2 for WA = 1;
+// copies 0, weights 0, copies 1, weights 1, copies 2 for WA = 2). W0..W3:
+// vector-memory operations of a stage's weight loads at positions 0..3; SX:
+// 1 when the Sx records are copied.
+constexpr int kActDepth = 4;
+struct ActLds {
+    u4_t* a[kActDepth];  // stage buffers, BM x 128 bytes each
+    u4_t* sx;            // the Sx records of one super-block: one 16-byte piece per thread
+    float* sc;           // the rows' scales 2^e, for the stores
+};
+template <int N>
+RFXQ_DEV void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int MT, int WA, int W0, int W1, int W2, int W3, int SX>
+struct StagePipe {
+    static_assert(WA == 1 || WA == 2, "weights one or two stages ahead");
+    static constexpr int w_at(int p) { return p == 0 ? W0 : p == 1 ? W1 : p == 2 ? W2 : W3; }
+    static constexpr int issued(int g) {  // operations stage g issues
+        return w_at((g + WA) & 3) + MT + (((g + 3) & 3) == 0 ? SX : 0);
+    }
+    // after stage 0's copies (with its Sx): the weights of stages 0..WA-1,
+    // the copies of stages 1 and 2
+    static constexpr int kPrologue = W0 + (WA == 2 ? W1 : 0) + 2 * MT;
+    // after stage g + 1's copies: stage g - 1's and stage g's operations
+    static constexpr int after(int g) { return issued((g + 3) & 3) + issued(g); }
+    static_assert(after(2) <= 63 && kPrologue <= 63, "vmcnt holds 6 bits");
+    RFXQ_DEV static void prologue_end() {
+        vm_wait<kPrologue>();
+        lds_barrier();
+    }
+    RFXQ_DEV static void stage_end(uint32_t g) {
+        if (g == 0u) vm_wait<after(0)>();
+        else if (g == 1u) vm_wait<after(1)>();
+        else if (g == 2u) vm_wait<after(2)>();
+        else vm_wait<after(3)>();
+        lds_barrier();
+    }
+};
+// the activation chunk a lane copies: LDS chunk c of row r holds logical
+// chunk c ^ ((r / 2) % 8), and a wave's copy writes its lanes' 16-byte
+// pieces in lane order (piece tid = chunk tid % 8 of row tid / 8)
+RFXQ_DEV uint32_t act_chunk(uint32_t tid) { return (tid & 7u) ^ ((tid >> 4) & 7u); }
 
 // f16 of an f32, round to nearest even, as the low 16 bits
 RFXQ_DEV uint32_t f16_rne(float v) { return __builtin_bit_cast(uint16_t, (half_t)v); }
@@ -168,13 +221,6 @@ RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col
     }
 }
 
-// the rows' scales 2^e into LDS (read by store_tile); visible after the
-// first barrier of the tile loop
-RFXQ_DEV void stage_row_scales(const MmqDesc& ds, uint32_t m0, uint32_t bm, float* sc_lds) {
-    const uint32_t t = threadIdx.x;
-    if (t < bm) sc_lds[t] = m0 + t < ds.m ? ds.xrs[act_row(ds, m0 + t)] : 0.0f;
-}
-
 // Workgroup b of a g-workgroup launch as a tile index such that the tiles
 // each XCD runs are contiguous: workgroups go round-robin to the 8 XCDs, and
 // neighbouring tiles (the row tiles of one column tile, then the next column
@@ -263,9 +309,12 @@ RFXQ_DEV u4_t q6k_multipliers(u4_t sc, uint32_t dbits, uint32_t h) {
 
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q4_K weights.
 template <int MT>
-RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& L) {
     using namespace mmqh;
-    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
+    constexpr uint32_t BM = Tile<MT>::BM;
+    // weight loads per stage: two code pieces, and the headers at position 0
+    constexpr int WA = 2;
+    using Pipe = StagePipe<MT, WA, 4, 2, 2, 2, 1>;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nsb = ds.k / 256u;
@@ -273,7 +322,6 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const uint32_t sb1 = min(nsb, sb0 + ds.sb_per_split);
     const uint32_t row_bytes = nsb * 144u;
     const uint32_t rec_bytes = nsb * 32u;
-    uint8_t* const sx_lds = lds + 2u * kAct;
 
     // Buffers start at the tile (tile_base): 32-bit offsets for any matrix
     // size. Weight columns past the matrix read past the buffer: zeros, no
@@ -283,15 +331,17 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const rsrc_t r_w = make_rsrc(ds.w + (uint64_t)n0 * row_bytes, min(BN, ds.n - n0) * row_bytes);
     const rsrc_t r_sx =
         make_rsrc(reinterpret_cast<const uint8_t*>(ds.xds) + (uint64_t)rb * rec_bytes, 0xFFFFFFFFu);
-    // Staged activations: piece 256u + tid is chunk tid%8 of row 32u + tid/8
-    // (LDS + 4096u); LDS chunk c of row r holds logical chunk c ^ ((r/2)%8).
-    // Sx: half tid%2 of row tid/2 (threads below 2 BM).
-    const uint32_t ra = tid >> 3, ca = tid & 7u;
+    // Staged activations, copied straight into LDS (buffer_load ... lds: the
+    // 64 lanes of a wave write 1 KB in lane order): piece 256u + tid of a
+    // stage buffer is chunk tid%8 of row 32u + tid/8; LDS chunk c of row r
+    // holds logical chunk c ^ ((r/2)%8), so the lane fetches that one.
+    // Sx: piece tid = half tid%2 of row tid/2 (rows past the tile's BM repeat
+    // its last row; never read).
+    const uint32_t ra = tid >> 3;
     uint32_t g_act[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * ca;
-    const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
-    const uint32_t g_sx = (act_row(ds, m0 + (tid >> 1)) - rb) * rec_bytes + 16u * (tid & 1u);
+    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * act_chunk(tid);
+    const uint32_t g_sx = (act_row(ds, m0 + min(tid >> 1, BM - 1u)) - rb) * rec_bytes + 16u * (tid & 1u);
     // Weights go straight to registers (no other wave reads a wave's
     // columns): lane (l32, h) of n-tile j loads, per stage, half h of the 32
     // quant bytes of column 64w + 32j + l32, and that column's 16-byte
@@ -305,33 +355,30 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     }
     const uint32_t nst = 4u * (sb1 - sb0);
 
-    // Loads are issued unconditionally so that the compiler's wait counts stay
-    // exact across the loop: past the last stage a lane reloads the last stage
-    // (in bounds; never used).
-    const bool sx_lane = tid < 2u * BM;
-    u4_t sa[MT], ssx, qn[2], hn[2];
-    auto load_act = [&](uint32_t st) {
+    // Every stage issues the same copies and loads whatever its position, so
+    // the wait counts below hold: past the last stage a lane copies the last
+    // stage again (in bounds; into a buffer no stage reads any more).
+    // Activations run kActDepth - 1 stages ahead, weights one.
+    auto copy_act = [&](uint32_t st, u4_t* buf, bool sx) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
         for (int u = 0; u < MT; u++)
-            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 128u * g, 0);
-        if ((st & 3u) == 0u && sx_lane) ssx = __builtin_amdgcn_raw_buffer_load_b128(r_sx, g_sx, 32u * sb, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, RFXQ_LDSP(buf + 256u * u + 64u * w), 16, g_act[u],
+                                                     512u * sb + 128u * g, 0, 0);
+        if (sx)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_sx, RFXQ_LDSP(L.sx + 64u * w), 16, g_sx, 32u * sb, 0, 0);
     };
-    auto load_w = [&](uint32_t st) {
+    u4_t qn[WA][2], hn[2];  // weights of WA stages (by stage), a super-block's headers
+    auto load_w = [&](uint32_t st, bool hdr) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
-        for (int j = 0; j < 2; j++) qn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], 144u * sb + 32u * g, 0);
-        if ((st & 3u) == 0u)
+        for (int j = 0; j < 2; j++)
+            qn[st % WA][j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_q[j], 144u * sb + 32u * g, 0);
+        if (hdr)
 #pragma unroll
             for (int j = 0; j < 2; j++) hn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_h[j], 144u * sb, 0);
-    };
-    auto store_act = [&](uint32_t st) {
-        uint8_t* S = lds + (st & 1u) * kAct;
-#pragma unroll
-        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
-        if ((st & 3u) == 0u && sx_lane) reinterpret_cast<u4_t*>(sx_lds)[tid] = ssx;
     };
 
     v16f_t acc[MT][2];
@@ -349,13 +396,23 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mg = 0x64006400u;
     asm("" : "+v"(mlo), "+v"(mhi), "+v"(mg));
 
-    if (nst > 0u) {
-        load_w(0u);
-        load_act(0u);
-        store_act(0u);
+    // the rows' scales 2^e (for the stores) read now, written to LDS after
+    // the loop: a buffer load, so no wait before the first stage covers them
+    float row_scale = 0.0f;
+    if (tid < BM && m0 + tid < ds.m)
+        row_scale = as_f32(bld4(make_rsrc(ds.xrs, 0xFFFFFFFFu), 4u * act_row(ds, m0 + tid)));
+    // prologue: stages 0-2 copied (with stage 0's Sx), stage 0's weights
+    copy_act(0u, L.a[0], true);
+    if constexpr (WA == 1) {
+        copy_act(1u, L.a[1], false);
+        load_w(0u, true);
+    } else {
+        load_w(0u, true);
+        copy_act(1u, L.a[1], false);
+        load_w(1u, false);
     }
-    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
-    __syncthreads();
+    copy_act(2u, L.a[2], false);
+    Pipe::prologue_end();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
         for (uint32_t g = 0; g < 4u; g++) {
@@ -363,12 +420,16 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
             u4_t hdr[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                q[j] = qn[j];
+                q[j] = qn[g % WA][j];
                 if (g == 0u) hdr[j] = hn[j];
             }
-            load_w(st + 1u);
-            load_act(st + 1u);
-            const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
+            // stage st + 1's weights, then stage st + 3 into the buffer stage
+            // st - 1 used (every wave is past it: the barrier that ended
+            // stage st - 1), with its Sx when it starts a super-block. (The
+            // weights first: their use next stage then waits only for them.)
+            load_w(st + WA, ((g + WA) & 3u) == 0u);
+            copy_act(st + 3u, L.a[(g + 3u) & 3u], g == 1u);
+            const u4_t* S16 = L.a[g];
             if (g == 0u) {
                 // super-block start: the columns' multipliers, and the
                 // constant part C_b * Sx_b into the accumulators
@@ -377,7 +438,7 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 for (int j = 0; j < 2; j++) q4k_sb_operands(hdr[j], cop[j], dsc[j]);
 #pragma unroll
                 for (int i = 0; i < MT; i++) {
-                    const u4_t sxo = reinterpret_cast<const u4_t*>(sx_lds)[2u * (32u * i + l32) + h];
+                    const u4_t sxo = L.sx[2u * (32u * i + l32) + h];
                     acc[i][0] = mfma16(cop[0], sxo, acc[i][0]);
                     acc[i][1] = mfma16(cop[1], sxo, acc[i][1]);
                 }
@@ -443,31 +504,36 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            store_act(st + 1u);
-            __syncthreads();
+            // stage st + 1's copies done (issued two stages ago; after them
+            // came stage st - 1's and stage st's copies and loads), then every
+            // wave past this stage's reads
+            Pipe::stage_end(g);
         }
     }
+    // no copy may land in LDS after the workgroup is gone
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid < BM) L.sc[tid] = row_scale;
+    lds_barrier();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], L.sc + 32u * i + 4u * h);
 }
 
 template <int MT>
-RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds);
+RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& ls);
 template <int MT>
-RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds);
+RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& lds);
 
 // One (32 MT)x256 tile (and one split-K range): the descriptor made uniform,
 // the tile decoded, and the rows computed by the body of as many 32-row tiles
 // as the tile has rows (a ragged last tile, or an expert group of 33 rows in
 // a 64-row tile, runs no MFMAs on absent rows).
 template <int MT, int TY>
-RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
+RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, const mmqh::ActLds& lds) {
     MmqDesc ds = dv;
     {
         uint32_t* p = reinterpret_cast<uint32_t*>(&ds);
@@ -500,13 +566,19 @@ RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, uint8_t* lds) {
 // the XCDs that own the tail of the tile range without work.
 #define RFXQ_MMQH_ENTRY(NAME, TILE, MT, WPE)                                                                \
     extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
-        __shared__ __attribute__((aligned(16))) uint8_t lds[mmqh::Tile<MT>::kLds];                            \
+        __shared__ __attribute__((aligned(16))) u4_t a0[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a1[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a2[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a3[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t sx[mmqh::kThreads];                                     \
+        __shared__ __attribute__((aligned(16))) float sc[mmqh::Tile<MT>::BM];                                \
         if (blockDim.x != mmqh::kThreads) return; /* the tile assumes exactly kThreads lanes */               \
         const uint32_t tiles = min(gridDim.x, mmq_tile_count(args));                                        \
         if (blockIdx.x >= tiles) return;                                                                     \
         const uint32_t b = mmqh::xcd_tile(blockIdx.x, tiles);                                               \
         const MmqDesc d = mmq_pick(args, b);                                                                 \
         if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;                                     \
+        const mmqh::ActLds lds{{a0, a1, a2, a3}, sx, sc};                                                    \
         mmqh_tile<MT, TILE>(d, b - d.wg_begin, lds);                                                          \
     }
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k, TY_Q4K, 4, 2)
@@ -516,9 +588,13 @@ RFXQ_MMQH_ENTRY(rfxq_mmqh_q4k_m64, TY_Q4K, 2, 3)
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q6_K weights:
 // the Q4_K tile's layout and pipeline, with the Q6_K weight operands.
 template <int MT>
-RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& ls) {
     using namespace mmqh;
-    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
+    constexpr uint32_t BM = Tile<MT>::BM;
+    // weight loads per stage: the ql pieces; the qh pieces at even positions;
+    // the scales and d at position 0
+    constexpr int WA = MT == 4 ? 1 : 2;  // (128-row tiles: two stages of registers would spill)
+    using Pipe = StagePipe<MT, WA, 8, 2, 4, 2, 0>;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nsb = ds.k / 256u;
@@ -535,14 +611,13 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     const uint32_t rb = act_base(ds, m0);
     const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
     const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), min(BN, ds.n - n0) * row_bytes + sh0);
-    const uint32_t ra = tid >> 3, ca = tid & 7u;
+    const uint32_t ra = tid >> 3;
     // activations: the Q4_K tile's staging, but the stage's logical chunks 4-7
     // (group B) sit 128 bytes after chunks 0-3 (group A) in the f16 row
     uint32_t g_act[MT];
-    const uint32_t cofs = 16u * ca + (ca >= 4u ? 64u : 0u);
+    const uint32_t lc = act_chunk(tid), cofs = 16u * lc + (lc >= 4u ? 64u : 0u);
 #pragma unroll
     for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + cofs;
-    const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
     // Weights straight to registers: lane (l32, h) of n-tile j loads, per
     // stage, positions [16h, 16h + 16) of the ql and qh pieces of column
     // 64w + 32j + l32 (five dwords each), and with the first stage of a
@@ -555,15 +630,18 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     }
     const uint32_t nst = 4u * (sb1 - sb0);
 
-    u4_t sa[MT], qln[2], qhn[2], scn[2];
+    // ql pieces of WA stages (by stage); qh, scales and d are copied out in
+    // the stage that issues their next load
+    u4_t qln[WA][2], qhn[2], scn[2];
     uint32_t dn[2];
-    auto load_act = [&](uint32_t st) {
+    auto copy_act = [&](uint32_t st, u4_t* buf) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
         const uint32_t n = g >> 1, s = g & 1u;
 #pragma unroll
         for (int u = 0; u < MT; u++)
-            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 256u * n + 64u * s, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, RFXQ_LDSP(buf + 256u * u + 64u * w), 16, g_act[u],
+                                                     512u * sb + 256u * n + 64u * s, 0, 0);
     };
     // 16-byte loads at 2-byte-aligned offsets (unaligned access mode)
     auto load_w = [&](uint32_t st) {
@@ -574,7 +652,7 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
         // the qh piece of half n serves both of its stages: loaded with s = 0
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            qln[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], base + 64u * n + 32u * s, 0);
+            qln[st % WA][j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], base + 64u * n + 32u * s, 0);
             if ((st & 1u) == 0u) qhn[j] = __builtin_amdgcn_raw_buffer_load_b128(r_w, g_c[j], base + 128u + 32u * n, 0);
         }
         if ((st & 3u) == 0u) {
@@ -584,11 +662,6 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 dn[j] = __builtin_amdgcn_raw_buffer_load_b16(r_w, g_c[j] - 16u * h, base + 208u, 0);
             }
         }
-    };
-    auto store_act = [&](uint32_t st) {
-        uint8_t* S = lds + (st & 1u) * kAct;
-#pragma unroll
-        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
     };
 
     v16f_t acc[MT][2];
@@ -603,13 +676,19 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     uint32_t mla = 0x000F000Fu, mqa = 0x00300030u, mlb = 0x00F000F0u, mqb = 0x03000300u, mg = 0x64006400u;
     asm("" : "+v"(mla), "+v"(mqa), "+v"(mlb), "+v"(mqb), "+v"(mg));
 
-    if (nst > 0u) {
+    float row_scale = 0.0f;  // written to LDS after the loop (as for Q4_K)
+    if (tid < BM && m0 + tid < ds.m) row_scale = as_f32(bld4(make_rsrc(ds.xrs, 0xFFFFFFFFu), 4u * act_row(ds, m0 + tid)));
+    copy_act(0u, ls.a[0]);
+    if constexpr (WA == 1) {
+        copy_act(1u, ls.a[1]);
         load_w(0u);
-        load_act(0u);
-        store_act(0u);
+    } else {
+        load_w(0u);
+        copy_act(1u, ls.a[1]);
+        load_w(1u);
     }
-    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
-    __syncthreads();
+    copy_act(2u, ls.a[2]);
+    Pipe::prologue_end();
     for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
         for (uint32_t g = 0; g < 4u; g++) {
@@ -617,13 +696,13 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
             const uint32_t n = g >> 1, s = g & 1u;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                L[j] = qln[j];
+                L[j] = qln[g % WA][j];
                 if (s == 0u) Q[j] = qhn[j];
                 if (g == 0u) mult[j] = q6k_multipliers(scn[j], dn[j], h);
             }
-            load_w(st + 1u);
-            load_act(st + 1u);
-            const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
+            load_w(st + WA);
+            copy_act(st + 3u, ls.a[(g + 3u) & 3u]);
+            const u4_t* S16 = ls.a[g];
             // groups A (e = 0) and B (e = 1): multipliers i = 4n + s + 2e
             uint32_t sm[2][2];
 #pragma unroll
@@ -689,13 +768,16 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            store_act(st + 1u);
-            __syncthreads();
+            Pipe::stage_end(g);
         }
     }
+    // no copy may land in LDS after the workgroup is gone
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid < BM) ls.sc[tid] = row_scale;
+    lds_barrier();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
+    const float* sc = ls.sc;
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
@@ -740,9 +822,13 @@ RFXQ_DEV u2_t q80_codes_f16(uint32_t v, h2_t dv, uint32_t mg) {
 // One (32 MT)x256 tile (and one split-K range) of Y = X . W^T for Q8_0 weights:
 // the Q4_K tile's activation staging and MFMA schedule, with Q8_0 operands.
 template <int MT, bool AL>
-RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& ls) {
     using namespace mmqh;
-    constexpr uint32_t BM = Tile<MT>::BM, kAct = Tile<MT>::kAct;
+    constexpr uint32_t BM = Tile<MT>::BM;
+    // weights two stages ahead in the 96- and 128-row bodies; one in the
+    // smaller ones, whose entries cap the registers lower
+    constexpr int WA = MT >= 3 ? 2 : 1;
+    using Pipe = StagePipe<MT, WA, 8, 8, 8, 8, 0>;  // weight loads: four per column and stage
     const uint32_t tid = threadIdx.x, lane = tid & 63u, l32 = lane & 31u, h = lane >> 5;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nsb = ds.k / 256u;
@@ -756,11 +842,10 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
     const uint32_t rb = act_base(ds, m0);
     const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
     const rsrc_t r_w = make_rsrc(reinterpret_cast<const void*>(wa - sh0), min(BN, ds.n - n0) * row_bytes + sh0);
-    const uint32_t ra = tid >> 3, ca = tid & 7u;
+    const uint32_t ra = tid >> 3;
     uint32_t g_act[MT];
 #pragma unroll
-    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * ca;
-    const uint32_t l_act = ra * 128u + 16u * (ca ^ ((ra >> 1) & 7u));
+    for (int u = 0; u < MT; u++) g_act[u] = (act_row(ds, m0 + ra + 32u * u) - rb) * ds.ldq + 16u * act_chunk(tid);
     // lane (l32, h) of n-tile j: column 64w + 32j + l32, codes [16h, +16) of
     // each block, and each block's d
     // (the lane-varying parts of an offset go in the VGPR offset: a
@@ -774,20 +859,24 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
     const uint32_t e_off = h ? 0u : 32u;  // aligned form: the dword with the other half's d
     const uint32_t nst = 4u * (sb1 - sb0);
 
-    // raw stage data per column: unaligned form qn = codes of blocks 0, 1 and
-    // dn = their d; aligned form qn[0] = bytes [16h, +16), qn[1] = bytes
-    // [36 + 16h, +16), dn[0] = the dword after qn[0], dn[1] = the other d's dword
-    u4_t sa[MT], qn[2][2];
-    uint32_t dn[2][2];
-    auto load_act = [&](uint32_t st) {
+    // raw stage data per column, of two stages (by stage parity): unaligned
+    // form qn = codes of blocks 0, 1 and dn = their d; aligned form qn[0] =
+    // bytes [16h, +16), qn[1] = bytes [36 + 16h, +16), dn[0] = the dword after
+    // qn[0], dn[1] = the other d's dword
+    u4_t qn_[WA][2][2];
+    uint32_t dn_[WA][2][2];
+    auto copy_act = [&](uint32_t st, u4_t* buf) {
         const uint32_t sl = min(st, nst - 1u);
         const uint32_t sb = sb0 + (sl >> 2), g = sl & 3u;
 #pragma unroll
         for (int u = 0; u < MT; u++)
-            sa[u] = __builtin_amdgcn_raw_buffer_load_b128(r_act, g_act[u], 512u * sb + 128u * g, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, RFXQ_LDSP(buf + 256u * u + 64u * w), 16, g_act[u],
+                                                     512u * sb + 128u * g, 0, 0);
     };
     auto load_w = [&](uint32_t st) {
         const uint32_t sl = min(st, nst - 1u);
+        auto& qn = qn_[st % WA];
+        auto& dn = dn_[st % WA];
         const uint32_t blk = 8u * sb0 + 2u * sl;  // the stage's first block in the row
         if constexpr (AL) {
             const uint32_t o = 34u * blk;  // dword aligned (blk is even)
@@ -809,11 +898,6 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
                 }
         }
     };
-    auto store_act = [&](uint32_t st) {
-        uint8_t* S = lds + (st & 1u) * kAct;
-#pragma unroll
-        for (int u = 0; u < MT; u++) *reinterpret_cast<u4_t*>(S + l_act + 4096u * u) = sa[u];
-    };
 
     v16f_t acc[MT][2];
 #pragma unroll
@@ -826,89 +910,104 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
     uint32_t mg = 0x64646464u, sgn = 0x80808080u;
     asm("" : "+v"(mg), "+v"(sgn));
 
-    if (nst > 0u) {
+    float row_scale = 0.0f;  // written to LDS after the loop (as for Q4_K)
+    if (tid < BM && m0 + tid < ds.m) row_scale = as_f32(bld4(make_rsrc(ds.xrs, 0xFFFFFFFFu), 4u * act_row(ds, m0 + tid)));
+    copy_act(0u, ls.a[0]);
+    if constexpr (WA == 1) {
+        copy_act(1u, ls.a[1]);
         load_w(0u);
-        load_act(0u);
-        store_act(0u);
+    } else {
+        load_w(0u);
+        copy_act(1u, ls.a[1]);
+        load_w(1u);
     }
-    stage_row_scales(ds, m0, BM, reinterpret_cast<float*>(lds + 2u * kAct + Tile<MT>::kSx));
-    __syncthreads();
-    for (uint32_t st = 0; st < nst; st++) {
-        u4_t q[2][2];
-        h2_t dv[2][2];
+    copy_act(2u, ls.a[2]);
+    Pipe::prologue_end();
+    for (uint32_t st0 = 0; st0 < nst; st0 += 4u) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            if constexpr (AL) {
-                const u4_t a = qn[j][0];
-                const uint32_t b = dn[j][0], e = dn[j][1];
-                q[j][0] = u4_t{alignbyte(a.y, a.x, 2u), alignbyte(a.z, a.y, 2u), alignbyte(a.w, a.z, 2u),
-                               alignbyte(b, a.w, 2u)} ^ u4_t{sgn, sgn, sgn, sgn};
-                q[j][1] = qn[j][1] ^ u4_t{sgn, sgn, sgn, sgn};
-                dv[j][0] = as_h2(splat16<0>(h ? e : a.x));
-                dv[j][1] = as_h2(h ? splat16<1>(b) : splat16<1>(e));
-            } else {
+        for (uint32_t g = 0; g < 4u; g++) {
+            const uint32_t st = st0 + g;
+            const auto& qn = qn_[g % WA];
+            const auto& dn = dn_[g % WA];
+            u4_t q[2][2];
+            h2_t dv[2][2];
 #pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    q[j][e] = qn[j][e] ^ u4_t{sgn, sgn, sgn, sgn};
-                    dv[j][e] = as_h2(splat16<0>(dn[j][e]));
+            for (int j = 0; j < 2; j++) {
+                if constexpr (AL) {
+                    const u4_t a = qn[j][0];
+                    const uint32_t b = dn[j][0], e = dn[j][1];
+                    q[j][0] = u4_t{alignbyte(a.y, a.x, 2u), alignbyte(a.z, a.y, 2u), alignbyte(a.w, a.z, 2u),
+                                   alignbyte(b, a.w, 2u)} ^ u4_t{sgn, sgn, sgn, sgn};
+                    q[j][1] = qn[j][1] ^ u4_t{sgn, sgn, sgn, sgn};
+                    dv[j][0] = as_h2(splat16<0>(h ? e : a.x));
+                    dv[j][1] = as_h2(h ? splat16<1>(b) : splat16<1>(e));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        q[j][e] = qn[j][e] ^ u4_t{sgn, sgn, sgn, sgn};
+                        dv[j][e] = as_h2(splat16<0>(dn[j][e]));
+                    }
                 }
             }
+            load_w(st + WA);
+            copy_act(st + 3u, ls.a[(g + 3u) & 3u]);
+            const u4_t* S16 = ls.a[g];
+            auto wop = [&](int t, int j) {
+                const int e = t >> 1, s2 = t & 1;
+                const u2_t lo = q80_codes_f16(q[j][e][2 * s2], dv[j][e], mg);
+                const u2_t hi = q80_codes_f16(q[j][e][2 * s2 + 1], dv[j][e], mg);
+                return u4_t{lo.x, lo.y, hi.x, hi.y};
+            };
+            u4_t Xc[MT], Wc[2];
+#pragma unroll
+            for (int i = 0; i < MT; i++) Xc[i] = S16[256u * i + a_act[0][0]];
+            Wc[0] = wop(0, 0);
+            Wc[1] = wop(0, 1);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                u4_t Xn[MT], Wn[2];
+                if (t < 3) {
+                    const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
+#pragma unroll
+                    for (int i = 0; i < MT; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
+                    Wn[0] = wop(t + 1, 0);
+                    Wn[1] = wop(t + 1, 1);
+                }
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
+                    acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
+                }
+                if (t < 3) {
+#pragma unroll
+                    for (int u = 0; u < MT; u++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                    }
+#pragma unroll
+                    for (int u = 0; u < MT; u++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < MT; i++) Xc[i] = Xn[i];
+                    Wc[0] = Wn[0];
+                    Wc[1] = Wn[1];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            Pipe::stage_end(g);
         }
-        load_w(st + 1u);
-        load_act(st + 1u);
-        const u4_t* S16 = reinterpret_cast<const u4_t*>(lds + (st & 1u) * kAct);
-        auto wop = [&](int t, int j) {
-            const int e = t >> 1, s2 = t & 1;
-            const u2_t lo = q80_codes_f16(q[j][e][2 * s2], dv[j][e], mg);
-            const u2_t hi = q80_codes_f16(q[j][e][2 * s2 + 1], dv[j][e], mg);
-            return u4_t{lo.x, lo.y, hi.x, hi.y};
-        };
-        u4_t Xc[MT], Wc[2];
-#pragma unroll
-        for (int i = 0; i < MT; i++) Xc[i] = S16[256u * i + a_act[0][0]];
-        Wc[0] = wop(0, 0);
-        Wc[1] = wop(0, 1);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            u4_t Xn[MT], Wn[2];
-            if (t < 3) {
-                const int e = (t + 1) >> 1, s2 = (t + 1) & 1;
-#pragma unroll
-                for (int i = 0; i < MT; i++) Xn[i] = S16[256u * i + a_act[e][s2]];
-                Wn[0] = wop(t + 1, 0);
-                Wn[1] = wop(t + 1, 1);
-            }
-#pragma unroll
-            for (int i = 0; i < MT; i++) {
-                acc[i][0] = mfma16(Wc[0], Xc[i], acc[i][0]);
-                acc[i][1] = mfma16(Wc[1], Xc[i], acc[i][1]);
-            }
-            if (t < 3) {
-#pragma unroll
-                for (int u = 0; u < MT; u++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-                }
-#pragma unroll
-                for (int u = 0; u < MT; u++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int i = 0; i < MT; i++) Xc[i] = Xn[i];
-                Wc[0] = Wn[0];
-                Wc[1] = Wn[1];
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        store_act(st + 1u);
-        __syncthreads();
     }
+    // no copy may land in LDS after the workgroup is gone
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid < BM) ls.sc[tid] = row_scale;
+    lds_barrier();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    const float* sc = reinterpret_cast<const float*>(lds + 2u * kAct + Tile<MT>::kSx);
+    const float* sc = ls.sc;
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
@@ -917,7 +1016,7 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
 }
 
 template <int MT>
-RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, uint8_t* lds) {
+RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_t ks, const mmqh::ActLds& lds) {
     if ((reinterpret_cast<uintptr_t>(ds.w) & 3u) == 0u) mmqh_q80_rows_t<MT, true>(ds, m0, n0, ks, lds);
     else mmqh_q80_rows_t<MT, false>(ds, m0, n0, ks, lds);
 }
