@@ -82,6 +82,12 @@ struct ActLds {
     u4_t* sx;            // the Sx records of one super-block: one 16-byte piece per thread
     float* sc;           // the rows' scales 2^e, for the stores
 };
+// stage buffer w (wave-uniform) of the pointers, by selects on the values:
+// an index that is not a constant, or a member call, would put the pointers
+// in scratch memory
+RFXQ_DEV u4_t* pick_buf(u4_t* a0, u4_t* a1, u4_t* a2, u4_t* a3, uint32_t w) {
+    return w == 0u ? a0 : w == 1u ? a1 : w == 2u ? a2 : a3;
+}
 template <int N>
 RFXQ_DEV void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -202,9 +208,9 @@ RFXQ_DEV uint32_t act_base(const MmqDesc& ds, uint32_t m0) { return ds.rows ? 0u
 // weights): lane (l32, h) holds weight column l32 and activation rows
 // 8 q4 + 4 h + r (q4, r in [0, 4)) as acc[4 q4 + r]. Stored as dwords: the
 // 32 lanes of a half write one row's 32 consecutive columns (128 contiguous
-// bytes per row and instruction; float4 stores of the transposed layout
-// touched 32 rows per instruction and cost ~16% of the 0.6B prefill set).
-// `row` = the tile's row 4h, `sc` = the LDS scales 2^e of rows row..row+27.
+// bytes per row and instruction). `row` = the tile's row 4h, `sc` = the LDS
+// scales 2^e of rows row..row+27. Outputs are written once and not read
+// back by the kernel: non-temporal stores.
 RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col, const v16f_t& acc,
                          const float* sc) {
     if (col >= ds.n) return;
@@ -216,9 +222,61 @@ RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint32_t m = row + 8u * q4 + r;
-            if (m < ds.m) yc[(uint64_t)m * ds.ldy] = acc[4 * q4 + r] * sv[r];
+            if (m < ds.m) __builtin_nontemporal_store(acc[4 * q4 + r] * sv[r], yc + (uint64_t)m * ds.ldy);
         }
     }
+}
+
+// A wave's MT x 2 accumulator tiles (rows m0 + 32i, columns c0 + 32j) with
+// 16-byte stores: each tile passes through the wave's 4 KB LDS region `buf`
+// (free once the tile loop is over) as a row-major 32x32 array whose column
+// index is xor'ed with 4 (R % 8) in row R (whole float4 groups stay
+// together), and lane (t + 4k, h) then reads and stores row 8q4 + 4h + t,
+// columns 4k..4k+3: eight lanes per 128-byte row piece and a quarter of the
+// dword stores' instructions (4-5% of the 0.6B prefill set). Outputs whose
+// rows are not 16-byte aligned take the dword stores.
+template <int MT>
+RFXQ_DEV void store_wave(const MmqDesc& ds, float* y, uint32_t m0, uint32_t c0, const v16f_t (&acc)[MT][2],
+                         const float* sc, u4_t* buf) {
+    const uint32_t lane = threadIdx.x & 63u, l32 = lane & 31u, h = lane >> 5;
+    if ((ds.ldy & 3u) != 0u || (reinterpret_cast<uintptr_t>(y) & 15u) != 0u) {
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                store_tile(ds, y, m0 + 32u * i + 4u * h, c0 + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+        return;
+    }
+    float* bf = reinterpret_cast<float*>(buf);
+    const uint32_t t = l32 & 3u, k = l32 >> 2;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t R = 8u * q4 + 4u * h + r;
+                    bf[32u * R + (l32 ^ ((R & 7u) << 2))] = acc[i][j][4 * q4 + r];
+                }
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const uint32_t R = 8u * q4 + 4u * h + t;
+                f4v_t v = *reinterpret_cast<const f4v_t*>(bf + 32u * R + ((4u * k) ^ ((R & 7u) << 2)));
+                v *= sc[32u * i + R];
+                const uint32_t m = m0 + 32u * i + R, c = c0 + 32u * j + 4u * k;
+                if (m >= ds.m) continue;
+                float* yr = y + (uint64_t)m * ds.ldy;
+                if (c + 3u < ds.n) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<f4v_t*>(yr + c));
+                } else {
+#pragma unroll
+                    for (uint32_t u = 0; u < 4u; u++)
+                        if (c + u < ds.n) __builtin_nontemporal_store(v[u], yr + c + u);
+                }
+            }
+        }
 }
 
 // Workgroup b of a g-workgroup launch as a tile index such that the tiles
@@ -516,11 +574,7 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     lds_barrier();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], L.sc + 32u * i + 4u * h);
+    store_wave<MT>(ds, y, m0, n0 + 64u * w, acc, L.sc, pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], w));
 }
 
 template <int MT>
@@ -778,11 +832,7 @@ RFXQ_DEV void mmqh_q6k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const float* sc = ls.sc;
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+    store_wave<MT>(ds, y, m0, n0 + 64u * w, acc, sc, pick_buf(ls.a[0], ls.a[1], ls.a[2], ls.a[3], w));
 }
 
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q6k, TY_Q6K, 4, 2)
@@ -1008,11 +1058,7 @@ RFXQ_DEV void mmqh_q80_rows_t(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint3
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
     const float* sc = ls.sc;
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-            store_tile(ds, y, m0 + 32u * i + 4u * h, n0 + 64u * w + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+    store_wave<MT>(ds, y, m0, n0 + 64u * w, acc, sc, pick_buf(ls.a[0], ls.a[1], ls.a[2], ls.a[3], w));
 }
 
 template <int MT>
