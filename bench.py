@@ -47,6 +47,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="skip prefill, 8B and CPU legs")
+    ap.add_argument("--legs", default=None,
+                    help="comma list of the legs to run after the headline (decode_8b, prefill, q8_0, moe); "
+                         "no CPU leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-only", action="store_true",
                     help="only the CPU baseline leg, as one JSON line (no GPU; run by the full bench in a child "
@@ -268,8 +271,12 @@ def main() -> int:
         result["roofline"]["traffic"] = json.load(open(traffic_file)).get("bytes_per_launch")
 
     del plans, copies
-    if not args.quick:
+    legs = {"decode_8b", "prefill", "q8_0", "moe"} if args.legs is None else set(args.legs.split(","))
+    if args.quick:
+        legs = set()
+    if "decode_8b" in legs:
         result["decode_8b"] = decode_8b_leg(rq, synth, torch, np, dev, timed)
+    if "prefill" in legs:
         result["prefill"] = prefill_leg(rq, synth, torch, np, dev, timed)
         # the metric's second half as top-level keys (the config 3 set)
         pf = result["prefill"]["qwen3_06b_m512"]
@@ -279,10 +286,12 @@ def main() -> int:
         result["prefill_ms_per_step"] = pf["ms_per_step"]
         result["prefill_tops_with_act_pass"] = pf["tops_with_act_pass"]
         result["prefill_kernel"] = "rfxq_mmqh_q4k (+ rfxq_mmqh_q6k for v_proj)"
+    if "q8_0" in legs:
         result["q8_0"] = q8_0_leg(rq, synth, torch, np, dev, timed)
+    if "moe" in legs:
         result["moe"] = moe_leg(rq, synth, torch, np, dev, timed)
     torch.cuda.empty_cache()
-    if not args.quick and not args.no_cpu:
+    if not args.quick and not args.no_cpu and args.legs is None:
         # in a child process with the caller's OpenMP settings: the passive
         # waiting set above slows the baseline's many short parallel regions
         import subprocess

@@ -252,6 +252,10 @@ struct MoePlanArgs {
     const float* logits;
     uint32_t normalize;
     float scale;
+    // 1: group the pairs in any order within an expert (places by LDS
+    // atomics, then a prefix sum of the counts); 0: a stable sort (token
+    // order within an expert)
+    uint32_t any_order;
 };
 
 // Exclusive prefix sum of v over the 1024 threads of the workgroup (every
@@ -286,7 +290,8 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
             moe_route_token<1024>(a.logits, t, a.E, a.k, a.normalize, a.scale, const_cast<int32_t*>(a.idx),
                                   const_cast<float*>(a.wts), L);
     }
-    // Stable counting sort of the pairs by expert: the pairs' experts and
+    // Grouping with `any_order` (the grouped MMQ form): below. Otherwise a
+    // stable counting sort of the pairs by expert: the pairs' experts and
     // weights read once into LDS; a histogram and its exclusive scan give each
     // expert's first position; then, chunk by chunk, a pair's rank among the
     // lanes of its wave with the same expert comes from ballots over the
@@ -297,77 +302,116 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
     __shared__ uint32_t base[kRouteMaxE];
     __shared__ uint16_t wcnt[16][kRouteMaxE];
     const uint32_t E = a.E, lane = tid & 63u, wave = tid >> 6;
-    for (uint32_t e = tid; e < E; e += 1024u) base[e] = 0u;
-#pragma unroll 4
-    for (uint32_t i = tid; i < P; i += 1024u) {
-        pe[i] = (uint16_t)min((uint32_t)a.idx[i], E - 1u);
-        pw[i] = a.wts[i];
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[pe[i]], 1u);
-    __syncthreads();
     __shared__ uint32_t tot[16];
-    const uint32_t hist = tid < E ? base[tid] : 0u;
-    const uint32_t first = plan_scan(hist, tot);
-    if (tid < E) {
-        base[tid] = first;
-        start[tid] = first;
-        cnt[tid] = hist;
-    }
-    for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
-        for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
+    if (a.any_order) {
+        // A pair's place among its expert's rows is its order of arrival at
+        // an LDS counter, which changes from call to call; no result depends
+        // on it: each output row of the expert GEMMs is computed from its own
+        // activation row alone, and the combine sums a token's pairs in
+        // expert order from comb_idx.
+        for (uint32_t e = tid; e < E; e += 1024u) cnt[e] = 0u;
         __syncthreads();
-        const uint32_t i = c0 + tid;
-        const bool valid = i < P;
-        const uint32_t e = valid ? (uint32_t)pe[i] : 0u;
-        uint64_t same = __ballot(valid);
+        uint32_t my_pos[kPlanMaxPairs / 1024u];
 #pragma unroll
-        for (uint32_t bit = 0; bit < 10u; bit++) {  // E <= 1024
-            const uint64_t ones = __ballot((e >> bit) & 1u);
-            same &= ((e >> bit) & 1u) ? ones : ~ones;
-        }
-        const uint32_t rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
-        if (valid && rank == 0u) wcnt[wave][e] = (uint16_t)__popcll(same);
-        __syncthreads();
-        if (valid) {
-            uint32_t q = base[e] + rank;
-            for (uint32_t w = 0; w < wave; w++) q += wcnt[w][e];
-            const uint32_t t = i / a.k;
-            a.pair_row[q] = (int32_t)t;
-            uint32_t slot = 0;
-            for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)pe[t * a.k + j] < e;
-            a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
-            a.comb_w[(uint64_t)t * a.k + slot] = pw[i];
-            if (a.gemv_gu) {
-                GemvDesc* dg = a.gemv_gu + 2u * q;
-                GemvDesc* du = dg + 1;
-                GemvDesc* dd = a.gemv_dn + q;
-                const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.vg);
-                const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.vu);
-                const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.vd);
-#pragma unroll
-                for (uint32_t f = 0; f < sizeof(GemvDesc) / 4u; f++) {
-                    reinterpret_cast<uint32_t*>(dg)[f] = tg[f];
-                    reinterpret_cast<uint32_t*>(du)[f] = tu[f];
-                    reinterpret_cast<uint32_t*>(dd)[f] = td[f];
-                }
-                dg->w = a.vg.w + (uint64_t)e * a.w_stride_gu;
-                du->w = a.vu.w + (uint64_t)e * a.w_stride_gu;
-                dd->w = a.vd.w + (uint64_t)e * a.w_stride_dn;
-                dg->x = du->x = a.vg.x + (uint64_t)t * a.hidden;
-                dg->y = a.vg.y + (uint64_t)q * a.ffn;
-                du->y = a.vu.y + (uint64_t)q * a.ffn;
-                dd->x = a.vd.x + (uint64_t)q * a.ffn;
-                dd->y = a.vd.y + (uint64_t)q * a.hidden;
+        for (uint32_t u = 0; u < kPlanMaxPairs / 1024u; u++) {
+            const uint32_t i = tid + 1024u * u;
+            if (i < P) {
+                const uint32_t e = min((uint32_t)a.idx[i], E - 1u);
+                pe[i] = (uint16_t)e;
+                pw[i] = a.wts[i];
+                my_pos[u] = atomicAdd(&cnt[e], 1u);
             }
         }
         __syncthreads();
-        if (tid < E) {
-            uint32_t n = 0;
-            for (uint32_t w = 0; w < 16u; w++) n += wcnt[w][tid];
-            base[tid] += n;
+        const uint32_t hist = tid < E ? cnt[tid] : 0u;
+        const uint32_t first = plan_scan(hist, tot);
+        if (tid < E) start[tid] = first;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t u = 0; u < kPlanMaxPairs / 1024u; u++) {
+            const uint32_t i = tid + 1024u * u;
+            if (i < P) {
+                const uint32_t e = pe[i], t = i / a.k;
+                const uint32_t q = start[e] + my_pos[u];
+                a.pair_row[q] = (int32_t)t;
+                uint32_t slot = 0;
+                for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)pe[t * a.k + j] < e;
+                a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
+                a.comb_w[(uint64_t)t * a.k + slot] = pw[i];
+            }
         }
-        __syncthreads();  // (the next chunk clears wcnt)
+    } else {
+        for (uint32_t e = tid; e < E; e += 1024u) base[e] = 0u;
+#pragma unroll 4
+        for (uint32_t i = tid; i < P; i += 1024u) {
+            pe[i] = (uint16_t)min((uint32_t)a.idx[i], E - 1u);
+            pw[i] = a.wts[i];
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < P; i += 1024u) atomicAdd(&base[pe[i]], 1u);
+        __syncthreads();
+        const uint32_t hist = tid < E ? base[tid] : 0u;
+        const uint32_t first = plan_scan(hist, tot);
+        if (tid < E) {
+            base[tid] = first;
+            start[tid] = first;
+            cnt[tid] = hist;
+        }
+        for (uint32_t c0 = 0; c0 < P; c0 += 1024u) {
+            for (uint32_t j = tid; j < 16u * E; j += 1024u) wcnt[j / E][j % E] = 0u;
+            __syncthreads();
+            const uint32_t i = c0 + tid;
+            const bool valid = i < P;
+            const uint32_t e = valid ? (uint32_t)pe[i] : 0u;
+            uint64_t same = __ballot(valid);
+#pragma unroll
+            for (uint32_t bit = 0; bit < 10u; bit++) {  // E <= 1024
+                const uint64_t ones = __ballot((e >> bit) & 1u);
+                same &= ((e >> bit) & 1u) ? ones : ~ones;
+            }
+            const uint32_t rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+            if (valid && rank == 0u) wcnt[wave][e] = (uint16_t)__popcll(same);
+            __syncthreads();
+            if (valid) {
+                uint32_t q = base[e] + rank;
+                for (uint32_t w = 0; w < wave; w++) q += wcnt[w][e];
+                const uint32_t t = i / a.k;
+                a.pair_row[q] = (int32_t)t;
+                uint32_t slot = 0;
+                for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)pe[t * a.k + j] < e;
+                a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
+                a.comb_w[(uint64_t)t * a.k + slot] = pw[i];
+                if (a.gemv_gu) {
+                    GemvDesc* dg = a.gemv_gu + 2u * q;
+                    GemvDesc* du = dg + 1;
+                    GemvDesc* dd = a.gemv_dn + q;
+                    const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.vg);
+                    const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.vu);
+                    const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.vd);
+#pragma unroll
+                    for (uint32_t f = 0; f < sizeof(GemvDesc) / 4u; f++) {
+                        reinterpret_cast<uint32_t*>(dg)[f] = tg[f];
+                        reinterpret_cast<uint32_t*>(du)[f] = tu[f];
+                        reinterpret_cast<uint32_t*>(dd)[f] = td[f];
+                    }
+                    dg->w = a.vg.w + (uint64_t)e * a.w_stride_gu;
+                    du->w = a.vu.w + (uint64_t)e * a.w_stride_gu;
+                    dd->w = a.vd.w + (uint64_t)e * a.w_stride_dn;
+                    dg->x = du->x = a.vg.x + (uint64_t)t * a.hidden;
+                    dg->y = a.vg.y + (uint64_t)q * a.ffn;
+                    du->y = a.vu.y + (uint64_t)q * a.ffn;
+                    dd->x = a.vd.x + (uint64_t)q * a.ffn;
+                    dd->y = a.vd.y + (uint64_t)q * a.hidden;
+                }
+            }
+            __syncthreads();
+            if (tid < E) {
+                uint32_t n = 0;
+                for (uint32_t w = 0; w < 16u; w++) n += wcnt[w][tid];
+                base[tid] += n;
+            }
+            __syncthreads();  // (the next chunk clears wcnt)
+        }
     }
     __syncthreads();
     if (a.gemv_gu) return;  // the GEMV form runs no MMQ launch

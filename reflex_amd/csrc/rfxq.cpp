@@ -914,7 +914,23 @@ uint32_t moe_tile_m(uint32_t pairs, uint32_t experts, bool f16, uint32_t ty, uin
     return waves(64u, ty == RFXQ_TYPE_Q6_K ? 2u : 3u) < waves(kMmqBM, 2u) ? 64u : kMmqBM;
 }
 
-rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o) {
+// Row tile of a GEMM of 256 rows or more launched alone (not in a grouped
+// launch, whose workgroups are counted over all its GEMMs; fewer rows keep
+// the tile that holds them) that is too small to occupy half
+// the CUs even at its largest split (nsb / 2 splits of 128- or 64-row
+// tiles): smaller row tiles, down to 32. Config 1's 1024 x 1024 Q8_0 matrix
+// at 512 rows has 16 tiles of 128 rows (32 workgroups with two splits) and
+// 64 of 32 rows (256 workgroups with four one-super-block splits).
+uint32_t small_gemm_tile_m(uint32_t tile_m, uint32_t rows, uint32_t n, uint32_t nsb, uint32_t cus) {
+    const uint64_t tn = (n + 255u) / 256u;
+    while (tile_m > 32u && (uint64_t)((rows + tile_m - 1u) / tile_m) * tn * std::max(1u, nsb / 2u) * 2u <
+                               std::max(cus, 1u))
+        tile_m /= 2u;
+    return tile_m;
+}
+
+rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o,
+                             bool alone = true) {
     rfxq_gemm_policy p;
     std::memset(&p, 0, sizeof p);
     p.splits = 1;
@@ -930,6 +946,7 @@ rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows,
     p.tile_m = f16 ? f16_tile_m(rows) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
     p.tile_n = tile_bn(f16);
     const uint32_t nsb = k / 256u;
+    if (f16 && alone && !o.quant_mma_splits && rows >= 256u) p.tile_m = small_gemm_tile_m(p.tile_m, rows, n, nsb, cus);
     const uint32_t tiles = ((rows + p.tile_m - 1u) / p.tile_m) * ((n + p.tile_n - 1u) / p.tile_n);
     uint32_t splits = 1;
     if (o.quant_mma_splits) splits = o.quant_mma_splits;
@@ -1267,12 +1284,14 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         if (reinterpret_cast<uintptr_t>(it.x) % (ext ? 256u : 16u))
             return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not %u-byte aligned", i, ext ? 256u : 16u);
         const uint32_t k = it.w->in_features;
-        rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o);
+        rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o, count == 1u);
         if (ext) {
             if (int rc = check_act(it.x, rows, k, "gemm_q8_1 plan")) return rc;
             const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, 0);
             pol.path = f16 ? PATH_MMQ_F16 : PATH_MMQ_INT8;
             pol.tile_m = f16 ? f16_tile_m(rows) : o.quant_mma_tile == 64 ? 64u : kMmqBM;
+            if (f16 && count == 1u && !o.quant_mma_splits && rows >= 256u)
+                pol.tile_m = small_gemm_tile_m(pol.tile_m, rows, it.w->out_features, k / 256u, cus);
         }
         if (pol.path == PATH_GEMV_ROWS) {
             for (uint32_t r = 0; r < rows; r++)
@@ -2629,8 +2648,9 @@ struct MoePlanArgs {
     const float* logits;
     uint32_t normalize;
     float scale;
+    uint32_t any_order;
 };
-static_assert(sizeof(MoePlanArgs) == 616, "MoePlanArgs layout");
+static_assert(sizeof(MoePlanArgs) == 624, "MoePlanArgs layout");
 
 
 int rfxq_moe_ffn_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const float* router_logits,
@@ -2858,6 +2878,7 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
     pa.bm_dn = bm_dn;
     pa.ffn = ffn;
     pa.hidden = hidden;
+    pa.any_order = gemv_form ? 0u : 1u;  // (the GEMV form keeps token order within an expert)
     GemvItem ig, iu, id;
     if (gemv_form) {
         if (int rc = make_gemv_item(x, &g0, gout, &ig)) return rc;

@@ -349,3 +349,17 @@ def test_moe_ffn_grouped_device_errors(rq):
     lg = torch.zeros(experts, device=DEV)
     with pytest.raises(rq.ReflexError, match="expert_count=2"):
         rq.moe_ffn_grouped_device(x, 1, hidden, lg, experts, 1, True, 1.0, g, g, d, torch.empty(hidden, device=DEV))
+
+
+def test_moe_device_prefill_bit_stable(rq, orc):
+    """The device plan groups each expert's rows in arrival order (LDS
+    atomics), which differs between calls; the layer's output does not:
+    repeated config 5 prefill calls are equal bit for bit."""
+    y_d, _, ref, ws, x, logits = _moe_device_case(rq, orc, 512, 128, 2048, 768, 8, 1400)
+    lg = _dev(logits)
+    for i in range(4):
+        out = torch.empty(512 * 2048, device=DEV)
+        rq.moe_ffn_grouped_device(x, 512, 2048, lg, 128, 8, True, 1.0, *ws, out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(512, 2048), y_d), f"call {i}"
+    assert orc.rel_err_row_l2(y_d, ref) < TOL

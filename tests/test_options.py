@@ -141,10 +141,17 @@ def test_policy_paths(rq):
 
 def test_policy_tiles_and_splits(rq):
     pol = rq.gemm_policy
-    # 0.6B q_proj at M=512: 4 x 8 tiles of 128 x 256 on 256 CUs
+    # 0.6B q_proj at M=512 alone: 4 x 8 tiles of 128 x 256 with at most
+    # nsb / 2 = 2 splits cover 64 of 256 CUs' 512 places, under half: 64-row
+    # tiles (8 x 8 x 2 splits = 128 workgroups)
     p = pol(Q4K, 1024, 2048, 512, 256)
-    assert (p["tile_m"], p["tile_n"]) == (128, 256)
+    assert (p["tile_m"], p["tile_n"]) == (64, 256)
     assert (p["splits"], p["sb_per_split"]) == (2, 2)   # capped at nsb / 2 = 2 splits
+    # config 1's 1024 x 1024 Q8_0 at M=512: 32-row tiles, one-super-block splits
+    p = pol(8, 1024, 1024, 512, 256)
+    assert (p["tile_m"], p["splits"], p["sb_per_split"]) == (32, 4, 1)
+    # 255 rows keep the tile that holds them
+    assert pol(Q4K, 1024, 2048, 255, 256)["tile_m"] == 128
     # 8B q_proj: 4 x 16 = 64 tiles -> ceil(512 / 64) = 8 splits of 2 super-blocks
     p = pol(Q4K, 4096, 4096, 512, 256)
     assert (p["splits"], p["sb_per_split"]) == (8, 2)
