@@ -309,6 +309,8 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         // on it: each output row of the expert GEMMs is computed from its own
         // activation row alone, and the combine sums a token's pairs in
         // expert order from comb_idx.
+        uint16_t* inv = &wcnt[0][0];  // pair index at each place (the sort's counts are not used here)
+        static_assert(sizeof(wcnt) >= kPlanMaxPairs * sizeof(uint16_t), "inverse places in wcnt");
         for (uint32_t e = tid; e < E; e += 1024u) cnt[e] = 0u;
         __syncthreads();
         uint32_t my_pos[kPlanMaxPairs / 1024u];
@@ -333,13 +335,17 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
             if (i < P) {
                 const uint32_t e = pe[i], t = i / a.k;
                 const uint32_t q = start[e] + my_pos[u];
-                a.pair_row[q] = (int32_t)t;
+                inv[q] = (uint16_t)i;
                 uint32_t slot = 0;
                 for (uint32_t j = 0; j < a.k; j++) slot += (uint32_t)pe[t * a.k + j] < e;
                 a.comb_idx[(uint64_t)t * a.k + slot] = (int32_t)q;
                 a.comb_w[(uint64_t)t * a.k + slot] = pw[i];
             }
         }
+        // pair_row[q] = token of the pair at place q, stored in place order
+        // (one CU's scattered dword stores to P places cost several us)
+        __syncthreads();
+        for (uint32_t q = tid; q < P; q += 1024u) a.pair_row[q] = (int32_t)(inv[q] / a.k);
     } else {
         for (uint32_t e = tid; e < E; e += 1024u) base[e] = 0u;
 #pragma unroll 4
@@ -425,48 +431,64 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         tmd = (m + a.bm_dn - 1u) / a.bm_dn;
     }
     const uint32_t wg_gu = plan_scan(2u * tm * tn_f, tot), wg_dn = plan_scan(tmd * tn_h, tot);
-    if (tid < a.E) {
-        const uint32_t e = tid;
-        const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
-        // descriptors from the templates, filled in place in global memory
-        MmqDesc* g = a.descs_gu + 2u * e;
-        MmqDesc* u = g + 1;
-        MmqDesc* d = a.descs_dn + e;
-        {
-            const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.tg);
-            const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.tu);
-            const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.td);
-            uint32_t* pg = reinterpret_cast<uint32_t*>(g);
-            uint32_t* pu = reinterpret_cast<uint32_t*>(u);
-            uint32_t* pd = reinterpret_cast<uint32_t*>(d);
+    // Descriptors from the templates, 128 experts at a time: filled in LDS
+    // (the pairs' weights are no longer needed: their space holds them),
+    // then stored with consecutive threads on consecutive words (one thread
+    // per expert writing its own descriptors scatters every store).
+    constexpr uint32_t kChunk = 128, kDw = sizeof(MmqDesc) / 4u;
+    static_assert(sizeof(pw) >= 3u * kChunk * sizeof(MmqDesc), "descriptor staging in pw");
+    MmqDesc* stg = reinterpret_cast<MmqDesc*>(pw);  // [2 kChunk] gate/up, then [kChunk] down
+    for (uint32_t c0 = 0; c0 < a.E; c0 += kChunk) {
+        const uint32_t nc = min(kChunk, a.E - c0);
+        __syncthreads();  // (the previous chunk's copies have read the staging)
+        if (tid >= c0 && tid < c0 + nc) {
+            const uint32_t e = tid;
+            const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
+            MmqDesc* g = stg + 2u * (e - c0);
+            MmqDesc* u = g + 1;
+            MmqDesc* d = stg + 2u * kChunk + (e - c0);
+            {
+                const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.tg);
+                const uint32_t* tu = reinterpret_cast<const uint32_t*>(&a.tu);
+                const uint32_t* td = reinterpret_cast<const uint32_t*>(&a.td);
+                uint32_t* pg = reinterpret_cast<uint32_t*>(g);
+                uint32_t* pu = reinterpret_cast<uint32_t*>(u);
+                uint32_t* pd = reinterpret_cast<uint32_t*>(d);
 #pragma unroll
-            for (uint32_t i = 0; i < sizeof(MmqDesc) / 4u; i++) {
-                pg[i] = tg[i];
-                pu[i] = tu[i];
-                pd[i] = td[i];
+                for (uint32_t i = 0; i < kDw; i++) {
+                    pg[i] = tg[i];
+                    pu[i] = tu[i];
+                    pd[i] = td[i];
+                }
             }
+            g->w = a.tg.w + (uint64_t)e * a.w_stride_gu;
+            u->w = a.tu.w + (uint64_t)e * a.w_stride_gu;
+            d->w = a.td.w + (uint64_t)e * a.w_stride_dn;
+            g->rows = u->rows = a.pair_row + st;
+            g->m = u->m = d->m = m;
+            g->tiles_m = u->tiles_m = tm;
+            d->tiles_m = tmd;
+            g->y = a.tg.y + (uint64_t)st * a.ffn;
+            u->y = a.tu.y + (uint64_t)st * a.ffn;
+            if (a.f16) {  // xh rows of 2*ffn bytes, xsx records of ffn/256 * 32 bytes, xrs
+                d->xq = a.td.xq + (uint64_t)st * a.ffn * 2u;
+                d->xds = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.td.xds) +
+                                                           (uint64_t)st * (a.ffn / 256u) * 32u);
+                d->xrs = a.td.xrs + st;
+            } else {
+                d->xq = a.td.xq + (uint64_t)st * a.ffn;
+                d->xds = a.td.xds + (uint64_t)st * (a.ffn / 32u);
+            }
+            d->y = a.td.y + (uint64_t)st * a.hidden;
+            g->wg_begin = wg_gu;
+            u->wg_begin = wg_gu + tm * tn_f;
+            d->wg_begin = wg_dn;
         }
-        g->w = a.tg.w + (uint64_t)e * a.w_stride_gu;
-        u->w = a.tu.w + (uint64_t)e * a.w_stride_gu;
-        d->w = a.td.w + (uint64_t)e * a.w_stride_dn;
-        g->rows = u->rows = a.pair_row + st;
-        g->m = u->m = d->m = m;
-        g->tiles_m = u->tiles_m = tm;
-        d->tiles_m = tmd;
-        g->y = a.tg.y + (uint64_t)st * a.ffn;
-        u->y = a.tu.y + (uint64_t)st * a.ffn;
-        if (a.f16) {  // xh rows of 2*ffn bytes, xsx records of ffn/256 * 32 bytes, xrs
-            d->xq = a.td.xq + (uint64_t)st * a.ffn * 2u;
-            d->xds = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.td.xds) +
-                                                       (uint64_t)st * (a.ffn / 256u) * 32u);
-            d->xrs = a.td.xrs + st;
-        } else {
-            d->xq = a.td.xq + (uint64_t)st * a.ffn;
-            d->xds = a.td.xds + (uint64_t)st * (a.ffn / 32u);
-        }
-        d->y = a.td.y + (uint64_t)st * a.hidden;
-        g->wg_begin = wg_gu;
-        u->wg_begin = wg_gu + tm * tn_f;
-        d->wg_begin = wg_dn;
+        __syncthreads();
+        const uint32_t* sw = reinterpret_cast<const uint32_t*>(stg);
+        uint32_t* gu_out = reinterpret_cast<uint32_t*>(a.descs_gu + 2u * c0);
+        uint32_t* dn_out = reinterpret_cast<uint32_t*>(a.descs_dn + c0);
+        for (uint32_t i = tid; i < 2u * nc * kDw; i += 1024u) gu_out[i] = sw[i];
+        for (uint32_t i = tid; i < nc * kDw; i += 1024u) dn_out[i] = sw[2u * kChunk * kDw + i];
     }
 }
