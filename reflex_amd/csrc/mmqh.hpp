@@ -1070,3 +1070,32 @@ RFXQ_DEV void mmqh_q80_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0, TY_Q8_0, 4, 2)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0_m32, TY_Q8_0, 1, 4)
 RFXQ_MMQH_ENTRY(rfxq_mmqh_q8_0_m64, TY_Q8_0, 2, 3)
+
+// One launch of 32-row tiles over GEMMs of Q4_K and Q6_K weights (a layer's
+// Q4_K projections with its Q6_K v / down at a few rows): each tile runs the
+// body of its descriptor's type (a uniform branch; the same code and results
+// as the per-type entries), so a few-row layer is one launch, not two (one
+// Qwen3-0.6B layer at 12 rows: 28.8 -> 19.3 us). Not for the larger tiles:
+// the 128-row bodies together spill registers (the 0.6B set at 512 rows gained
+// nothing, and an 8B layer, whose Q6_K GEMMs then lose their split-K, lost
+// 8%), and the 64-row ones run at different occupancies per type.
+#define RFXQ_MMQH_MIX_ENTRY(NAME, MT, WPE)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void NAME(MmqArgs args) { \
+        __shared__ __attribute__((aligned(16))) u4_t a0[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a1[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a2[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t a3[mmqh::Tile<MT>::kAct / 16u];                          \
+        __shared__ __attribute__((aligned(16))) u4_t sx[mmqh::kThreads];                                     \
+        __shared__ __attribute__((aligned(16))) float sc[mmqh::Tile<MT>::BM];                                \
+        if (blockDim.x != mmqh::kThreads) return; /* the tile assumes exactly kThreads lanes */               \
+        const uint32_t tiles = min(gridDim.x, mmq_tile_count(args));                                        \
+        if (blockIdx.x >= tiles) return;                                                                     \
+        const uint32_t b = mmqh::xcd_tile(blockIdx.x, tiles);                                               \
+        const MmqDesc d = mmq_pick(args, b);                                                                 \
+        if (b - d.wg_begin >= d.tiles_m * d.tiles_n * d.splits) return;                                     \
+        const mmqh::ActLds lds{{a0, a1, a2, a3}, sx, sc};                                                    \
+        const uint32_t ty = __builtin_amdgcn_readfirstlane(d.type);                                         \
+        if (ty == TY_Q6K) mmqh_tile<MT, TY_Q6K>(d, b - d.wg_begin, lds);                                      \
+        else mmqh_tile<MT, TY_Q4K>(d, b - d.wg_begin, lds);                                                    \
+    }
+RFXQ_MMQH_MIX_ENTRY(rfxq_mmqh_mix_m32, 1, 3)

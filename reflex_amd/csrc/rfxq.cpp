@@ -145,6 +145,7 @@ struct Ctx {
     hipFunction_t gemv = nullptr, quant = nullptr, quant_multi = nullptr, reduce = nullptr, reduce_multi = nullptr;
     hipFunction_t mmq[3] = {}, dots[3] = {}, mmq64[3] = {};
     hipFunction_t mmqh[3][3] = {};  // [Q4_K, Q6_K, Q8_0][128-row, 32-row, 64-row tiles]
+    hipFunction_t mmqh_mix_m32 = nullptr;  // 32-row tiles, Q4_K or Q6_K per descriptor
     hipFunction_t act_f16 = nullptr, act_f16_multi = nullptr, act_f16_wg = nullptr, act_f16_multi_wg = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
@@ -221,6 +222,7 @@ int load_ctx(int device, Ctx** out) {
         {&c->mmqh[2][0], "rfxq_mmqh_q8_0"},
         {&c->mmqh[2][1], "rfxq_mmqh_q8_0_m32"},
         {&c->mmqh[2][2], "rfxq_mmqh_q8_0_m64"},
+        {&c->mmqh_mix_m32, "rfxq_mmqh_mix_m32"},
         {&c->act_f16, "rfxq_act_f16"},
         {&c->act_f16_multi, "rfxq_act_f16_multi"},
         {&c->act_f16_wg, "rfxq_act_f16_wg"},
@@ -1118,6 +1120,10 @@ int launch_combine(Ctx* c, const float* pair_out, const int32_t* idx, const floa
 
 // f16: Q4_K / Q6_K descriptors on rfxq_mmqh_q4k / _q6k (f16 activation
 // layout; tile_m 32: the *_m32 kernels); int8: tile_m 64 takes rfxq_mmq_*_m64
+// f16 tiles of this type and height run in the mixed-type kernel (Q4_K and
+// Q6_K 32-row tiles: the same bodies, one launch for a few-row layer)
+bool mix_f16(uint32_t ty, uint32_t tile_m) { return (ty == RFXQ_TYPE_Q4_K || ty == RFXQ_TYPE_Q6_K) && tile_m == 32u; }
+
 int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const MmqDesc* table, uint32_t total_wgs,
                bool dots, hipStream_t stream, bool f16 = false, uint32_t tile_m = kMmqBM) {
     const bool m64 = !f16 && tile_m == 64u;
@@ -1127,7 +1133,9 @@ int launch_mmq(Ctx* c, uint32_t ty, const MmqDesc* descs, uint32_t count, const 
     a.table = table;
     if (count <= kMmqInline) std::copy(descs, descs + count, a.inl);
     hipFunction_t f = dots ? c->dots[type_index(ty)] : m64 ? c->mmq64[type_index(ty)] : c->mmq[type_index(ty)];
-    if (f16 && !dots) f = c->mmqh[type_index(ty)][tile_m == 32u ? 1 : tile_m == 64u ? 2 : 0];
+    // f16: Q4_K and Q6_K 32-row tiles mixed in one launch, others per type
+    if (f16 && !dots)
+        f = mix_f16(ty, tile_m) ? c->mmqh_mix_m32 : c->mmqh[type_index(ty)][tile_m == 32u ? 1 : tile_m == 64u ? 2 : 0];
     return launch(f, total_wgs, 0, stream, &a, sizeof a, "rfxq_mmq launch", kMmqThreads);
 }
 
@@ -1267,6 +1275,11 @@ uint32_t group_tile_m(uint32_t g) {
     return v == 1u || v == 4u ? 64u : v == 3u ? 32u : kMmqBM;
 }
 uint32_t group_variant(bool f16, uint32_t tile_m) { return f16 ? (tile_m == 32u ? 3u : tile_m == 64u ? 4u : 2u) : (tile_m == 64u ? 1u : 0u); }
+// the group (launch) of a GEMM: type_index + 3 * variant, except that the f16
+// 32-row tiles of Q4_K and Q6_K share one launch (rfxq_mmqh_mix_m32)
+uint32_t group_index(uint32_t ty, bool f16, uint32_t tile_m) {
+    return (mix_f16(ty, tile_m) && f16 ? 0u : (uint32_t)type_index(ty)) + 3u * group_variant(f16, tile_m);
+}
 
 // `ext` (optional, one per item): the items' x are caller activation buffers
 // (rfxq_act_q8_1_size layouts, already quantized): every GEMM takes an MMQ
@@ -1299,7 +1312,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
             continue;
         }
         const bool f16 = pol.path == PATH_MMQ_F16;
-        item_kernel[i] = type_index(it.w->ggml_type) + 3u * group_variant(f16, pol.tile_m);
+        item_kernel[i] = group_index(it.w->ggml_type, f16, pol.tile_m);
         size_t ai = 0;
         while (ai < g->acts.size() && g->acts[ai].x != it.x) ai++;
         if (ai == g->acts.size()) {
@@ -2077,7 +2090,7 @@ int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint3
         const uint32_t k = it.w->in_features;
         const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, 0);
         const uint32_t tile_m = f16 ? (rows <= 32u ? 32u : kMmqBM) : o.quant_mma_tile == 64u ? 64u : kMmqBM;
-        const uint32_t t = type_index(it.w->ggml_type) + 3u * group_variant(f16, tile_m);
+        const uint32_t t = group_index(it.w->ggml_type, f16, tile_m);
         MmqDesc d;
         std::memset(&d, 0, sizeof d);
         d.w = it.w->data;

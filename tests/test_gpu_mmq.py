@@ -353,11 +353,12 @@ def test_gemm_caller_workspace(rq, orc):
         rq.gemm(_dev(x), w, m, workspace=ws[:100])
 
 
-def test_gemm_batch_and_plan_match_single_gemms(rq, orc, opts):
+@pytest.mark.parametrize("rows", [300, 12, 29])
+def test_gemm_batch_and_plan_match_single_gemms(rq, orc, opts, rows):
     """Grouped GEMMs (each activation brought into its layouts once, one launch
-    per weight type) give the single-GEMM results bit for
-    bit (split-K off on both sides; by default a group this small splits K)."""
-    rows = 300
+    per weight type; at up to 32 rows Q4_K and Q6_K share one launch of 32-row
+    tiles) give the single-GEMM results bit for bit (split-K off on both
+    sides; by default a group this small splits K)."""
     shapes = [(Q4K, 768, 1024), (Q4K, 256, 1024), (Q6K, 256, 1024), (Q8_0, 512, 1024), (Q4K, 640, 2048)]
     xa = _dev(synth.activations(rows * 1024, 71))
     xb = _dev(synth.activations(rows * 2048, 72))
