@@ -50,30 +50,35 @@ extern "C" __global__ __launch_bounds__(256) void rfxq_silu_and_mul(const float*
 
 // out[t,:] = sum_j w[t,j] * pair_out[idx[t,j],:] for j in 0..k (pairs sorted
 // by expert), evaluated as fma(w, v, acc) from acc = 0. With `vec` (hidden a
-// multiple of 4, 16-byte aligned rows) a workgroup takes whole tokens, four
-// columns per lane, the k rows' loads issued together; else one element per
-// lane. Same operations in the same order either way.
+// multiple of 4, 16-byte aligned rows) a workgroup takes 1024 columns of a
+// token, four per lane, the k rows' loads issued together; else one element
+// per lane. Same operations in the same order either way.
 extern "C" __global__ __launch_bounds__(256) void rfxq_moe_combine(const float* __restrict__ pair_out,
                                                                   const int32_t* __restrict__ idx,
                                                                   const float* __restrict__ w,
                                                                   float* __restrict__ out, uint32_t tokens,
                                                                   uint32_t k, uint32_t hidden, uint32_t vec) {
     if (vec) {
-        for (uint32_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+        // a workgroup per (token, 1024-column chunk); every one of the k
+        // rows' loads is issued (an absent pair reads row 0 and keeps acc
+        // by a select), so they are in flight together
+        const uint32_t chunks = (hidden + 1023u) / 1024u;
+        for (uint32_t b = blockIdx.x; b < tokens * chunks; b += gridDim.x) {
+            const uint32_t t = b / chunks;
             const uint64_t tk = (uint64_t)t * k;
-            for (uint32_t c = 4u * threadIdx.x; c < hidden; c += 1024u) {
+            const uint32_t c = (b % chunks) * 1024u + 4u * threadIdx.x;
+            if (c < hidden) {
                 float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 8
                 for (uint32_t j = 0; j < k; j++) {
                     const int32_t p = idx[tk + j];
-                    if (p >= 0) {
-                        const float wj = w[tk + j];
-                        const float4 v = *reinterpret_cast<const float4*>(pair_out + (uint64_t)p * hidden + c);
-                        acc.x = fmaf(wj, v.x, acc.x);
-                        acc.y = fmaf(wj, v.y, acc.y);
-                        acc.z = fmaf(wj, v.z, acc.z);
-                        acc.w = fmaf(wj, v.w, acc.w);
-                    }
+                    const bool has = p >= 0;
+                    const float wj = w[tk + j];
+                    const float4 v = *reinterpret_cast<const float4*>(pair_out + (uint64_t)(has ? p : 0) * hidden + c);
+                    acc.x = has ? fmaf(wj, v.x, acc.x) : acc.x;
+                    acc.y = has ? fmaf(wj, v.y, acc.y) : acc.y;
+                    acc.z = has ? fmaf(wj, v.z, acc.z) : acc.z;
+                    acc.w = has ? fmaf(wj, v.w, acc.w) : acc.w;
                 }
                 *reinterpret_cast<float4*>(out + (uint64_t)t * hidden + c) = acc;
             }

@@ -1112,7 +1112,7 @@ int launch_combine(Ctx* c, const float* pair_out, const int32_t* idx, const floa
         float* out;
         uint32_t tokens, k, hidden, vec;
     } a = {pair_out, idx, w, out, tokens, k, hidden, vec ? 1u : 0u};
-    const uint64_t blocks = vec ? std::min<uint64_t>(tokens, 16384u)
+    const uint64_t blocks = vec ? std::min<uint64_t>((uint64_t)tokens * ((hidden + 1023u) / 1024u), 16384u)
                                 : std::min<uint64_t>(((uint64_t)tokens * hidden + 255u) / 256u, 16384u);
     return launch(c->combine, (uint32_t)std::max<uint64_t>(blocks, 1u), 0, stream, &a, sizeof a,
                   "moe_combine launch");
