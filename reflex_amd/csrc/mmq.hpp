@@ -41,8 +41,15 @@ struct MmqDesc {
     float* y;               // [splits][m][ldy] (splits > 1: workspace)
     uint32_t m, n, k, type;
     uint32_t ldq, ldy, tiles_m, tiles_n;
-    uint32_t splits, sb_per_split, wg_begin, pad;
-    int32_t* dots_out;      // [m][n][k/32] for the rfxq_mmq_dots_* test hook
+    uint32_t splits, sb_per_split, wg_begin;
+    // 1: a gate/up pair (the Q4_K f16 tiles, mmqh.hpp): w holds the gate
+    // weights, w_up the up weights of the same shape, and y receives
+    // s = silu(gate) * up [m][n]; tiles are 128 columns wide
+    uint32_t gu_pair;
+    union {
+        int32_t* dots_out;      // [m][n][k/32] for the rfxq_mmq_dots_* test hook (int8 kernels)
+        const uint8_t* w_up;    // gu_pair: the up weights
+    };
     const float* xrs;       // f16-activation kernels (mmqh.hpp): [m] row scales 2^e
 };
 

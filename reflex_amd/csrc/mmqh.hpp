@@ -212,7 +212,7 @@ RFXQ_DEV uint32_t act_base(const MmqDesc& ds, uint32_t m0) { return ds.rows ? 0u
 // scales 2^e of rows row..row+27. Outputs are written once and not read
 // back by the kernel: non-temporal stores.
 RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col, const v16f_t& acc,
-                         const float* sc) {
+                         const float* sc, bool scale = true) {
     if (col >= ds.n) return;
     float* yc = y + col;
 #pragma unroll
@@ -222,7 +222,7 @@ RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint32_t m = row + 8u * q4 + r;
-            if (m < ds.m) __builtin_nontemporal_store(acc[4 * q4 + r] * sv[r], yc + (uint64_t)m * ds.ldy);
+            if (m < ds.m) __builtin_nontemporal_store(scale ? acc[4 * q4 + r] * sv[r] : acc[4 * q4 + r], yc + (uint64_t)m * ds.ldy);
         }
     }
 }
@@ -235,16 +235,17 @@ RFXQ_DEV void store_tile(const MmqDesc& ds, float* y, uint32_t row, uint32_t col
 // columns 4k..4k+3: eight lanes per 128-byte row piece and a quarter of the
 // dword stores' instructions (4-5% of the 0.6B prefill set). Outputs whose
 // rows are not 16-byte aligned take the dword stores.
-template <int MT>
+template <int MT, int JMASK = 3>
 RFXQ_DEV void store_wave(const MmqDesc& ds, float* y, uint32_t m0, uint32_t c0, const v16f_t (&acc)[MT][2],
-                         const float* sc, u4_t* buf) {
+                         const float* sc, u4_t* buf, bool scale = true) {
     const uint32_t lane = threadIdx.x & 63u, l32 = lane & 31u, h = lane >> 5;
     if ((ds.ldy & 3u) != 0u || (reinterpret_cast<uintptr_t>(y) & 15u) != 0u) {
 #pragma unroll
         for (int i = 0; i < MT; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                store_tile(ds, y, m0 + 32u * i + 4u * h, c0 + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h);
+                if (JMASK >> j & 1)
+                    store_tile(ds, y, m0 + 32u * i + 4u * h, c0 + 32u * j + l32, acc[i][j], sc + 32u * i + 4u * h, scale);
         return;
     }
     float* bf = reinterpret_cast<float*>(buf);
@@ -253,6 +254,7 @@ RFXQ_DEV void store_wave(const MmqDesc& ds, float* y, uint32_t m0, uint32_t c0, 
     for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) {
+            if (!(JMASK >> j & 1)) continue;
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++)
 #pragma unroll
@@ -264,7 +266,7 @@ RFXQ_DEV void store_wave(const MmqDesc& ds, float* y, uint32_t m0, uint32_t c0, 
             for (int q4 = 0; q4 < 4; q4++) {
                 const uint32_t R = 8u * q4 + 4u * h + t;
                 f4v_t v = *reinterpret_cast<const f4v_t*>(bf + 32u * R + ((4u * k) ^ ((R & 7u) << 2)));
-                v *= sc[32u * i + R];
+                if (scale) v *= sc[32u * i + R];
                 const uint32_t m = m0 + 32u * i + R, c = c0 + 32u * j + 4u * k;
                 if (m >= ds.m) continue;
                 float* yr = y + (uint64_t)m * ds.ldy;
@@ -387,7 +389,13 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     // fault. Activation rows are clamped or gathered (act_row): in bounds.
     const uint32_t rb = act_base(ds, m0);
     const rsrc_t r_act = make_rsrc(ds.xq + (uint64_t)rb * ds.ldq, 0xFFFFFFFFu);
-    const rsrc_t r_w = make_rsrc(ds.w + (uint64_t)n0 * row_bytes, min(BN, ds.n - n0) * row_bytes);
+    // a gate/up pair: waves 0-1 the gate columns [n0, n0 + 128), waves 2-3
+    // the same columns of up
+    const bool pair = ds.gu_pair != 0u;
+    const bool upw = pair && w >= 2u;
+    const uint32_t wc = pair ? (w & 1u) : w;  // the wave's 64-column block
+    const rsrc_t r_w = make_rsrc((upw ? ds.w_up : ds.w) + (uint64_t)n0 * row_bytes,
+                                 min(pair ? BN / 2u : BN, ds.n - n0) * row_bytes);
     const rsrc_t r_sx =
         make_rsrc(reinterpret_cast<const uint8_t*>(ds.xds) + (uint64_t)rb * rec_bytes, 0xFFFFFFFFu);
     // Staged activations, copied straight into LDS (buffer_load ... lds: the
@@ -415,9 +423,9 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     uint32_t col[2], g_q[2], g_h[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        col[j] = 64u * w + 32u * j + l32;
+        col[j] = 64u * wc + 32u * j + l32;
         g_h[j] = col[j] * row_bytes;
-        g_q[j] = (64u * w + 32u * j + (l32 & 15u)) * row_bytes + 16u + 32u * (l32 >> 4) + 16u * h;
+        g_q[j] = (64u * wc + 32u * j + (l32 & 15u)) * row_bytes + 16u + 32u * (l32 >> 4) + 16u * h;
     }
     const uint32_t g_qb = 16u * row_bytes;  // load B: 16 columns on
     const uint32_t nst = 4u * (sb1 - sb0);
@@ -594,7 +602,52 @@ RFXQ_DEV void mmqh_q4k_rows(const MmqDesc& ds, uint32_t m0, uint32_t n0, uint32_
     lds_barrier();
 
     float* y = ds.y + (uint64_t)ks * ds.m * ds.ldy;
-    store_wave<MT>(ds, y, m0, n0 + 64u * w, acc, L.sc, pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], w));
+    if (!pair) {
+        store_wave<MT>(ds, y, m0, n0 + 64u * w, acc, L.sc, pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], w));
+        return;
+    }
+    // gate/up pair: the two waves of a 64-column block split the epilogue.
+    // The gate wave passes its j = 1 tiles to the up wave, the up wave its
+    // j = 0 tiles to the gate wave, through the stage buffers (tile (i, j) of
+    // the block c in buffer 2c + j at 4 KB i, each lane's 16 values at 64
+    // bytes lane: both waves' accumulators have one layout); each then
+    // stores s = silu(g) * u for its 32 columns, g and u the scaled outputs
+    // (silu_and_mul.cu:7-23: g / (1 + expf(-g)) * u), unscaled.
+    const int keep = upw ? 1 : 0;  // the j-tile this wave finishes
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        float* b = reinterpret_cast<float*>(pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], 2u * wc + (1u - keep))) +
+                   1024u * i + 16u * lane;
+        const v16f_t& v = acc[i][1 - keep];
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) *reinterpret_cast<f4v_t*>(b + r) = f4v_t{v[r], v[r + 1], v[r + 2], v[r + 3]};
+    }
+    lds_barrier();
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const float* b = reinterpret_cast<const float*>(pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], 2u * wc + keep)) +
+                             1024u * i + 16u * lane;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const f4v_t pv = *reinterpret_cast<const f4v_t*>(b + 4 * q4);
+                const float4 s4 = *reinterpret_cast<const float4*>(L.sc + 32u * i + 4u * h + 8u * q4);
+                const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float mine = acc[i][keep][4 * q4 + r] * sv[r], other = pv[r] * sv[r];
+                    const float g = upw ? other : mine, u = upw ? mine : other;
+                    acc[i][keep][4 * q4 + r] = (g / (1.0f + expf(-g))) * u;
+                }
+            }
+        }
+    }
+    lds_barrier();  // every passed tile read before the stores reuse the buffers
+    if (upw)
+        store_wave<MT, 2>(ds, y, m0, n0 + 64u * wc, acc, L.sc, pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], w), false);
+    else
+        store_wave<MT, 1>(ds, y, m0, n0 + 64u * wc, acc, L.sc, pick_buf(L.a[0], L.a[1], L.a[2], L.a[3], w), false);
 }
 
 template <int MT>
@@ -618,7 +671,7 @@ RFXQ_DEV void mmqh_tile(const MmqDesc& dv, uint32_t t_local, const mmqh::ActLds&
     const uint32_t ks = t_local % ds.splits;
     const uint32_t rest = t_local / ds.splits;
     const uint32_t tm = rest % ds.tiles_m, tn = rest / ds.tiles_m;
-    const uint32_t m0 = tm * 32u * MT, n0 = tn * mmqh::BN;
+    const uint32_t m0 = tm * 32u * MT, n0 = tn * (ds.gu_pair ? mmqh::BN / 2u : mmqh::BN);
     const uint32_t sub = min((uint32_t)MT, (ds.m - m0 + 31u) / 32u);  // 32-row tiles with rows
     auto run = [&](auto mt) {
         constexpr int M = decltype(mt)::value;

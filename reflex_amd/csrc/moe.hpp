@@ -261,6 +261,9 @@ struct MoePlanArgs {
     // atomics, then a prefix sum of the counts); 0: a stable sort (token
     // order within an expert)
     uint32_t any_order;
+    // 1: gate and up in one descriptor per expert (MmqDesc::gu_pair; the
+    // template tg carries the pair fields, tu the up weights' base)
+    uint32_t gu_pair;
 };
 
 // Exclusive prefix sum of v over the 1024 threads of the workgroup (every
@@ -435,7 +438,8 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         tm = (m + a.bm - 1u) / a.bm;
         tmd = (m + a.bm_dn - 1u) / a.bm_dn;
     }
-    const uint32_t wg_gu = plan_scan(2u * tm * tn_f, tot), wg_dn = plan_scan(tmd * tn_h, tot);
+    const uint32_t gpe = a.gu_pair ? 1u : 2u;  // gate/up descriptors per expert
+    const uint32_t wg_gu = plan_scan(gpe * tm * tn_f, tot), wg_dn = plan_scan(tmd * tn_h, tot);
     // Descriptors from the templates, 128 experts at a time: filled in LDS
     // (the pairs' weights are no longer needed: their space holds them),
     // then stored with consecutive threads on consecutive words (one thread
@@ -449,8 +453,8 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
         if (tid >= c0 && tid < c0 + nc) {
             const uint32_t e = tid;
             const uint32_t st = m ? start[e] : 0u;  // (an expert with no rows has no tiles)
-            MmqDesc* g = stg + 2u * (e - c0);
-            MmqDesc* u = g + 1;
+            MmqDesc* g = stg + gpe * (e - c0);
+            MmqDesc* u = g + 1;  // (not used for a pair)
             MmqDesc* d = stg + 2u * kChunk + (e - c0);
             {
                 const uint32_t* tg = reinterpret_cast<const uint32_t*>(&a.tg);
@@ -462,19 +466,25 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
 #pragma unroll
                 for (uint32_t i = 0; i < kDw; i++) {
                     pg[i] = tg[i];
-                    pu[i] = tu[i];
+                    if (!a.gu_pair) pu[i] = tu[i];
                     pd[i] = td[i];
                 }
             }
             g->w = a.tg.w + (uint64_t)e * a.w_stride_gu;
-            u->w = a.tu.w + (uint64_t)e * a.w_stride_gu;
+            if (a.gu_pair) g->w_up = a.tu.w + (uint64_t)e * a.w_stride_gu;
+            else u->w = a.tu.w + (uint64_t)e * a.w_stride_gu;
             d->w = a.td.w + (uint64_t)e * a.w_stride_dn;
-            g->rows = u->rows = a.pair_row + st;
-            g->m = u->m = d->m = m;
-            g->tiles_m = u->tiles_m = tm;
+            g->rows = a.pair_row + st;
+            g->m = d->m = m;
+            g->tiles_m = tm;
             d->tiles_m = tmd;
             g->y = a.tg.y + (uint64_t)st * a.ffn;
-            u->y = a.tu.y + (uint64_t)st * a.ffn;
+            if (!a.gu_pair) {
+                u->rows = a.pair_row + st;
+                u->m = m;
+                u->tiles_m = tm;
+                u->y = a.tu.y + (uint64_t)st * a.ffn;
+            }
             if (a.f16) {  // xh rows of 2*ffn bytes, xsx records of ffn/256 * 32 bytes, xrs
                 d->xq = a.td.xq + (uint64_t)st * a.ffn * 2u;
                 d->xds = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.td.xds) +
@@ -486,14 +496,14 @@ extern "C" __global__ __launch_bounds__(1024) void rfxq_moe_plan(MoePlanArgs a) 
             }
             d->y = a.td.y + (uint64_t)st * a.hidden;
             g->wg_begin = wg_gu;
-            u->wg_begin = wg_gu + tm * tn_f;
+            if (!a.gu_pair) u->wg_begin = wg_gu + tm * tn_f;
             d->wg_begin = wg_dn;
         }
         __syncthreads();
         const uint32_t* sw = reinterpret_cast<const uint32_t*>(stg);
-        uint32_t* gu_out = reinterpret_cast<uint32_t*>(a.descs_gu + 2u * c0);
+        uint32_t* gu_out = reinterpret_cast<uint32_t*>(a.descs_gu + gpe * c0);
         uint32_t* dn_out = reinterpret_cast<uint32_t*>(a.descs_dn + c0);
-        for (uint32_t i = tid; i < 2u * nc * kDw; i += 1024u) gu_out[i] = sw[i];
+        for (uint32_t i = tid; i < gpe * nc * kDw; i += 1024u) gu_out[i] = sw[i];
         for (uint32_t i = tid; i < nc * kDw; i += 1024u) dn_out[i] = sw[2u * kChunk * kDw + i];
     }
 }

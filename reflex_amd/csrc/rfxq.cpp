@@ -103,11 +103,16 @@ struct MmqDesc {
     float* y;
     uint32_t m, n, k, type;
     uint32_t ldq, ldy, tiles_m, tiles_n;
-    uint32_t splits, sb_per_split, wg_begin, pad;
-    int32_t* dots_out;
+    uint32_t splits, sb_per_split, wg_begin;
+    uint32_t gu_pair;  // gate/up pair with silu(gate) * up stored (Q4_K f16 tiles)
+    union {
+        int32_t* dots_out;
+        const uint8_t* w_up;
+    };
     const float* xrs;
 };
 constexpr uint32_t kMmqInline = 2;
+constexpr uint32_t mmqh_pair_bn = 128;  // columns of a gate/up pair tile (mmqh.hpp)
 struct MmqArgs {
     const MmqDesc* table;
     uint32_t ndesc, pad;
@@ -2662,6 +2667,7 @@ struct MoePlanArgs {
     uint32_t normalize;
     float scale;
     uint32_t any_order;
+    uint32_t gu_pair;
 };
 static_assert(sizeof(MoePlanArgs) == 624, "MoePlanArgs layout");
 
@@ -2892,6 +2898,16 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
     pa.ffn = ffn;
     pa.hidden = hidden;
     pa.any_order = gemv_form ? 0u : 1u;  // (the GEMV form keeps token order within an expert)
+    // Q4_K gate / up on the f16 tiles: one pair descriptor per expert whose
+    // tiles store silu(gate) * up (f32, into gout), then one f16 activation
+    // pass for down (RFXQ_MOE_GU_PAIR=0: gate and up GEMMs, then SiLU·up)
+    const char* gp = std::getenv("RFXQ_MOE_GU_PAIR");
+    const bool gu_pair = !gemv_form && f16 && gate->ggml_type == RFXQ_TYPE_Q4_K && !(gp && std::strcmp(gp, "0") == 0);
+    if (gu_pair) {
+        pa.gu_pair = 1u;
+        pa.tg.gu_pair = 1u;
+        pa.tg.tiles_n = (ffn + mmqh_pair_bn - 1u) / mmqh_pair_bn;
+    }
     GemvItem ig, iu, id;
     if (gemv_form) {
         if (int rc = make_gemv_item(x, &g0, gout, &ig)) return rc;
@@ -2945,10 +2961,15 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
         // launch grids: upper bounds on the tiles (sum over experts of
         // ceil(rows_e / bm) <= ceil(P / bm) + experts); surplus workgroups return
         const uint32_t bound_gu = (P + bm - 1u) / bm + expert_count, bound_dn = (P + bm_dn - 1u) / bm_dn + expert_count;
-        if (int rc = launch_mmq(c, gate->ggml_type, nullptr, 2u * expert_count, d_gu,
-                                2u * bound_gu * pa.tg.tiles_n, false, stream, f16, bm))
+        const uint32_t gpe = gu_pair ? 1u : 2u;
+        if (int rc = launch_mmq(c, gate->ggml_type, nullptr, gpe * expert_count, d_gu,
+                                gpe * bound_gu * pa.tg.tiles_n, false, stream, f16, bm))
             return rc;
-        if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
+        if (gu_pair) {
+            if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, false, true, stream)) return rc;
+        } else if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) {
+            return rc;
+        }
         if (int rc = launch_mmq(c, down->ggml_type, nullptr, expert_count, d_dn, bound_dn * pa.td.tiles_n, false,
                                 stream, f16, bm_dn))
             return rc;

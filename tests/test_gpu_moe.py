@@ -363,3 +363,40 @@ def test_moe_device_prefill_bit_stable(rq, orc):
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().reshape(512, 2048), y_d), f"call {i}"
     assert orc.rel_err_row_l2(y_d, ref) < TOL
+
+
+@pytest.mark.parametrize("tokens,experts,hidden,ffn,k,down_ty", [(512, 128, 2048, 768, 8, Q4K), (64, 16, 512, 256, 4, Q4K),
+                                                                  (300, 8, 512, 512, 2, Q4K), (512, 128, 2048, 768, 8, Q6K)])
+def test_moe_gate_up_pair_matches_separate(rq, orc, tokens, experts, hidden, ffn, k, down_ty):
+    """Device-routed prefill with Q4_K gate / up: the pair tiles (gate and up
+    columns in one workgroup, silu(gate) * up stored from the epilogue, then
+    one f16 activation pass) give the separate gate and up GEMMs + SiLU·up
+    launch's output bit for bit (RFXQ_MOE_GU_PAIR=0 selects the latter), and
+    meet the bound against the host reference."""
+    import os
+    seed = 1500 + tokens + experts + ffn + down_ty
+    gate = synth.weights(Q4K, experts * ffn, hidden, seed)
+    up = synth.weights(Q4K, experts * ffn, hidden, seed + 1)
+    down = synth.weights(down_ty, experts * hidden, ffn, seed + 2)
+    x = _dev(synth.activations(tokens * hidden, seed + 3))
+    logits = synth.normals(seed + 4, tokens * experts).reshape(tokens, experts)
+    dty = rq.GgmlType.Q4K if down_ty == Q4K else rq.GgmlType.Q6K
+    ws = (rq.Weight(rq.GgmlType.Q4K, _dev(gate), [hidden, ffn, experts]),
+          rq.Weight(rq.GgmlType.Q4K, _dev(up), [hidden, ffn, experts]),
+          rq.Weight(dty, _dev(down), [ffn, hidden, experts]))
+    lg = _dev(logits)
+    outs = {}
+    try:
+        for pair in ("1", "0"):
+            os.environ["RFXQ_MOE_GU_PAIR"] = pair
+            out = torch.empty(tokens * hidden, device=DEV)
+            rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+            torch.cuda.synchronize()
+            outs[pair] = out.cpu().numpy().reshape(tokens, hidden)
+    finally:
+        os.environ.pop("RFXQ_MOE_GU_PAIR", None)
+    assert np.array_equal(outs["1"], outs["0"])
+    routes = [orc.route_top_k(logits[t], k) for t in range(tokens)]
+    ref = orc.moe_ffn_grouped_reference(x.cpu().numpy().reshape(tokens, hidden), routes, gate, up, down, Q4K,
+                                        hidden, ffn, experts, down_ty=down_ty)
+    assert orc.rel_err_row_l2(outs["1"], ref) < TOL
