@@ -602,6 +602,34 @@ def prefill_leg(rq, synth, torch, np, dev, timed):
         "silu_and_mul_then_quantize_us": round(ms_unfused * 1e3, 1)}
     print(f"producers 8B M=512: rmsnorm_q8_1 {ms_rms * 1e3:.1f} us, silu_and_mul_q8_1 {ms_silu * 1e3:.1f} us "
           f"(unfused {ms_unfused * 1e3:.1f} us)", file=sys.stderr, flush=True)
+    del x, gate, up, tmp
+    # an 8B FFN's gate + up + SiLU·up at M=512 from the rmsnorm's buffer, up to
+    # the down GEMM's activation buffer: two GEMMs and the fused SiLU·up
+    # producer, against rfxq_gemm_gate_up_silu_q8_1 (gate/up pair tiles)
+    wg = rq.Weight.from_blocks(synth.Q4K, synth.weights(synth.Q4K, ffn, hid, synth.seed_for(4, 0, 4)), hid, ffn,
+                               device=dev)
+    wu = rq.Weight.from_blocks(synth.Q4K, synth.weights(synth.Q4K, ffn, hid, synth.seed_for(4, 0, 5)), hid, ffn,
+                               device=dev)
+    g_out = torch.empty(rows * ffn, device=dev)
+    u_out = torch.empty(rows * ffn, device=dev)
+    y_s = torch.empty(rows * ffn, device=dev)
+
+    def separate(i):
+        rq.gemm_q8_1(act_h, wg, rows, out=g_out)
+        rq.gemm_q8_1(act_h, wu, rows, out=u_out)
+        lib.rfxq_silu_and_mul_q8_1(g_out.data_ptr(), u_out.data_ptr(), rows, ffn, act_f.data_ptr(), None, st())
+
+    def fused(i):
+        lib.rfxq_gemm_gate_up_silu_q8_1(act_h.data_ptr(), rows, wg.cref(), wu.cref(), act_f.data_ptr(),
+                                        y_s.data_ptr(), None, 0, st())
+
+    ms_sep = timed(separate, 40, 20)
+    ms_fus = timed(fused, 40, 20)
+    ops = 2 * 2 * rows * ffn * hid
+    out["gate_up_silu_8b_m512"] = {"separate_us": round(ms_sep * 1e3, 1), "fused_us": round(ms_fus * 1e3, 1),
+                                   "fused_tops": round(ops / (ms_fus * 1e-3) / 1e12, 1)}
+    print(f"8B gate + up + SiLU·up M=512: separate {ms_sep * 1e3:.1f} us, fused {ms_fus * 1e3:.1f} us "
+          f"({ops / (ms_fus * 1e-3) / 1e12:.0f} TOPS)", file=sys.stderr, flush=True)
     return out
 
 

@@ -254,9 +254,27 @@ int rfxq_rmsnorm_q8_1(const float* x, const float* weight, uint32_t rows, uint32
                       float* y, hipStream_t stream);
 
 /* Model::silu_and_mul (src/kernels_cuda/silu_and_mul.cu:7-23) fused with the
- * quantization of its output (y optional, equal to rfxq_silu_and_mul's). */
+ * quantization of its output (y optional, equal to rfxq_silu_and_mul's; it
+ * must not alias gate or up, which are read once per layout). */
 int rfxq_silu_and_mul_q8_1(const float* gate, const float* up, uint32_t rows, uint32_t k, void* act, float* y,
                            hipStream_t stream);
+
+/* An FFN's gate and up GEMMs with Model::silu_and_mul fused into them: from
+ * one activation buffer, y = silu(x . Wg^T) * (x . Wu^T) [rows][ffn] (f32,
+ * required) and act_out (rfxq_act_q8_1_size(rows, ffn) bytes) =
+ * rfxq_quantize_act_q8_1(y), ready for the down GEMM (rfxq_gemm_q8_1).
+ * Replaces gemm(gate) + gemm(up) + silu_and_mul (src/model/dense.rs:1476-1478,
+ * silu_and_mul.cu:7-23) with the same values: for Q4_K weights on the f16
+ * kernels one launch whose tiles hold gate and up columns of the same outputs
+ * (no gate / up outputs in memory) and one quantization launch; otherwise
+ * the separate GEMMs and rfxq_silu_and_mul_q8_1, with
+ * rfxq_gemm_gate_up_silu_workspace_size bytes of workspace (0 for the fused
+ * form; NULL uses the library's). No single reference counterpart. gate and
+ * up must have one type and shape. */
+int rfxq_gemm_gate_up_silu_q8_1(const void* act, uint32_t rows, const rfxq_weight* gate, const rfxq_weight* up,
+                                void* act_out, float* y, void* workspace, uint64_t workspace_bytes,
+                                hipStream_t stream);
+uint64_t rfxq_gemm_gate_up_silu_workspace_size(const rfxq_weight* gate, uint32_t rows);
 
 /* rfxq_gemm / rfxq_gemm_batch from an activation buffer (rows as written).
  * The workspace holds split-K partials only (rfxq_gemm_workspace_size

@@ -110,6 +110,8 @@ SIGNATURES = {
     "rfxq_rmsnorm_q8_1": (_I, [_P, _P, _U32, _U32, ctypes.c_float, _P, _P, _P]),
     "rfxq_silu_and_mul_q8_1": (_I, [_P, _P, _U32, _U32, _P, _P, _P]),
     "rfxq_gemm_q8_1": (_I, [_P, _U32, _WP, _P, _P, _U64, _P]),
+    "rfxq_gemm_gate_up_silu_q8_1": (_I, [_P, _U32, _WP, _WP, _P, _P, _P, _U64, _P]),
+    "rfxq_gemm_gate_up_silu_workspace_size": (_U64, [_WP, _U32]),
     "rfxq_gemm_q8_1_batch": (_I, [_P, _U32, _U32, _P]),
     "rfxq_gemm_q8_1_plan_create": (_I, [_P, _U32, _U32, _I, ctypes.POINTER(_P)]),
 }

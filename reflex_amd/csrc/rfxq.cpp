@@ -2075,6 +2075,79 @@ int rfxq_gemm_q8_1(const void* act, uint32_t rows, const rfxq_weight* w, float* 
     return ok();
 }
 
+// the fused form of rfxq_gemm_gate_up_silu_q8_1: Q4_K gate / up on the f16 kernels
+static bool gate_up_pair_ok(const rfxq_weight* gate, const rfxq_options& o) {
+    return o.mmq_f16 && gate->ggml_type == RFXQ_TYPE_Q4_K && f16_capable(gate->ggml_type, gate->in_features, 0);
+}
+
+uint64_t rfxq_gemm_gate_up_silu_workspace_size(const rfxq_weight* gate, uint32_t rows) {
+    if (!gate || rows == 0 || !options_ok()) return 0;
+    if (gate_up_pair_ok(gate, opt())) return 0;
+    // the gate and up GEMMs' outputs, then their split-K partials
+    return 2u * align256((uint64_t)rows * gate->out_features * 4u) + rfxq_gemm_workspace_size(gate, std::max(rows, 2u));
+}
+
+int rfxq_gemm_gate_up_silu_q8_1(const void* act, uint32_t rows, const rfxq_weight* gate, const rfxq_weight* up,
+                                void* act_out, float* y, void* workspace, uint64_t workspace_bytes,
+                                hipStream_t stream) {
+    if (int rc = check_mmq_weight(gate, "gemm_gate_up_silu_q8_1 gate")) return rc;
+    if (int rc = check_mmq_weight(up, "gemm_gate_up_silu_q8_1 up")) return rc;
+    if (gate->ggml_type != up->ggml_type || gate->in_features != up->in_features ||
+        gate->out_features != up->out_features || gate->len != up->len)
+        return fail(RFXQ_ERR_OTHER, "gemm_gate_up_silu_q8_1: gate and up must share a type and shape");
+    const uint32_t k = gate->in_features, ffn = gate->out_features;
+    if (int rc = check_act(act, rows, k, "gemm_gate_up_silu_q8_1")) return rc;
+    if (int rc = check_act(act_out, rows, ffn, "gemm_gate_up_silu_q8_1 act_out")) return rc;
+    if (!y || reinterpret_cast<uintptr_t>(y) % 16u)
+        return fail(RFXQ_ERR_INVALID_INPUT, "gemm_gate_up_silu_q8_1: y is NULL or not 16-byte aligned");
+    Ctx* c;
+    if (int rc = current_ctx(&c)) return rc;
+    rfxq_options o;
+    if (int rc = get_options(&o)) return rc;
+    if (gate_up_pair_ok(gate, o)) {
+        // one launch of pair tiles (128 columns: gate in waves 0-1, up in 2-3,
+        // silu(gate) * up stored), never split along K
+        MmqDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.w = gate->data;
+        d.w_up = static_cast<const uint8_t*>(up->data);
+        act_desc(&d, static_cast<const uint8_t*>(act), act_layout(rows, k), true, k);
+        d.y = y;
+        d.m = rows;
+        d.n = ffn;
+        d.k = k;
+        d.type = gate->ggml_type;
+        d.ldy = ffn;
+        const uint32_t tile_m = f16_tile_m(rows);
+        d.tiles_m = (rows + tile_m - 1u) / tile_m;
+        d.tiles_n = (ffn + mmqh_pair_bn - 1u) / mmqh_pair_bn;
+        d.splits = 1;
+        d.sb_per_split = k / 256u;
+        d.gu_pair = 1;
+        if (int rc = launch_mmq(c, d.type, &d, 1, nullptr, d.tiles_m * d.tiles_n, false, stream, true, tile_m))
+            return rc;
+        return rfxq_quantize_act_q8_1(y, rows, ffn, act_out, stream);
+    }
+    // separate GEMMs into the workspace, then SiLU·up into y and act_out
+    // (not in place: rfxq_silu_and_mul_q8_1 reads its inputs once per layout)
+    const uint64_t u_bytes = align256((uint64_t)rows * ffn * 4u);
+    const uint64_t need = rfxq_gemm_gate_up_silu_workspace_size(gate, rows);
+    void* ws = workspace;
+    if (!ws) {
+        if (int rc = ctx_workspace(c, need, &ws, stream)) return rc;
+    } else if (workspace_bytes < need) {
+        return fail(RFXQ_ERR_INVALID_INPUT, "gemm_gate_up_silu_q8_1: workspace of %llu bytes, needs %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)need);
+    }
+    uint8_t* wb = static_cast<uint8_t*>(ws);
+    float* g = reinterpret_cast<float*>(wb);
+    float* u = reinterpret_cast<float*>(wb + u_bytes);
+    uint8_t* part = wb + 2u * u_bytes;
+    if (int rc = rfxq_gemm_q8_1(act, rows, gate, g, part, need - 2u * u_bytes, stream)) return rc;
+    if (int rc = rfxq_gemm_q8_1(act, rows, up, u, part, need - 2u * u_bytes, stream)) return rc;
+    return rfxq_silu_and_mul_q8_1(g, u, rows, ffn, act_out, y, stream);
+}
+
 int rfxq_gemm_q8_1_batch(const rfxq_gemm_q8_1_item* items, uint32_t count, uint32_t rows, hipStream_t stream) {
     if (count == 0) return ok();
     if (!items) return fail(RFXQ_ERR_INVALID_INPUT, "gemm_q8_1_batch: items is NULL");

@@ -27,6 +27,7 @@ __all__ = [
     "moe_gather", "moe_scatter_add", "silu_and_mul", "moe_ffn_grouped", "init",
     "moe_route_device", "moe_ffn_grouped_device",
     "act_q8_1_size", "quantize_act_q8_1", "rmsnorm_q8_1", "silu_and_mul_q8_1", "gemm_q8_1", "gemm_q8_1_batch",
+    "gemm_gate_up_silu_q8_1",
     "get_options", "set_options", "options", "gemm_policy", "PATH_GEMV_ROWS", "PATH_MMQ_INT8", "PATH_MMQ_F16",
 ]
 
@@ -419,6 +420,18 @@ def gemm_q8_1(act: torch.Tensor, w: Weight, rows: int, out: torch.Tensor | None 
     with _dev(act):
         _check(lib().rfxq_gemm_q8_1(act.data_ptr(), rows, w.cref(), y.data_ptr(), None, 0, _stream()))
     return y
+
+
+def gemm_gate_up_silu_q8_1(act: torch.Tensor, rows: int, gate: Weight, up: Weight):
+    """gemm(gate) + gemm(up) + silu_and_mul fused (dense.rs:1476-1478):
+    (act_out for the down GEMM, y = silu(gate) * up [rows][ffn] f32)."""
+    ffn = gate.out_features
+    act_out = _act(rows, ffn, act.device)
+    y = torch.empty(rows * ffn, dtype=torch.float32, device=act.device)
+    with _dev(act):
+        _check(lib().rfxq_gemm_gate_up_silu_q8_1(act.data_ptr(), rows, gate.cref(), up.cref(), act_out.data_ptr(),
+                                                 y.data_ptr(), None, 0, _stream()))
+    return act_out, y
 
 
 def gemm_q8_1_batch(items: list[tuple[torch.Tensor, Weight, torch.Tensor]], rows: int) -> None:

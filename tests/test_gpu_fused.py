@@ -134,3 +134,35 @@ def test_gemm_q8_1_plan_matches_f32_plan(rq):
             plan.run()
             for (_, _, a), (_, _, b) in zip(f32_items, q_items):
                 assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("ty", [Q4K, Q6K])
+@pytest.mark.parametrize("rows,ffn,k", [(512, 3072, 1024), (64, 768, 2048), (12, 3072, 1024), (300, 1280, 1024),
+                                        (512, 14336, 4096)])
+def test_gemm_gate_up_silu_q8_1(rq, orc, opts, ty, rows, ffn, k):
+    """gemm(gate) + gemm(up) + silu_and_mul fused: y and the activation
+    buffer equal the separate GEMMs (for Q4_K with split-K off, as the fused
+    tiles never split) followed by rfxq_silu_and_mul_q8_1, bit for bit (Q4_K: one launch
+    of gate/up pair tiles at 32-, 64- and 128-row tiles; Q6_K: the separate
+    path itself), and y meets the bound against dequant + f64."""
+    x = synth.activations(rows * k, 31 + rows)
+    gate_np = synth.weights(ty, ffn, k, 32 + ffn)
+    up_np = synth.weights(ty, ffn, k, 33 + ffn)
+    gate = rq.Weight.from_blocks(ty, gate_np, k, ffn, device=DEV)
+    up = rq.Weight.from_blocks(ty, up_np, k, ffn, device=DEV)
+    act = rq.quantize_act_q8_1(_dev(x), rows, k)
+    opts(quant_mma_splits=1 if ty == Q4K else 0)   # (the separate path keeps the default split policy)
+    g = rq.gemm_q8_1(act, gate, rows)
+    u = rq.gemm_q8_1(act, up, rows)
+    want_act, want_y = rq.silu_and_mul_q8_1(g, u, rows, ffn, want_y=True)
+    opts(quant_mma_splits=0)
+    got_act, got_y = rq.gemm_gate_up_silu_q8_1(act, rows, gate, up)
+    assert torch.equal(got_y, want_y)
+    _same_act(got_act, want_act, rows, ffn)
+    if rows * ffn * k <= 512 * 3072 * 1024:
+        xs = x.reshape(rows, k).astype(np.float64)
+        gr = orc.reference_gemm(ty, gate_np, ffn, k, xs)
+        ur = orc.reference_gemm(ty, up_np, ffn, k, xs)
+        with np.errstate(over="ignore"):
+            ref = gr / (1.0 + np.exp(-gr)) * ur
+        assert orc.rel_err_row_l2(got_y.cpu().numpy().reshape(rows, ffn), ref) < 1e-3
