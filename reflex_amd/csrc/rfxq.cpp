@@ -871,6 +871,7 @@ uint32_t tile_bn(bool f16) { return f16 ? 256u : 128u; }
 //   REFLEX_QUANT_MMA_SPLITS forces the count.
 enum : uint32_t { PATH_GEMV_ROWS = RFXQ_PATH_GEMV_ROWS, PATH_MMQ_INT8 = RFXQ_PATH_MMQ_INT8, PATH_MMQ_F16 = RFXQ_PATH_MMQ_F16 };
 constexpr uint32_t kGemvRowsMax = 4;
+constexpr uint64_t kGemvReread = 56ull << 20;  // bytes of weight re-reads above which few rows take tiles
 
 // Super-blocks per split-K workgroup for the GEMMs of one launch (their
 // tile counts and super-blocks per row): the fewest, at least min_sb, whose
@@ -936,14 +937,27 @@ uint32_t small_gemm_tile_m(uint32_t tile_m, uint32_t rows, uint32_t n, uint32_t 
     return tile_m;
 }
 
+// raw bytes of a weight matrix
+uint64_t gemm_weight_bytes(uint32_t ty, uint32_t k, uint32_t n) {
+    return ty == RFXQ_TYPE_Q8_0 ? (uint64_t)n * (k / 32u) * 34u : (uint64_t)n * (k / 256u) * (ty == RFXQ_TYPE_Q6_K ? 210u : 144u);
+}
+
 rfxq_gemm_policy gemm_policy(uint32_t ty, uint32_t k, uint32_t n, uint32_t rows, uint32_t cus, const rfxq_options& o,
-                             bool alone = true) {
+                             bool alone = true, uint64_t group_bytes = 0) {
     rfxq_gemm_policy p;
     std::memset(&p, 0, sizeof p);
     p.splits = 1;
     const bool f16 = o.mmq_f16 && f16_capable(ty, k, 0);
+    // f16 path: up to kGemvRowsMax rows run as GEMVs, except 3+ rows whose
+    // re-reads of the weights ((rows - 1) x their bytes: this GEMM's alone,
+    // or `group_bytes`, a grouped launch's, so that all of its GEMMs take one
+    // path) would reach kGemvReread (56 MiB): they read them once on 32-row tiles (an
+    // 8B layer at 3 / 4 rows: 78 us on tiles against 84-87 / 90-109 us as
+    // GEMVs or mixed; a 0.6B layer, 9 MB, stays faster as GEMVs at 2-4 rows)
+    const uint64_t wbytes = group_bytes ? group_bytes : gemm_weight_bytes(ty, k, n);
+    const bool few_gemv = rows <= kGemvRowsMax && (rows <= 2u || (uint64_t)(rows - 1u) * wbytes < kGemvReread);
     const bool gemv = rows <= 1 || !o.quant_mma || (o.quant_mma_max_rows && rows > o.quant_mma_max_rows) ||
-                      (rows <= o.fused_max_rows && (!f16 || rows <= kGemvRowsMax)) || k % 256u != 0 ||
+                      (rows <= o.fused_max_rows && (!f16 || few_gemv)) || k % 256u != 0 ||
                       (o.mmq_f16 && !f16);
     if (gemv) {
         p.path = PATH_GEMV_ROWS;
@@ -1295,6 +1309,9 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
     rfxq_options o;
     if (int rc = get_options(&o)) return rc;
     std::vector<uint32_t> item_act(count, ~0u), item_kernel(count, 0);
+    uint64_t group_bytes = 0;  // the few-row path is chosen for the group as a whole
+    for (uint32_t i = 0; i < count; i++)
+        if (items[i].w) group_bytes += gemm_weight_bytes(items[i].w->ggml_type, items[i].w->in_features, items[i].w->out_features);
     for (uint32_t i = 0; i < count; i++) {
         const rfxq_gemm_item& it = items[i];
         if (int rc = check_weight(it.w, "gemm group")) return rc;
@@ -1302,7 +1319,7 @@ int build_gemm_group(const rfxq_gemm_item* items, uint32_t count, uint32_t rows,
         if (reinterpret_cast<uintptr_t>(it.x) % (ext ? 256u : 16u))
             return fail(RFXQ_ERR_OTHER, "gemm group: x of item %u is not %u-byte aligned", i, ext ? 256u : 16u);
         const uint32_t k = it.w->in_features;
-        rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o, count == 1u);
+        rfxq_gemm_policy pol = gemm_policy(it.w->ggml_type, k, it.w->out_features, rows, cus, o, count == 1u, group_bytes);
         if (ext) {
             if (int rc = check_act(it.x, rows, k, "gemm_q8_1 plan")) return rc;
             const bool f16 = o.mmq_f16 && f16_capable(it.w->ggml_type, k, 0);

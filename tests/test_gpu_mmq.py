@@ -185,11 +185,13 @@ def test_gemm_prefill_8b_sampled_rows(rq, orc, name, ty, n, k):
     _check_gemm(rq, orc, ty, 512, n, k, synth.weights(ty, n, k, seed), x, rows)
 
 
-@pytest.mark.parametrize("rows", [5, 12, 29, 48])
+@pytest.mark.parametrize("rows", [3, 4, 5, 12, 29, 48])
 @pytest.mark.parametrize("name,ty,n,k", [c for c in synth.QWEN3_8B_LAYER if c[0] in ("q_proj", "down_proj")],
                          ids=["q_proj", "down_proj"])
 def test_gemm_few_rows_8b(rq, orc, rows, name, ty, n, k):
-    """The few-row paths (32- and 64-row tiles, every row checked) at the 8B shapes."""
+    """The few-row paths (GEMVs per row for q_proj at 3-4 rows, 32-row tiles
+    for down at 3-4 rows and for both from 5 rows, 64-row tiles; every row
+    checked) at the 8B shapes."""
     seed = synth.seed_for(4, 3, rows)
     x = synth.activations(rows * k, seed + 1000).reshape(rows, k)
     _check_gemm(rq, orc, ty, rows, n, k, synth.weights(ty, n, k, seed), x)
@@ -351,6 +353,26 @@ def test_gemm_caller_workspace(rq, orc):
     assert orc.rel_err_row_l2(y, orc.mmqh_model_reference(Q6K, w_np, n, k, x)) < MODEL_TOL
     with pytest.raises(rq.ReflexError):
         rq.gemm(_dev(x), w, m, workspace=ws[:100])
+
+
+def test_gemm_plan_few_rows_large_group(rq, orc):
+    """A grouped plan of an 8B layer at 3 rows takes one path for all its
+    GEMMs (their re-reads together pass 56 MiB: 32-row tiles), and each
+    output meets the bound against dequant + f64."""
+    rows = 3
+    items, refs = [], []
+    xs = {}
+    for i, (name, ty, n, k) in enumerate(synth.QWEN3_8B_LAYER):
+        if k not in xs:
+            xs[k] = synth.activations(rows * k, 90 + k % 97).reshape(rows, k)
+        w_np = synth.weights(ty, n, k, 120 + i)
+        items.append((_dev(xs[k].reshape(-1)), _weight(rq, ty, w_np, n, k), torch.empty(rows * n, device=DEV)))
+        refs.append((ty, w_np, n, k, xs[k]))
+    rq.GemmPlan(items, rows).run()
+    torch.cuda.synchronize()
+    for (_, _, y), (ty, w_np, n, k, x) in zip(items, refs):
+        ref = orc.reference_gemm(ty, w_np, n, k, x)
+        assert orc.rel_err_row_l2(y.cpu().numpy().reshape(rows, n), ref) < TOL
 
 
 @pytest.mark.parametrize("rows", [300, 12, 29])

@@ -109,6 +109,14 @@ def test_policy_paths(rq):
     assert [pol(Q4K, 1024, 2048, m)["tile_m"] for m in (32, 33, 64, 65)] == [32, 64, 64, 128]
     with rq.options(fused_max_rows=2):
         assert pol(Q4K, 1024, 2048, 3)["path"] == F16
+    # 3-4 rows of a large matrix read it once on 32-row tiles: (rows - 1) x
+    # its bytes of re-reads reach 56 MiB (8B gate 14336 x 4096 Q4_K, 33 MB;
+    # down 4096 x 14336 Q6_K, 48 MB); 2 rows stay GEMVs
+    assert pol(Q4K, 4096, 14336, 2)["path"] == G
+    assert pol(Q4K, 4096, 14336, 3)["path"] == F16
+    assert pol(Q6K, 14336, 4096, 3)["path"] == F16
+    assert pol(Q4K, 4096, 4096, 4)["path"] == G          # 9.4 MB x 3: GEMVs when alone
+    assert pol(Q8_0, 4096, 14336, 3)["path"] == F16
     with rq.options(mmq_f16=0):   # the int8 path keeps GEMVs up to fused_max_rows
         assert pol(Q4K, 1024, 2048, 16)["path"] == G
         assert pol(Q4K, 1024, 2048, 17)["path"] == I8

@@ -29,11 +29,12 @@ def _pair(rq, x, w, rows):
 @pytest.mark.parametrize("ty,n,k,rows", [
     (Q4K, 4096, 4096, (512, 300)),   # f16 MMQ with split-K (8 splits), then fewer rows
     (Q6K, 1024, 3072, (512, 77)),    # Q6_K f16 MMQ
-    (Q4K, 2048, 1024, (12, 5)),      # few rows: one GEMV per row
+    (Q4K, 2048, 1024, (12, 5)),      # few rows: 32-row tiles
     (Q8_0, 1024, 1024, (64, 2)),     # Q8_0: f16 MMQ, then GEMV rows
     (Q8_0, 4096, 4096, (512, 9)),    # Q8_0 f16 MMQ, 128- then 32-row tiles
     (Q4K, 2048, 1024, (1, 1)),       # one row: the decode GEMV
-    (Q6K, 4096, 14336, (3, 1)),      # long rows (several passes per row) at a few rows, then one
+    (Q6K, 4096, 14336, (2, 1)),      # long rows (several passes per row) at a few rows, then one
+    (Q6K, 4096, 14336, (3, 2)),      # a large matrix at 3 rows (32-row tiles), then GEMV rows
     (Q4K, 1024, 14336, (4, 2)),
 ])
 def test_no_alloc_matches_gemm_two_calls(rq, ty, n, k, rows):
