@@ -2681,11 +2681,28 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         wg += d.tiles_m * d.tiles_n;
         descs.push_back(d);
     };
+    // Q4_K gate / up on the f16 tiles: one gate/up pair descriptor per expert
+    // (its tiles store SiLU·up into gout), then an f16 activation pass of it,
+    // as the device-routed path does (RFXQ_MOE_GU_PAIR=0: separate gate and up)
+    const char* gp = std::getenv("RFXQ_MOE_GU_PAIR");
+    const bool gu_pair = f16 && gate->ggml_type == RFXQ_TYPE_Q4_K && !(gp && std::strcmp(gp, "0") == 0);
     for (uint32_t e = 0; e < expert_count; e++) {
         const uint32_t m = off[e + 1] - off[e];
         if (!m) continue;
-        add(gate, e, B + o_x, Lx, 0, d_pr + off[e], m, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
-        add(up, e, B + o_x, Lx, 0, d_pr + off[e], m, uout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+        if (gu_pair) {
+            const uint32_t wg0 = wg_gu;
+            add(gate, e, B + o_x, Lx, 0, d_pr + off[e], m, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+            MmqDesc& d = descs.back();
+            rfxq_weight ue;
+            expert_slice(up, e, &ue, "moe_ffn_grouped");
+            d.w_up = static_cast<const uint8_t*>(ue.data);
+            d.gu_pair = 1u;
+            d.tiles_n = (ffn + mmqh_pair_bn - 1u) / mmqh_pair_bn;
+            wg_gu = wg0 + d.tiles_m * d.tiles_n;
+        } else {
+            add(gate, e, B + o_x, Lx, 0, d_pr + off[e], m, gout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+            add(up, e, B + o_x, Lx, 0, d_pr + off[e], m, uout + (uint64_t)off[e] * ffn, ffn, wg_gu);
+        }
     }
     const uint32_t n_gu = (uint32_t)descs.size();
     uint32_t wg_dn = 0;
@@ -2711,7 +2728,11 @@ int rfxq_moe_ffn_grouped(const float* x, uint32_t rows, uint32_t hidden, const f
         if (int rc = launch_mmq(c, gate->ggml_type, descs.data(), n_gu, d_desc, wg_gu, false, stream, f16, bm_gu))
             return rc;
     }
-    if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) return rc;
+    if (gu_pair) {
+        if (int rc = launch_act(c, gout, P, ffn, B + o_s, Ls, false, true, stream)) return rc;
+    } else if (int rc = launch_silu_act(c, gout, uout, P, ffn, B + o_s, Ls, !f16, f16, stream)) {
+        return rc;
+    }
     if (n_dn) {
         if (int rc = launch_mmq(c, down->ggml_type, descs.data() + n_gu, n_dn, d_desc + n_gu, wg_dn, false, stream,
                                 f16, bm_dn))

@@ -368,11 +368,11 @@ def test_moe_device_prefill_bit_stable(rq, orc):
 @pytest.mark.parametrize("tokens,experts,hidden,ffn,k,down_ty", [(512, 128, 2048, 768, 8, Q4K), (64, 16, 512, 256, 4, Q4K),
                                                                   (300, 8, 512, 512, 2, Q4K), (512, 128, 2048, 768, 8, Q6K)])
 def test_moe_gate_up_pair_matches_separate(rq, orc, tokens, experts, hidden, ffn, k, down_ty):
-    """Device-routed prefill with Q4_K gate / up: the pair tiles (gate and up
-    columns in one workgroup, silu(gate) * up stored from the epilogue, then
-    one f16 activation pass) give the separate gate and up GEMMs + SiLU·up
-    launch's output bit for bit (RFXQ_MOE_GU_PAIR=0 selects the latter), and
-    meet the bound against the host reference."""
+    """Prefill with Q4_K gate / up, device and host routing: the pair tiles
+    (gate and up columns in one workgroup, silu(gate) * up stored from the
+    epilogue, then one f16 activation pass) give the separate gate and up
+    GEMMs + SiLU·up launch's output bit for bit (RFXQ_MOE_GU_PAIR=0 selects
+    the latter), and meet the bound against the host reference."""
     import os
     seed = 1500 + tokens + experts + ffn + down_ty
     gate = synth.weights(Q4K, experts * ffn, hidden, seed)
@@ -389,13 +389,19 @@ def test_moe_gate_up_pair_matches_separate(rq, orc, tokens, experts, hidden, ffn
     try:
         for pair in ("1", "0"):
             os.environ["RFXQ_MOE_GU_PAIR"] = pair
-            out = torch.empty(tokens * hidden, device=DEV)
-            rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
-            torch.cuda.synchronize()
-            outs[pair] = out.cpu().numpy().reshape(tokens, hidden)
+            for dev_routing in (True, False):
+                out = torch.empty(tokens * hidden, device=DEV)
+                if dev_routing:
+                    rq.moe_ffn_grouped_device(x, tokens, hidden, lg, experts, k, True, 1.0, *ws, out)
+                else:
+                    rq.moe_ffn_grouped(x, tokens, hidden, logits, experts, k, True, 1.0, *ws, out)
+                torch.cuda.synchronize()
+                outs[(pair, dev_routing)] = out.cpu().numpy().reshape(tokens, hidden)
     finally:
         os.environ.pop("RFXQ_MOE_GU_PAIR", None)
-    assert np.array_equal(outs["1"], outs["0"])
+    for dev_routing in (True, False):
+        assert np.array_equal(outs[("1", dev_routing)], outs[("0", dev_routing)]), f"device routing {dev_routing}"
+    outs["1"] = outs[("1", True)]
     routes = [orc.route_top_k(logits[t], k) for t in range(tokens)]
     ref = orc.moe_ffn_grouped_reference(x.cpu().numpy().reshape(tokens, hidden), routes, gate, up, down, Q4K,
                                         hidden, ffn, experts, down_ty=down_ty)
