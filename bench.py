@@ -59,6 +59,8 @@ def main() -> int:
     ap.add_argument("--prefill-probe", nargs="?", const="gate8b", choices=("gate8b", "set06b"),
                     help="only run the 8B gate GEMM (14336x4096 Q4_K, M=512; gate8b, the default) or the "
                          "Qwen3-0.6B M=512 set's GEMM plan (set06b) a few times (for rocprofv3 --pmc runs)")
+    ap.add_argument("--moe-probe", action="store_true",
+                    help="only run config 5's device-routed MoE prefill (512 tokens) ten times (for rocprofv3 --pmc runs)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, WRITE_SIZE) of a "
                          "--traffic-probe run into profiles/gemv_decode06b_traffic.json")
@@ -107,6 +109,19 @@ def main() -> int:
         qplan = rq.GemmPlan(q_items, 512, quantized=True)
         for _ in range(10):
             qplan.run()
+        torch.cuda.synchronize()
+        return 0
+    if args.moe_probe:
+        cfg = synth.MOE
+        E, H, F, K, tokens = cfg["experts"], cfg["hidden"], cfg["ffn"], cfg["top_k"], cfg["tokens"]
+        gate, up, down = (rq.Weight.from_blocks(cfg["ty"], synth.weights(cfg["ty"], E * o, i, synth.seed_for(5, 0, p)),
+                                                i, o, expert_count=E, device=dev)
+                          for p, i, o in ((0, H, F), (1, H, F), (2, F, H)))
+        x = torch.from_numpy(synth.activations(tokens * H, synth.seed_for(5, 0, 3))).to(dev)
+        lg = torch.from_numpy(synth.normals(synth.seed_for(5, 0, 4), tokens * E).reshape(tokens, E)).to(dev)
+        y = torch.empty(tokens * H, device=dev)
+        for _ in range(10):
+            rq.moe_ffn_grouped_device(x, tokens, H, lg, E, K, True, 1.0, gate, up, down, y)
         torch.cuda.synchronize()
         return 0
     if args.prefill_probe:
