@@ -165,3 +165,28 @@ def test_synth_generators_deterministic_and_distributed():
     q8 = synth.weights(synth.Q8_0, 16, 1024, 7).reshape(-1, 34)[:, 2:].view(np.int8)
     assert q8.min() >= -127 and q8.max() <= 127
     assert synth.weight_bytes(synth.Q4K, 2048, 1024) == 1179648
+
+
+def test_gate_up_silu_preconditions_fail_before_gpu():
+    """rfxq_gemm_gate_up_silu_q8_1 checks its weights and buffers before any
+    device work, and asks for no workspace on the fused (Q4_K pair-tile)
+    path."""
+    rq = _lib()
+    L = rq.lib()
+    f = L.rfxq_gemm_gate_up_silu_q8_1
+    act, y = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    g4 = _w(rq, 12, 1024, 768)
+    u6 = _w(rq, 14, 1024, 768)
+    u4n = _w(rq, 12, 1024, 512)
+    for up in (u6, u4n):  # another type, another shape
+        rc = f(act, 4, ctypes.byref(g4), ctypes.byref(up), act, y, None, 0, None)
+        assert rc == 12 and "share a type and shape" in L.rfxq_last_error().decode()
+    rc = f(ctypes.c_void_p(4096 + 16), 4, ctypes.byref(g4), ctypes.byref(g4), act, y, None, 0, None)
+    assert rc == 12 and "256-byte aligned" in L.rfxq_last_error().decode()
+    rc = f(act, 4, ctypes.byref(g4), ctypes.byref(g4), act, ctypes.c_void_p(8192 + 4), None, 0, None)
+    assert rc == 11 and "16-byte aligned" in L.rfxq_last_error().decode()
+    rc = f(act, 0, ctypes.byref(g4), ctypes.byref(g4), act, y, None, 0, None)
+    assert rc == 12
+    assert L.rfxq_gemm_gate_up_silu_workspace_size(ctypes.byref(g4), 64) == 0
+    # the separate form (Q6_K): the two outputs, then the GEMMs' split-K partials
+    assert L.rfxq_gemm_gate_up_silu_workspace_size(ctypes.byref(_w(rq, 14, 1024, 768)), 64) >= 2 * 64 * 768 * 4
