@@ -153,47 +153,18 @@ RFXQ_DEV float wave_max(float v) {
 
 constexpr uint32_t kDecRouteMaxE = 256;  // experts the one-wave router takes (4 per lane)
 
-// float -> uint32 with the same order (larger float, larger key)
-RFXQ_DEV uint32_t order_key(float f) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// the wave's largest 64-bit key, uniform: DPP steps leave every lane with
-// its 16-lane row's largest, then the four rows' compare on the scalar unit
-// (selects throughout: no branches, no LDS round trip)
-RFXQ_DEV uint64_t wave_max_u64(uint64_t key) {
-#define RFXQ_MAX64_STEP(ctrl)                                                                              \
-    {                                                                                                      \
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)key, (ctrl), 0xF, 0xF, false); \
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(key >> 32), (ctrl), 0xF, 0xF, false); \
-        const uint64_t o = ((uint64_t)hi << 32) | lo;                                                      \
-        key = o > key ? o : key;                                                                           \
-    }
-    RFXQ_MAX64_STEP(0xB1);   // quad_perm [1,0,3,2]
-    RFXQ_MAX64_STEP(0x4E);   // quad_perm [2,3,0,1]
-    RFXQ_MAX64_STEP(0x141);  // row_half_mirror
-    RFXQ_MAX64_STEP(0x140);  // row_mirror
-#undef RFXQ_MAX64_STEP
-    uint64_t best = 0;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), 16 * r) << 32) |
-                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, 16 * r);
-        best = o > best ? o : best;
-    }
-    return best;
-}
-
 // route_top_k_with_norm (src/moe.rs:47-98) of one token by one wave (no
 // barrier, no LDS): softmax with the maximum subtracted (expf, the sum by a
 // fixed wave reduction), probabilities p = v / sum, and the k best by p
 // descending then index ascending (a NaN p ranks below every number),
 // renormalised by their sum in selection order when `normalize`, times
-// `scale`. Lane l holds experts l + 64 i; the k best are picked in k rounds
-// of a wave-wide maximum of 64-bit (probability order, index) keys. Deterministic, so every
-// wave of a token finds the same routing. Returns slot `slot`'s expert; lanes
-// < k write idx / wts when `write`.
+// `scale`. Lane l holds experts l + 64 i. Each of the k rounds takes the
+// wave-wide maximum of the ranking values (p; NaN -0.5, absent experts -2,
+// taken ones -3) and, among the experts holding it, the lowest index: the
+// first set bit of the ballots of chunks i = 0, 1, ... (p is never -0.0, so
+// float equality is the reference's tie). Deterministic, so every wave of a
+// token finds the same routing. Returns slot `slot`'s expert; lanes < k write
+// idx / wts when `write`.
 struct RouteLogits {
     float v[kDecRouteMaxE / 64u];
 };
@@ -226,32 +197,40 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
         sum += v[i];  // (absent experts add 0)
     }
     sum = group_sum<64>(sum);
-    // ranking keys: (order of p, then the lower index) in one 64-bit value;
-    // a NaN p ranks as -0.5, absent experts as -2, taken ones as 0
-    uint64_t rk[NV];
+    // ranking values: p, a NaN p -0.5, absent experts -2 (taken ones: -3)
+    float rv[NV];
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
         const uint32_t e = lane + 64u * i;
         v[i] = v[i] / sum;
-        rk[i] = ((uint64_t)order_key(e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f) << 32) | (uint32_t)~e;
+        rv[i] = e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f;
     }
     float my_p = 0.0f, top_sum = 0.0f;
     int32_t my_e = 0, pick = 0;
     for (uint32_t r = 0; r < k; r++) {
-        uint64_t bk = rk[0];
+        float m = rv[0];
 #pragma unroll
-        for (uint32_t i = 1; i < NV; i++) bk = rk[i] > bk ? rk[i] : bk;
-        bk = wave_max_u64(bk);
-        const uint32_t be = ~(uint32_t)bk;
-        // the winner's probability, read by its lane and broadcast
-        const uint32_t owner = be & 63u, oi = be >> 6;
-        float pv = 0.0f;
+        for (uint32_t i = 1; i < NV; i++)
+            if (64u * i < E) m = fmaxf(m, rv[i]);  // (E is uniform: chunks past it are skipped)
+        m = wave_max(m);
+        // the lowest expert holding the maximum
+        uint32_t be = 0xFFFFFFFFu;
 #pragma unroll
         for (uint32_t i = 0; i < NV; i++) {
-            pv = i == oi ? v[i] : pv;
-            rk[i] = rk[i] == bk ? 0ull : rk[i];  // taken
+            if (64u * i < E) {
+                const uint64_t bits = __ballot(rv[i] == m);
+                if (be == 0xFFFFFFFFu && bits) be = 64u * i + (uint32_t)__builtin_ctzll(bits);
+            }
         }
+        be = __builtin_amdgcn_readfirstlane(be);
+        // the winner's probability, read by its lane and broadcast
+        const uint32_t owner = be & 63u, oi = be >> 6;
+        float pv = v[0];
+#pragma unroll
+        for (uint32_t i = 1; i < NV; i++) pv = i == oi ? v[i] : pv;
         pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), owner));
+#pragma unroll
+        for (uint32_t i = 0; i < NV; i++) rv[i] = lane + 64u * i == be ? -3.0f : rv[i];  // taken
         top_sum += pv;  // in selection order
         if (lane == r) {
             my_p = pv;
@@ -269,7 +248,9 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
 template <typename T, int LPR>
 RFXQ_DEV void moe_dec_gu(const MoeDecArgs& a, uint8_t* lds) {
 #pragma clang fp contract(off)
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    // uniform: the wave picks the weight tensor, whose V# must stay scalar
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t per_t = a.k * a.nb1;
     const uint32_t t = blockIdx.x / per_t, j = (blockIdx.x / a.nb1) % a.k, b = blockIdx.x % a.nb1;
     const float* xt = a.x + (uint64_t)t * a.hidden;

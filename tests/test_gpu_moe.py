@@ -183,12 +183,14 @@ def test_moe_route_device_nan_logits_give_valid_experts(rq):
     assert np.isfinite(w[[0, 2]]).all()
 
 
-def _moe_device_case(rq, orc, tokens, experts, hidden, ffn, top_k, seed):
+def _moe_device_case(rq, orc, tokens, experts, hidden, ffn, top_k, seed, ties=False):
     gate = synth.weights(Q4K, experts * ffn, hidden, seed)
     up = synth.weights(Q4K, experts * ffn, hidden, seed + 1)
     down = synth.weights(Q4K, experts * hidden, ffn, seed + 2)
     x = _dev(synth.activations(tokens * hidden, seed + 3))
     logits = synth.normals(seed + 4, tokens * experts).reshape(tokens, experts)
+    if ties:  # whole numbers: many experts share each probability
+        logits = np.round(logits).astype(np.float32)
     W = lambda a, i, o: rq.Weight(rq.GgmlType.Q4K, _dev(a), [i, o, experts])  # noqa: E731
     ws = (W(gate, hidden, ffn), W(up, hidden, ffn), W(down, ffn, hidden))
     out_d = torch.empty(tokens * hidden, device=DEV)
@@ -247,6 +249,18 @@ def test_moe_ffn_grouped_device_decode(rq, orc, tokens, k):
     1-2 pairs exercise the table path of launches with few descriptors);
     5 tokens take the grouped MMQ path."""
     y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, 128, 2048, 768, k, 900 + tokens + k)
+    assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
+    assert orc.rel_err_row_l2(y_d, ref) < TOL
+
+
+@pytest.mark.parametrize("tokens,experts,k", [(1, 128, 8), (3, 128, 8), (2, 200, 8), (4, 40, 6), (1, 256, 16)])
+def test_moe_decode_tied_logits(rq, orc, tokens, experts, k):
+    """Decode routing in every workgroup of the gate/up launch with tied
+    probabilities (whole-number logits): the k best by probability, then the
+    lowest index, as the host router picks them (a different expert among
+    the tied ones would change the output by far more than the bound)."""
+    y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, experts, 256, 256, k, 990 + experts + tokens,
+                                              ties=True)
     assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
     assert orc.rel_err_row_l2(y_d, ref) < TOL
 
