@@ -140,15 +140,19 @@ struct MoeRowDot {
     }
 };
 
-// wave-wide maximum (every lane ends with it; order-independent)
+// wave-wide maximum (every lane ends with it; order-independent): DPP
+// steps leave each 16-lane row's maximum in its lanes, then the four rows'
+// are read out (no LDS round trip, as a swizzle across rows would take)
 RFXQ_DEV float wave_max(float v) {
     v = fmaxf(v, RFXQ_DPP(v, 0xB1));
     v = fmaxf(v, RFXQ_DPP(v, 0x4E));
     v = fmaxf(v, RFXQ_DPP(v, 0x141));
     v = fmaxf(v, RFXQ_DPP(v, 0x140));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
-    return fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
-                 __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
 }
 
 constexpr uint32_t kDecRouteMaxE = 256;  // experts the one-wave router takes (4 per lane)
@@ -185,15 +189,17 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
     float v[NV];
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) v[i] = rl.v[i];
+    // (chunks i with 64 i >= E hold no expert: skipped, a uniform branch)
     float mx = -INFINITY;
 #pragma unroll
-    for (uint32_t i = 0; i < NV; i++) mx = lane + 64u * i < E ? fmaxf(mx, v[i]) : mx;
+    for (uint32_t i = 0; i < NV; i++)
+        if (64u * i < E) mx = lane + 64u * i < E ? fmaxf(mx, v[i]) : mx;
     mx = wave_max(mx);
     float sum = 0.0f;
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
         const bool in = lane + 64u * i < E;
-        v[i] = in ? expf(v[i] - mx) : 0.0f;
+        v[i] = 64u * i < E && in ? expf(v[i] - mx) : 0.0f;
         sum += v[i];  // (absent experts add 0)
     }
     sum = group_sum<64>(sum);
@@ -202,7 +208,7 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
         const uint32_t e = lane + 64u * i;
-        v[i] = v[i] / sum;
+        if (64u * i < E) v[i] = v[i] / sum;
         rv[i] = e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f;
     }
     float my_p = 0.0f, top_sum = 0.0f;
