@@ -155,6 +155,23 @@ RFXQ_DEV float wave_max(float v) {
                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
 }
 
+// the same for 32-bit signed integers (the DPP moves fold into v_max_i32)
+RFXQ_DEV int32_t wave_max_i32(int32_t v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// float -> int32 of the same order (signed compare): negative floats have
+// their magnitude bits flipped
+RFXQ_DEV int32_t order_key(float f) {
+    const int32_t b = __builtin_bit_cast(int32_t, f);
+    return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+
 constexpr uint32_t kDecRouteMaxE = 256;  // experts the one-wave router takes (4 per lane)
 
 // route_top_k_with_norm (src/moe.rs:47-98) of one token by one wave (no
@@ -203,28 +220,29 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
         sum += v[i];  // (absent experts add 0)
     }
     sum = group_sum<64>(sum);
-    // ranking values: p, a NaN p -0.5, absent experts -2 (taken ones: -3)
-    float rv[NV];
+    // ranking keys: the order of p (a NaN p as -0.5, absent experts as -2;
+    // taken ones INT32_MIN), compared as integers
+    int32_t rk[NV];
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
         const uint32_t e = lane + 64u * i;
         if (64u * i < E) v[i] = v[i] / sum;
-        rv[i] = e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f;
+        rk[i] = order_key(e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f);
     }
     float my_p = 0.0f, top_sum = 0.0f;
     int32_t my_e = 0, pick = 0;
     for (uint32_t r = 0; r < k; r++) {
-        float m = rv[0];
+        int32_t m = rk[0];
 #pragma unroll
         for (uint32_t i = 1; i < NV; i++)
-            if (64u * i < E) m = fmaxf(m, rv[i]);  // (E is uniform: chunks past it are skipped)
-        m = wave_max(m);
+            if (64u * i < E) m = max(m, rk[i]);  // (E is uniform: chunks past it are skipped)
+        m = wave_max_i32(m);
         // the lowest expert holding the maximum
         uint32_t be = 0xFFFFFFFFu;
 #pragma unroll
         for (uint32_t i = 0; i < NV; i++) {
             if (64u * i < E) {
-                const uint64_t bits = __ballot(rv[i] == m);
+                const uint64_t bits = __ballot(rk[i] == m);
                 if (be == 0xFFFFFFFFu && bits) be = 64u * i + (uint32_t)__builtin_ctzll(bits);
             }
         }
@@ -236,7 +254,7 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
         for (uint32_t i = 1; i < NV; i++) pv = i == oi ? v[i] : pv;
         pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), owner));
 #pragma unroll
-        for (uint32_t i = 0; i < NV; i++) rv[i] = lane + 64u * i == be ? -3.0f : rv[i];  // taken
+        for (uint32_t i = 0; i < NV; i++) rk[i] = lane + 64u * i == be ? INT32_MIN : rk[i];  // taken
         top_sum += pv;  // in selection order
         if (lane == r) {
             my_p = pv;
