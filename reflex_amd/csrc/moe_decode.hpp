@@ -198,25 +198,25 @@ RFXQ_DEV void moe_route_load(const float* __restrict__ logits, uint32_t t, uint3
     for (uint32_t i = 0; i < kDecRouteMaxE / 64u; i++) rl.v[i] = as_f32(bld4(lr, 4u * (lane + 64u * i)));
 }
 
-RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, uint32_t k, uint32_t normalize,
-                                float scale, int32_t* __restrict__ idx, float* __restrict__ wts, uint32_t slot,
-                                bool write) {
-    constexpr uint32_t NV = kDecRouteMaxE / 64u;
+// NV = ceil(E / 64) chunks of experts per lane (1, 2 or 4), so no chunk
+// loop tests E. Only the writing wave needs every pick's probability; the
+// others need pick `slot` alone and stop there.
+template <uint32_t NV>
+RFXQ_DEV int32_t moe_route_wave_n(const RouteLogits& rl, uint32_t t, uint32_t E, uint32_t k, uint32_t normalize,
+                                  float scale, int32_t* __restrict__ idx, float* __restrict__ wts, uint32_t slot,
+                                  bool write) {
     const uint32_t lane = threadIdx.x & 63u;
     float v[NV];
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) v[i] = rl.v[i];
-    // (chunks i with 64 i >= E hold no expert: skipped, a uniform branch)
     float mx = -INFINITY;
 #pragma unroll
-    for (uint32_t i = 0; i < NV; i++)
-        if (64u * i < E) mx = lane + 64u * i < E ? fmaxf(mx, v[i]) : mx;
+    for (uint32_t i = 0; i < NV; i++) mx = lane + 64u * i < E ? fmaxf(mx, v[i]) : mx;
     mx = wave_max(mx);
     float sum = 0.0f;
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
-        const bool in = lane + 64u * i < E;
-        v[i] = 64u * i < E && in ? expf(v[i] - mx) : 0.0f;
+        v[i] = lane + 64u * i < E ? expf(v[i] - mx) : 0.0f;
         sum += v[i];  // (absent experts add 0)
     }
     sum = group_sum<64>(sum);
@@ -225,48 +225,55 @@ RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, u
     int32_t rk[NV];
 #pragma unroll
     for (uint32_t i = 0; i < NV; i++) {
-        const uint32_t e = lane + 64u * i;
-        if (64u * i < E) v[i] = v[i] / sum;
-        rk[i] = order_key(e < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f);
+        v[i] = v[i] / sum;
+        rk[i] = order_key(lane + 64u * i < E ? (v[i] == v[i] ? v[i] : -0.5f) : -2.0f);
     }
     float my_p = 0.0f, top_sum = 0.0f;
     int32_t my_e = 0, pick = 0;
-    for (uint32_t r = 0; r < k; r++) {
+    const uint32_t rounds = write ? k : slot + 1u;
+    for (uint32_t r = 0; r < rounds; r++) {
         int32_t m = rk[0];
 #pragma unroll
-        for (uint32_t i = 1; i < NV; i++)
-            if (64u * i < E) m = max(m, rk[i]);  // (E is uniform: chunks past it are skipped)
+        for (uint32_t i = 1; i < NV; i++) m = max(m, rk[i]);
         m = wave_max_i32(m);
         // the lowest expert holding the maximum
         uint32_t be = 0xFFFFFFFFu;
 #pragma unroll
         for (uint32_t i = 0; i < NV; i++) {
-            if (64u * i < E) {
-                const uint64_t bits = __ballot(rk[i] == m);
-                if (be == 0xFFFFFFFFu && bits) be = 64u * i + (uint32_t)__builtin_ctzll(bits);
-            }
+            const uint64_t bits = __ballot(rk[i] == m);
+            if (be == 0xFFFFFFFFu && bits) be = 64u * i + (uint32_t)__builtin_ctzll(bits);
         }
         be = __builtin_amdgcn_readfirstlane(be);
-        // the winner's probability, read by its lane and broadcast
-        const uint32_t owner = be & 63u, oi = be >> 6;
-        float pv = v[0];
-#pragma unroll
-        for (uint32_t i = 1; i < NV; i++) pv = i == oi ? v[i] : pv;
-        pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), owner));
 #pragma unroll
         for (uint32_t i = 0; i < NV; i++) rk[i] = lane + 64u * i == be ? INT32_MIN : rk[i];  // taken
-        top_sum += pv;  // in selection order
-        if (lane == r) {
-            my_p = pv;
-            my_e = (int32_t)be;
-        }
         if (r == slot) pick = (int32_t)be;
+        if (write) {
+            // the winner's probability, read by its lane and broadcast
+            const uint32_t owner = be & 63u, oi = be >> 6;
+            float pv = v[0];
+#pragma unroll
+            for (uint32_t i = 1; i < NV; i++) pv = i == oi ? v[i] : pv;
+            pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), owner));
+            top_sum += pv;  // in selection order
+            if (lane == r) {
+                my_p = pv;
+                my_e = (int32_t)be;
+            }
+        }
     }
     if (write && lane < k) {
         idx[(uint64_t)t * k + lane] = my_e;
         wts[(uint64_t)t * k + lane] = (normalize ? my_p / top_sum : my_p) * scale;
     }
     return pick;
+}
+
+RFXQ_DEV int32_t moe_route_wave(const RouteLogits& rl, uint32_t t, uint32_t E, uint32_t k, uint32_t normalize,
+                                float scale, int32_t* __restrict__ idx, float* __restrict__ wts, uint32_t slot,
+                                bool write) {
+    if (E <= 64u) return moe_route_wave_n<1>(rl, t, E, k, normalize, scale, idx, wts, slot, write);
+    if (E <= 128u) return moe_route_wave_n<2>(rl, t, E, k, normalize, scale, idx, wts, slot, write);
+    return moe_route_wave_n<4>(rl, t, E, k, normalize, scale, idx, wts, slot, write);
 }
 
 template <typename T, int LPR>
