@@ -295,10 +295,11 @@ RFXQ_DEV void moe_dec_gu(const MoeDecArgs& a, uint8_t* lds) {
     __builtin_amdgcn_sched_barrier(0);  // (keeps the x loads after these)
     XRegs xr;
     moe_x_load(xt, a.hidden, xr, tid);
-    // every wave routes the token itself (no barrier); one workgroup per
-    // token writes the routing for the down launch
-    if (a.logits)
-        e_raw = moe_route_wave(lg, t, a.E, a.k, a.normalize, a.scale, a.idx, a.wts, j, wave == 0u && j == 0u && b == 0u);
+    // every wave routes the token itself (no barrier) as far as its slot;
+    // one wave per token routes it again in full, while its weights are in
+    // flight, and writes the routing for the down launch
+    const bool writer = a.logits && wave == 0u && j == 0u && b == 0u;
+    if (a.logits) e_raw = moe_route_wave(lg, t, a.E, a.k, a.normalize, a.scale, a.idx, a.wts, j, false);
     int32_t e = e_raw;
     e = __builtin_amdgcn_readfirstlane(min((uint32_t)e, a.E - 1u));
     // waves 0-1: gate rows, waves 2-3: up rows (a wave-uniform weight tensor);
@@ -312,6 +313,7 @@ RFXQ_DEV void moe_dec_gu(const MoeDecArgs& a, uint8_t* lds) {
     const rsrc_t rs = moe_rsrc(p ? a.wu : a.wg, (uint64_t)a.E * a.eb_gu, &sh);
     MoeRowDot<T, LPR> rd(rs, sh + (uint32_t)(e * a.eb_gu) + r * row_bytes, a.hidden, li);
     rd.fetch0();
+    if (writer) (void)moe_route_wave(lg, t, a.E, a.k, a.normalize, a.scale, a.idx, a.wts, j, true);
     uint32_t* lds_x = reinterpret_cast<uint32_t*>(lds + a.lds_x1);
     float* lds_s = reinterpret_cast<float*>(lds_x + a.hidden / 2u);
     float* lds_p = lds_s + a.hidden / 16u;  // 4 floats: the stage's wave maxima
