@@ -348,11 +348,27 @@ RFXQ_DEV void moe_dec_down(const MoeDecArgs& a, uint8_t* lds) {
     int32_t* le = reinterpret_cast<int32_t*>(lds);
     float* lw = reinterpret_cast<float*>(le + 64);
     uint32_t* ord = reinterpret_cast<uint32_t*>(lw + 64);
+    // lane group gi = (row, slot) item: row rl = item / k, slot j = item % k;
+    // each lane loads its slot's expert itself, so its first weights are
+    // requested as soon as that arrives (before the LDS tables, the combine
+    // order and the staging of x)
+    constexpr uint32_t RPW = 64u / LPR;
+    const uint32_t gi = lane / LPR, li = lane % LPR;
+    const uint32_t item = wave * RPW + gi, rl = item / a.k, j = item % a.k;
     const rsrc_t ri = make_rsrc(a.idx + (uint64_t)t * a.k, a.k * 4u), rw = make_rsrc(a.wts + (uint64_t)t * a.k, a.k * 4u);
+    const uint32_t e_slot = bld4(ri, 4u * min(j, a.k - 1u));
     const uint32_t my_e = bld4(ri, 4u * (tid & 63u)), my_w = bld4(rw, 4u * (tid & 63u));
     __builtin_amdgcn_sched_barrier(0);  // (keeps the row's loads after these)
     XRegs xr;
     moe_x_load(st, K2, xr, tid);
+    const uint32_t r = min(b * a.nr2 + rl, a.hidden - 1u);
+    const uint32_t row_bytes = a.ffn / T::QK * T::BB;
+    const uint32_t upp = a.ffn / (T::QK / T::UPB);  // units per slot in the staged row
+    uint32_t sh;
+    const rsrc_t rs = moe_rsrc(a.wd, (uint64_t)a.E * a.eb_dn, &sh);
+    const uint32_t e = min(e_slot, a.E - 1u);
+    MoeRowDot<T, LPR> rd(rs, sh + (uint32_t)(e * a.eb_dn) + r * row_bytes, a.ffn, li);
+    rd.fetch0();  // (items past the rows fetch a valid row; their dots are not used)
     if (tid < a.k) {
         le[tid] = (int32_t)min(my_e, a.E - 1u);
         lw[tid] = as_f32(my_w);
@@ -364,19 +380,6 @@ RFXQ_DEV void moe_dec_down(const MoeDecArgs& a, uint8_t* lds) {
         for (uint32_t i = 0; i < a.k; i++) rank += (le[i] < me || (le[i] == me && i < tid)) ? 1u : 0u;
         ord[rank] = tid;
     }
-    // lane group gi = (row, slot) item: row rl = item / k, slot j = item % k;
-    // the first weights are requested before x is staged
-    constexpr uint32_t RPW = 64u / LPR;
-    const uint32_t gi = lane / LPR, li = lane % LPR;
-    const uint32_t item = wave * RPW + gi, rl = item / a.k, j = item % a.k;
-    const uint32_t r = min(b * a.nr2 + rl, a.hidden - 1u);
-    const uint32_t row_bytes = a.ffn / T::QK * T::BB;
-    const uint32_t upp = a.ffn / (T::QK / T::UPB);  // units per slot in the staged row
-    uint32_t sh;
-    const rsrc_t rs = moe_rsrc(a.wd, (uint64_t)a.E * a.eb_dn, &sh);
-    const uint32_t e = (uint32_t)le[min(j, a.k - 1u)];
-    MoeRowDot<T, LPR> rd(rs, sh + (uint32_t)(e * a.eb_dn) + r * row_bytes, a.ffn, li);
-    rd.fetch0();  // (items past the rows fetch a valid row; their dots are not used)
     uint32_t* lds_x = reinterpret_cast<uint32_t*>(lds + a.lds_x2);
     float* lds_s = reinterpret_cast<float*>(lds_x + K2 / 2u);
     float* lds_p = lds_s + K2 / 16u;
