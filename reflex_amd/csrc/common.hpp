@@ -158,6 +158,21 @@ RFXQ_DEV float group_sum(float v) {
     return v;
 }
 
+// wave-wide maximum (every lane ends with it; order-independent): DPP
+// steps leave each 16-lane row's maximum in its lanes, then the four rows'
+// are read out (no LDS round trip, as a swizzle across rows would take)
+RFXQ_DEV float wave_max(float v) {
+    v = fmaxf(v, RFXQ_DPP(v, 0xB1));
+    v = fmaxf(v, RFXQ_DPP(v, 0x4E));
+    v = fmaxf(v, RFXQ_DPP(v, 0x141));
+    v = fmaxf(v, RFXQ_DPP(v, 0x140));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
+
 // Index of element e inside a run stored pair-permuted: within each group of
 // four, elements (0,1,2,3) live at (0,2,1,3), so one dword holds the f16 pair
 // (e, e+2) that a masked packed byte word produces.

@@ -115,8 +115,7 @@ RFXQ_DEV float gemv_stage_x(const float* __restrict__ x, uint32_t k, uint32_t hi
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xr.v[i].x), fabsf(xr.v[i].y)), fmaxf(fabsf(xr.v[i].z), fabsf(xr.v[i].w))));
         }
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    amax = wave_max(amax);
     if ((tid & 63u) == 0u) lds_st32(lds_addr(lds_p) + 4u * (tid >> 6), __builtin_bit_cast(uint32_t, amax));
     lds_barrier();
     {

@@ -110,8 +110,9 @@ constexpr uint32_t kPlanMaxPairs = 16384;  // sort keys in LDS
 
 // route_top_k_with_norm (src/moe.rs:47-98), one workgroup of G threads per
 // token: softmax of the logits (max subtracted; the sum by wave 0 as lane
-// sums over its experts l, l + 64, ... then a butterfly over the lanes, so it
-// can differ from a sequential sum in the last bit), the k best by
+// sums over its experts l, l + 64, ... then group_sum's lane reduction, so it
+// can differ from a sequential sum in the last bit; the decode router sums
+// in the same order, so both give the same probabilities), the k best by
 // probability descending then expert index ascending, renormalised by their
 // sum (in selection order) when `normalize`; weights multiplied by `scale`.
 // Selection by rank: the ranking values go to LDS and every expert counts
@@ -142,8 +143,7 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
         L.pv[e] = v;
         mx = fmaxf(mx, v);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    mx = wave_max(mx);
     if (lane == 0u) L.red[wave] = mx;
     for (uint32_t e = tid; e < E; e += G) L.rank[e] = 0u;
     __syncthreads();
@@ -155,8 +155,7 @@ __device__ __forceinline__ void moe_route_token(const float* __restrict__ logits
     if (wave == 0u) {
         float sum = 0.0f;
         for (uint32_t e = lane; e < E; e += 64u) sum += L.pv[e];
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+        sum = group_sum<64>(sum);
         if (lane == 0u) L.red[0] = sum;
     }
     __syncthreads();

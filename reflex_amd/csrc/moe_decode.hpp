@@ -140,21 +140,6 @@ struct MoeRowDot {
     }
 };
 
-// wave-wide maximum (every lane ends with it; order-independent): DPP
-// steps leave each 16-lane row's maximum in its lanes, then the four rows'
-// are read out (no LDS round trip, as a swizzle across rows would take)
-RFXQ_DEV float wave_max(float v) {
-    v = fmaxf(v, RFXQ_DPP(v, 0xB1));
-    v = fmaxf(v, RFXQ_DPP(v, 0x4E));
-    v = fmaxf(v, RFXQ_DPP(v, 0x141));
-    v = fmaxf(v, RFXQ_DPP(v, 0x140));
-    const int b = __builtin_bit_cast(int, v);
-    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
-                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
-                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
-                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
-}
-
 // the same for 32-bit signed integers (the DPP moves fold into v_max_i32)
 RFXQ_DEV int32_t wave_max_i32(int32_t v) {
     v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));

@@ -90,8 +90,7 @@ RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t*
 // and, optionally, the source values themselves to yout (f32 [rows][k]).
 // row exponent of the f16 layout from the row's max |x|
 RFXQ_DEV int act_f16_exp(float mx) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     return (mx > 0.0f && mx <= 3.4028235e38f) ? min(max(ilogbf(mx) - 8, -120), 120) : 0;
 }
 
@@ -187,8 +186,7 @@ RFXQ_DEV void act_f16_row_wg(const Src& src, uint32_t r, uint32_t k, uint16_t* _
     } else {
         for (uint32_t c = 4u * tid; c < k; c += 1024u) mx = fmaxf(mx, absmax4(src.load(r, c)));
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     if (lane == 0u) wmax[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
