@@ -48,17 +48,20 @@ RFXQ_DEV void quant_q8_1_rows(const Src& src, uint32_t rows, uint32_t k, int8_t*
         const float4 v = src.load(row, 32u * blk + 4u * part);
         if (yout && valid) *reinterpret_cast<float4*>(yout + (uint64_t)row * k + 32u * blk + 4u * part) = v;
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        // the block's maximum in all 8 lanes (DPP within the lane group)
+        amax = fmaxf(amax, RFXQ_DPP(amax, 0xB1));
+        amax = fmaxf(amax, RFXQ_DPP(amax, 0x4E));
+        amax = fmaxf(amax, RFXQ_DPP(amax, 0x141));
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id);
         const int q2 = (int)roundf(v.z * id), q3 = (int)roundf(v.w * id);
         float sum = ((v.x + v.y) + v.z) + v.w;
-        sum += __shfl_xor(sum, 4, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 1, 64);
+        // lane distance 4, 2, 1 for the group's first lane (the one that
+        // stores it): row_shl:4, then quad_perm swaps of 2 and 1
+        sum += RFXQ_DPP(sum, 0x104);
+        sum += RFXQ_DPP(sum, 0x4E);
+        sum += RFXQ_DPP(sum, 0xB1);
         if (valid) {
             const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
                                     ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
@@ -107,9 +110,10 @@ RFXQ_DEV void act_f16_chunk(float4 v, uint32_t lane, uint32_t c, uint64_t ro, ui
     hv.y = h2_bits(h2_t{h1, h3});
     *reinterpret_cast<uint2*>(xh + ro + c) = hv;
     float s = (((float)h0 + (float)h1) + (float)h2) + (float)h3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    // lane distance 1, 2 (quad_perm swaps), then the other quad's sum by
+    // row_half_mirror: the same additions as a butterfly for the group's
+    // first lane, which stores it (every lane of a quad holds the same sum)
+    s = group_sum<8>(s);
     if ((lane & 7u) == 0u) {
         const uint32_t blk = c / 32u;
         const half_t hi = (half_t)s;
