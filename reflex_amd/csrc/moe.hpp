@@ -270,12 +270,18 @@ struct MoePlanArgs {
 // LDS). Integer adds, so the grouping does not matter.
 __device__ __forceinline__ uint32_t plan_scan(uint32_t v, uint32_t* tot) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    // inclusive within each 16-lane row (DPP row_shr 1, 2, 4, 8: lanes
+    // shifted in from outside the row add 0), then the earlier rows' totals
     uint32_t x = v;
-#pragma unroll
-    for (uint32_t o = 1; o < 64u; o <<= 1) {
-        const uint32_t y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, false);
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+    const uint32_t row = lane >> 4;
+    x += (row >= 1u ? r0 : 0u) + (row >= 2u ? r1 : 0u) + (row >= 3u ? r2 : 0u);
     if (lane == 63u) tot[wave] = x;
     __syncthreads();
     uint32_t pre = 0;
