@@ -143,18 +143,26 @@ RFXQ_DEV uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t shift_bytes) {
 
 // Sum over groups of WIDTH consecutive lanes (a power of two <= 64). Within a
 // 16-lane row the sum uses DPP (every lane of the group ends with it); across
-// rows a swizzle (32) and readlanes (64, result valid in every lane).
+// rows the gfx950 row swaps: v_permlane16_swap gives every lane of rows 2i,
+// 2i + 1 the pair row0 + row1 of its half (32), v_permlane32_swap every lane
+// the two halves' sum, lower half first (64). (Every lane of a row holds the
+// same value by then, so the lane alignment of the swaps does not matter.)
 template <int WIDTH>
 RFXQ_DEV float group_sum(float v) {
     if (WIDTH >= 2) v += RFXQ_DPP(v, 0xB1);
     if (WIDTH >= 4) v += RFXQ_DPP(v, 0x4E);
     if (WIDTH >= 8) v += RFXQ_DPP(v, 0x141);
     if (WIDTH >= 16) v += RFXQ_DPP(v, 0x140);
-    if (WIDTH >= 32)  // xor 16 within each 32-lane half: and_mask 0x1f, xor_mask 0x10
-        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-    if (WIDTH >= 64)
-        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    if (WIDTH >= 32) {
+        const uint32_t b = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
+    if (WIDTH >= 64) {
+        const uint32_t b = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+        v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
     return v;
 }
 
