@@ -140,14 +140,18 @@ struct MoeRowDot {
     }
 };
 
-// the same for 32-bit signed integers (the DPP moves fold into v_max_i32)
+// the wave's maximum of 32-bit signed integers in every lane: DPP steps
+// (folded into v_max_i32) within each row, then the row swaps across rows
+// (all in vector registers: no round trip through scalar ones)
 RFXQ_DEV int32_t wave_max_i32(int32_t v) {
     v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
     v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
     v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
     v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
-    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+    const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = max((int32_t)a[0], (int32_t)a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return max((int32_t)b[0], (int32_t)b[1]);
 }
 
 // float -> int32 of the same order (signed compare): negative floats have
