@@ -92,7 +92,13 @@ struct MoeDecArgs {
     uint32_t nb1, nr1;     // gate/up: row blocks per slot, rows per block (of each projection)
     uint32_t nb2, nr2;     // down: row blocks per token, rows per block
     uint32_t lds_x1, lds_x2;  // byte offsets of the staged x in LDS
+    // host routing of up to kDecInlinePairs pairs carried in the kernel
+    // arguments (n_inline != 0: read instead of idx / wts; no upload)
+    uint32_t n_inline;
+    int32_t h_idx[32];
+    float h_w[32];
 };
+constexpr uint32_t kDecInlinePairs = 32;
 
 // buffer resource over a stacked tensor whose data may start 2 bytes past a
 // dword: base rounded down, the remainder (*sh) added to every offset
@@ -280,7 +286,7 @@ RFXQ_DEV void moe_dec_gu(const MoeDecArgs& a, uint8_t* lds) {
     RouteLogits lg;
     int32_t e_raw = 0;
     if (a.logits) moe_route_load(a.logits, t, a.E, lg);
-    else e_raw = a.idx[(uint64_t)t * a.k + j];
+    else e_raw = a.n_inline ? a.h_idx[t * a.k + j] : a.idx[(uint64_t)t * a.k + j];
     __builtin_amdgcn_sched_barrier(0);  // (keeps the x loads after these)
     XRegs xr;
     moe_x_load(xt, a.hidden, xr, tid);
@@ -344,9 +350,21 @@ RFXQ_DEV void moe_dec_down(const MoeDecArgs& a, uint8_t* lds) {
     constexpr uint32_t RPW = 64u / LPR;
     const uint32_t gi = lane / LPR, li = lane % LPR;
     const uint32_t item = wave * RPW + gi, rl = item / a.k, j = item % a.k;
-    const rsrc_t ri = make_rsrc(a.idx + (uint64_t)t * a.k, a.k * 4u), rw = make_rsrc(a.wts + (uint64_t)t * a.k, a.k * 4u);
-    const uint32_t e_slot = bld4(ri, 4u * min(j, a.k - 1u));
-    const uint32_t my_e = bld4(ri, 4u * (tid & 63u)), my_w = bld4(rw, 4u * (tid & 63u));
+    uint32_t e_slot, my_e = 0, my_w = 0;
+    if (a.n_inline) {  // the host's routing in the kernel arguments
+        const int32_t* hi = &a.h_idx[0] + t * a.k;
+        const float* hw = &a.h_w[0] + t * a.k;
+        e_slot = (uint32_t)hi[min(j, a.k - 1u)];
+        if (tid < a.k) {
+            my_e = (uint32_t)hi[tid];
+            my_w = __builtin_bit_cast(uint32_t, hw[tid]);
+        }
+    } else {
+        const rsrc_t ri = make_rsrc(a.idx + (uint64_t)t * a.k, a.k * 4u), rw = make_rsrc(a.wts + (uint64_t)t * a.k, a.k * 4u);
+        e_slot = bld4(ri, 4u * min(j, a.k - 1u));
+        my_e = bld4(ri, 4u * (tid & 63u));
+        my_w = bld4(rw, 4u * (tid & 63u));
+    }
     __builtin_amdgcn_sched_barrier(0);  // (keeps the row's loads after these)
     XRegs xr;
     moe_x_load(st, K2, xr, tid);

@@ -2815,8 +2815,12 @@ struct MoeDecArgs {
     uint32_t nb1, nr1;
     uint32_t nb2, nr2;
     uint32_t lds_x1, lds_x2;
+    uint32_t n_inline;
+    int32_t h_idx[32];
+    float h_w[32];
 };
-constexpr uint32_t kDecRouteMaxE = 256;  // moe_decode.hpp
+constexpr uint32_t kDecRouteMaxE = 256;     // moe_decode.hpp
+constexpr uint32_t kDecInlinePairs = 32;    // moe_decode.hpp
 
 // Lanes per row of the decode kernels: a power of two in [4, 32] dividing the
 // row's units, with at least `min_units` units per lane (fewer loads in
@@ -2842,7 +2846,7 @@ int dec_lpr(uint32_t units, uint32_t min_units, uint32_t max_lpr) {
 int moe_decode_launch(Ctx* c, const float* x, uint32_t rows, uint32_t hidden, const float* logits, int32_t* idx,
                       float* wts, uint32_t E, uint32_t k, int normalize, float scale, const rfxq_weight* gate,
                       const rfxq_weight* up, const rfxq_weight* down, float* s, float* out, hipStream_t stream,
-                      bool* done) {
+                      bool* done, const uint32_t* host_idx = nullptr, const float* host_w = nullptr) {
     *done = false;
     const uint32_t ffn = gate->out_features;
     const int tg = type_index(gate->ggml_type), td = type_index(down->ggml_type);
@@ -2882,6 +2886,13 @@ int moe_decode_launch(Ctx* c, const float* x, uint32_t rows, uint32_t hidden, co
     a.nb2 = (hidden + a.nr2 - 1u) / a.nr2;
     a.lds_x1 = 0u;
     a.lds_x2 = 768u;  // experts, weights, combine order
+    if (host_idx) {  // the host's routing in the kernel arguments (the caller checked the count)
+        a.n_inline = rows * k;
+        for (uint32_t q = 0; q < rows * k; q++) {
+            a.h_idx[q] = (int32_t)host_idx[q];
+            a.h_w[q] = host_w[q];
+        }
+    }
     const uint32_t K2 = k * ffn;
     const uint32_t lds1 = a.lds_x1 + hidden * 2u + hidden / 4u + 16u + 2u * a.nr1 * 4u;
     const uint32_t lds2 = a.lds_x2 + K2 * 2u + K2 / 4u + 16u + a.nr2 * k * 4u;
@@ -3031,6 +3042,15 @@ int moe_grouped_device(const float* x, uint32_t rows, uint32_t hidden, const flo
         pa.vd = id.d;
     }
 
+    if (host_idx && gemv_form && P <= kDecInlinePairs) {
+        // few pairs routed on the host: the two decode launches take them in
+        // their kernel arguments (no table upload) where the shapes allow
+        bool done = false;
+        if (int rc = moe_decode_launch(c, x, rows, hidden, nullptr, d_idx, d_w, expert_count, top_k, normalize,
+                                       weight_scale, gate, up, down, gout, out, stream, &done, host_idx, host_w))
+            return rc;
+        if (done) return ok();
+    }
     if (host_idx) {  // routed on the host
         std::vector<uint8_t> host(o_w - o_idx + (uint64_t)P * 4u, 0);
         std::memcpy(host.data(), host_idx, (uint64_t)P * 4u);
