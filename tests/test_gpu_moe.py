@@ -242,12 +242,12 @@ def test_moe_q6k_down_projection(rq, orc, tokens):
         assert e < TOL
 
 
-@pytest.mark.parametrize("tokens,k", [(1, 8), (4, 8), (1, 1), (2, 1), (5, 8)])
+@pytest.mark.parametrize("tokens,k", [(1, 8), (4, 8), (1, 1), (2, 1), (5, 8), (2, 16), (3, 16)])
 def test_moe_ffn_grouped_device_decode(rq, orc, tokens, k):
-    """Up to 4 tokens run every routed pair as GEMVs whose descriptors the
-    device plan writes (as the host-routed path does with host-built ones;
-    1-2 pairs exercise the table path of launches with few descriptors);
-    5 tokens take the grouped MMQ path."""
+    """Up to 4 tokens take the two decode launches (device routing in the
+    first; host routing of up to 32 pairs in the kernel arguments, 48 pairs
+    uploaded); 5 tokens take the grouped MMQ path. Device- and host-routed
+    calls agree and meet the bound."""
     y_d, y_h, ref, _, _, _ = _moe_device_case(rq, orc, tokens, 128, 2048, 768, k, 900 + tokens + k)
     assert orc.rel_err_row_l2(y_d, y_h.astype(np.float64)) < 1e-5
     assert orc.rel_err_row_l2(y_d, ref) < TOL
