@@ -175,12 +175,12 @@ constexpr uint32_t kDecRouteMaxE = 256;  // experts the one-wave router takes (4
 // descending then index ascending (a NaN p ranks below every number),
 // renormalised by their sum in selection order when `normalize`, times
 // `scale`. Lane l holds experts l + 64 i. Each of the k rounds takes the
-// wave-wide maximum of the ranking values (p; NaN -0.5, absent experts -2,
-// taken ones -3) and, among the experts holding it, the lowest index: the
-// first set bit of the ballots of chunks i = 0, 1, ... (p is never -0.0, so
-// float equality is the reference's tie). Deterministic, so every wave of a
-// token finds the same routing. Returns slot `slot`'s expert; lanes < k write
-// idx / wts when `write`.
+// wave-wide maximum of the ranking keys (the integer order of p; NaN p as
+// -0.5, absent experts as -2, taken ones INT32_MIN) and, among the experts
+// holding it, the lowest index: the first set bit of the ballots of chunks
+// i = 0, 1, ... (p is never -0.0, so equal keys are the reference's ties).
+// Deterministic, so every wave of a token finds the same routing. Returns
+// slot `slot`'s expert; lanes < k write idx / wts when `write`.
 struct RouteLogits {
     float v[kDecRouteMaxE / 64u];
 };
