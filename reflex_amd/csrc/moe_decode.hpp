@@ -434,3 +434,27 @@ RFXQ_MOE_DEC(q8_0, Q80, 4)
 RFXQ_MOE_DEC(q8_0, Q80, 8)
 RFXQ_MOE_DEC(q8_0, Q80, 16)
 RFXQ_MOE_DEC(q8_0, Q80, 32)
+
+// rfxq_moe_route's work with one wave per token (at most kDecRouteMaxE
+// experts, k <= 64; x rows of up to kActRegK values): the token's logits and
+// its row of x are requested together, the wave routes the token
+// (moe_route_wave, every pick and weight written: the same probabilities,
+// picks and weights as rfxq_moe_route) and, with xh, writes the row's f16
+// layout (act_f16_row's arithmetic). No barrier: waves past the last token
+// return at once.
+extern "C" __global__ __launch_bounds__(256) void rfxq_moe_route_w(const float* __restrict__ logits, uint32_t tokens,
+                                                                  uint32_t E, uint32_t k, uint32_t normalize,
+                                                                  float scale, int32_t* __restrict__ idx,
+                                                                  float* __restrict__ wts, const float* __restrict__ x,
+                                                                  uint32_t hidden, uint16_t* __restrict__ xh,
+                                                                  uint16_t* __restrict__ xsx, float* __restrict__ xrs) {
+    const uint32_t t = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
+    if (t >= tokens) return;
+    RouteLogits lg;
+    moe_route_load(logits, t, E, lg);
+    float4 v[kActRowRegs];
+    const QuantSrcPlain src{x, hidden, nullptr};
+    if (xh) act_f16_row_load(src, t, hidden, v);
+    (void)moe_route_wave(lg, t, E, k, normalize, scale, idx, wts, 0u, true);
+    if (xh) act_f16_row_put(v, t, hidden, xh, xsx, xrs, nullptr);
+}

@@ -128,36 +128,52 @@ RFXQ_DEV void act_f16_chunk(float4 v, uint32_t lane, uint32_t c, uint64_t ro, ui
 // are read twice (the maximum, then the layout).
 constexpr uint32_t kActRegK = 4096;
 
+// act_f16_row's register form (k <= kActRegK) in two steps, so a caller can
+// put the row's loads in flight beside other loads
+constexpr uint32_t kActRowRegs = kActRegK / 256u;
 template <class Src>
-RFXQ_DEV void act_f16_row(const Src& src, uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
-                          uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
+RFXQ_DEV void act_f16_row_load(const Src& src, uint32_t r, uint32_t k, float4 (&v)[kActRowRegs]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t nsb = k / 256u;
+#pragma unroll
+    for (uint32_t i = 0; i < kActRowRegs; i++)
+        if (i < nsb) v[i] = src.load(r, 4u * lane + 256u * i);
+}
+
+RFXQ_DEV void act_f16_row_put(const float4 (&v)[kActRowRegs], uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
+                              uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t ro = (uint64_t)r * k;
     const uint32_t nsb = k / 256u;
-    int e;
+    float mx = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kActRowRegs; i++)
+        if (i < nsb) mx = fmaxf(mx, absmax4(v[i]));
+    const int e = act_f16_exp(mx);
+    const float scale = ldexpf(1.0f, -e);
+#pragma unroll
+    for (uint32_t i = 0; i < kActRowRegs; i++)
+        if (i < nsb) act_f16_chunk(v[i], lane, 4u * lane + 256u * i, ro, r, nsb, scale, xh, xsx, yout);
+    if (lane == 0u) xrs[r] = ldexpf(1.0f, e);
+}
+
+template <class Src>
+RFXQ_DEV void act_f16_row(const Src& src, uint32_t r, uint32_t k, uint16_t* __restrict__ xh,
+                          uint16_t* __restrict__ xsx, float* __restrict__ xrs, float* __restrict__ yout) {
     if (k <= kActRegK) {
-        constexpr uint32_t NC = kActRegK / 256u;
-        float4 v[NC];
-        float mx = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < NC; i++)
-            if (i < nsb) v[i] = src.load(r, 4u * lane + 256u * i);
-#pragma unroll
-        for (uint32_t i = 0; i < NC; i++)
-            if (i < nsb) mx = fmaxf(mx, absmax4(v[i]));
-        e = act_f16_exp(mx);
-        const float scale = ldexpf(1.0f, -e);
-#pragma unroll
-        for (uint32_t i = 0; i < NC; i++)
-            if (i < nsb) act_f16_chunk(v[i], lane, 4u * lane + 256u * i, ro, r, nsb, scale, xh, xsx, yout);
-    } else {
-        float mx = 0.0f;
-        for (uint32_t c = 4u * lane; c < k; c += 256u) mx = fmaxf(mx, absmax4(src.load(r, c)));
-        e = act_f16_exp(mx);
-        const float scale = ldexpf(1.0f, -e);
-        for (uint32_t c = 4u * lane; c < k; c += 256u)
-            act_f16_chunk(src.load(r, c), lane, c, ro, r, nsb, scale, xh, xsx, yout);
+        float4 v[kActRowRegs];
+        act_f16_row_load(src, r, k, v);
+        act_f16_row_put(v, r, k, xh, xsx, xrs, yout);
+        return;
     }
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t ro = (uint64_t)r * k;
+    const uint32_t nsb = k / 256u;
+    float mx = 0.0f;
+    for (uint32_t c = 4u * lane; c < k; c += 256u) mx = fmaxf(mx, absmax4(src.load(r, c)));
+    const int e = act_f16_exp(mx);
+    const float scale = ldexpf(1.0f, -e);
+    for (uint32_t c = 4u * lane; c < k; c += 256u) act_f16_chunk(src.load(r, c), lane, c, ro, r, nsb, scale, xh, xsx, yout);
     if (lane == 0u) xrs[r] = ldexpf(1.0f, e);
 }
 

@@ -138,6 +138,7 @@ constexpr uint32_t kMaxLds = 65536;    // dynamic LDS per GEMV workgroup (plus i
 constexpr uint32_t kMaxGemvK = 16384;  // x staged in LDS: k*2 + k/4 bytes <= 36 KB
 constexpr uint32_t kMoeGemvRows = 4;   // moe_ffn_grouped: up to this many tokens run as GEMVs
 constexpr uint32_t kRouteMaxE = 1024;     // rfxq_moe_route: experts per token
+constexpr uint32_t kDecRouteMaxE = 256;  // moe_decode.hpp: experts of the one-wave router
 constexpr uint32_t kPlanMaxPairs = 16384;  // rfxq_moe_plan: routed pairs sorted in LDS
 constexpr uint32_t kNormRowsPerWg = 4;  // rows per rfxq_rmsnorm_q8_1 workgroup (the kernel's constant)
 
@@ -154,7 +155,7 @@ struct Ctx {
     hipFunction_t act_f16 = nullptr, act_f16_multi = nullptr, act_f16_wg = nullptr, act_f16_multi_wg = nullptr;
     hipFunction_t deq[3][2] = {};
     hipFunction_t gather = nullptr, scatter = nullptr, silu = nullptr, combine = nullptr;
-    hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_plan = nullptr;
+    hipFunction_t rms_q = nullptr, silu_q = nullptr, moe_route = nullptr, moe_route_w = nullptr, moe_plan = nullptr;
     // MoE decode kernels: [Q4_K, Q6_K, Q8_0][4, 8, 16, 32 lanes per row]
     hipFunction_t moe_dec_gu[3][4] = {}, moe_dec_dn[3][4] = {};
     void* ws = nullptr;
@@ -244,6 +245,7 @@ int load_ctx(int device, Ctx** out) {
         {&c->rms_q, "rfxq_rmsnorm_q8_1"},
         {&c->silu_q, "rfxq_silu_and_mul_q8_1"},
         {&c->moe_route, "rfxq_moe_route"},
+        {&c->moe_route_w, "rfxq_moe_route_w"},
         {&c->moe_plan, "rfxq_moe_plan"},
         {&c->combine, "rfxq_moe_combine"},
     };
@@ -2478,6 +2480,9 @@ int moe_route_launch(Ctx* c, const float* logits, uint32_t tokens, uint32_t E, u
         uint16_t* xsx;
         float* xrs;
     } a = {logits, tokens, E, k, normalize ? 1u : 0u, scale, 0, idx, w, x, hidden, 0, xh, xsx, xrs};
+    // a wave per token (rfxq_moe_route_w) where its limits hold
+    if (E <= kDecRouteMaxE && k <= 64u && (!xh || hidden <= 4096u))
+        return launch(c->moe_route_w, (tokens + 3u) / 4u, 0, stream, &a, sizeof a, "rfxq_moe_route_w launch");
     return launch(c->moe_route, tokens, 0, stream, &a, sizeof a, "rfxq_moe_route launch");
 }
 
@@ -2819,7 +2824,6 @@ struct MoeDecArgs {
     int32_t h_idx[32];
     float h_w[32];
 };
-constexpr uint32_t kDecRouteMaxE = 256;     // moe_decode.hpp
 constexpr uint32_t kDecInlinePairs = 32;    // moe_decode.hpp
 
 // Lanes per row of the decode kernels: a power of two in [4, 32] dividing the
